@@ -1,0 +1,56 @@
+// ah_internal.h — host-side internals shared by runtime.cpp, executor.cpp and plans.cpp.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <functional>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/anneal_hip.h"
+
+namespace ah {
+
+int set_error(int code, const char *fmt, ...);
+int fail_hip(hipError_t e, const char *what);
+
+#define AH_HIP(expr)                                   \
+    do {                                               \
+        hipError_t e_ = (expr);                        \
+        if (e_ != hipSuccess) return ::ah::fail_hip(e_, #expr); \
+    } while (0)
+
+int64_t dtype_bytes(int32_t dtype);
+
+// Built-in template kernel, selected by a "tmpl:" source key. run() launches it on the stream with
+// the ExecItem's buffers (PARAM order) and the symbolic scalars.
+struct TemplateKernel {
+    std::string key;
+    std::unordered_map<std::string, std::string> params;
+    std::function<int(ah_device *, void *const *ptrs, int32_t n_ptrs, const int32_t *scalars, int32_t n_scalars)> run;
+};
+
+}  // namespace ah
+
+struct ah_kernel {
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;
+    ah::TemplateKernel *tmpl = nullptr;
+};
+
+struct ah_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    hipDeviceProp_t props{};
+    std::unordered_map<std::string, ah_kernel *> modules;
+    std::string arch;
+};
+
+struct ah_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace ah {
+int template_create(const std::string &source, TemplateKernel **out);
+}

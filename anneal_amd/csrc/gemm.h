@@ -1,0 +1,54 @@
+// gemm.h — descriptor for the MFMA contraction templates (host + device).
+//
+// One descriptor covers every GEMM-shaped REDUCE(ADD, MUL(..)) the reference scheduler emits for a
+// Linear layer (tensor/reduce.go:105-166 via tensor/nn/nn.go:154-162) and its backward
+// (tensor/gradient_ruleset.go:137-140, 207-233, 285-306):
+//   C[m,n] = epilogue( sum_k A(m,k) * B(n,k) )
+// A(m,k) is read from a row-major [M,K] array (ta=0, "K-contiguous") or a [K,M] array (ta=1);
+// B(n,k) from [N,K] (tb=0) or [K,N] (tb=1). Forward Linear is (0,0); dX = dY·W is (0,1);
+// dW = dYᵀ·X is (1,1).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ah {
+
+enum GemmDtype : int { GEMM_F32 = 0, GEMM_F16 = 1 };
+
+enum GemmEpi : int {
+    EPI_STORE = 0,      // C = scale*acc
+    EPI_BIAS = 1,       // C = acc + bias[n]            (f16: f16(f16(acc) + bias))
+    EPI_BIAS_RELU = 2,  // C = relu_tag(acc + bias[n])
+    EPI_MSE = 3,        // f16: P = f16(f16(acc)+bias); C = f16(P - aux); loss += (P-aux)^2; colsum += C
+    EPI_MASK = 4,       // C = relu_dead(aux) ? 0 : scale*acc; colsum += C (unrounded)
+    EPI_SGD = 5,        // g = scale*acc; gout = g (opt); W32 -= lr*g; W16 = f16(W32) (opt)
+};
+
+struct GemmDesc {
+    int dtype;        // GemmDtype of A and B
+    int epi;          // GemmEpi
+    int ta, tb;       // operand layouts (see above)
+    int M, N, K;
+    const void *A;
+    const void *B;
+    long lda, ldb;    // row strides of the stored arrays, in elements
+    void *C;          // output (type = dtype, except EPI_SGD which writes W32/W16)
+    long ldc;
+    const void *bias; // [N], type = dtype
+    const void *aux;  // [M,N] with ldaux, type = dtype (MSE targets / ReLU activations)
+    long ldaux;
+    float scale;
+    float *colsum;    // [N] f32 accumulator (atomic), optional
+    float *W32;       // EPI_SGD master weights [M,N] (row stride ldc)
+    void *W16;        // EPI_SGD f16 copy, optional
+    float lr;
+    float *gout;      // EPI_SGD gradient output [M,N] (row stride ldc), optional
+    float *lossacc;   // EPI_MSE scalar accumulator
+    int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
+};
+
+#ifdef __HIP_PLATFORM_AMD__
+hipError_t gemm_launch(const GemmDesc &d, hipStream_t s);
+#endif
+
+}  // namespace ah

@@ -1,0 +1,356 @@
+// gemm.hip — LDS-staged MFMA contraction templates for gfx950 (CDNA4).
+//
+// Block tile BM x BN, 256 threads = 4 wave64s in a 2x2 arrangement, each wave owning a
+// (BM/2) x (BN/2) sub-tile built from 32x32 MFMA blocks (f16: v_mfma_f32_32x32x16_f16,
+// f32: v_mfma_f32_32x32x2f32). K advances in stages of 8 16-byte chunks per row (64 halves or
+// 32 floats); two LDS stages are double-buffered so global loads of stage k+1 overlap the MFMAs of
+// stage k. LDS rows are 128 B with an XOR swizzle of the 16-byte chunk index by (row & 7), so
+// the ds_read_b128 fragment reads of 8 consecutive rows fall in distinct bank groups.
+//
+// Operands stored MN-contiguous ([K][M] / [K][N]) are transposed on the way into LDS: each
+// thread loads a VEC x VEC sub-block with VEC coalesced 16-byte loads and writes VEC K-contiguous
+// 16-byte rows, so the MFMA fragment reads are identical for every layout.
+//
+// Accumulation is f32 for both input types, matching the reference's f32 accumulator for f16
+// reduces (codegen/lower.go:667-716); products of f16 inputs are exact in f32.
+#include "ah_common.h"
+#include "gemm.h"
+
+namespace ah {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ int lds_off(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<half_t> {
+    static constexpr int VEC = 8;
+    typedef half_t vec_t __attribute__((ext_vector_type(8)));
+    __device__ static __forceinline__ void mma(const vec_t &a, const vec_t &b, floatx16 &c) {
+        c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mfma<float> {
+    static constexpr int VEC = 4;
+    typedef float vec_t __attribute__((ext_vector_type(4)));
+    // Lanes 0-31 hold k = 4c+q of chunk c, lanes 32-63 those of chunk c+1; the q-th MFMA
+    // contracts element q of both halves. A and B use the same assignment, so the sum covers
+    // each k exactly once.
+    __device__ static __forceinline__ void mma(const vec_t &a, const vec_t &b, floatx16 &c) {
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[1], b[1], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[2], b[2], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[3], b[3], c, 0, 0, 0);
+    }
+};
+
+// Guarded element-wise fill of one 16-byte chunk (slow path for unaligned / ragged shapes).
+template <typename T>
+__device__ __forceinline__ u32x4 load_chunk_guarded(const T *p, long step, int n_valid) {
+    constexpr int VEC = 16 / sizeof(T);
+    T tmp[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; e++) tmp[e] = (e < n_valid) ? p[e * step] : (T)0;
+    u32x4 r;
+    __builtin_memcpy(&r, tmp, 16);
+    return r;
+}
+
+// Operand tile R rows x (8 chunks) from a K-contiguous array [rows][K].
+template <typename T, int R>
+struct LoadK {
+    static constexpr int VEC = 16 / sizeof(T);
+    static constexpr int PER = R * 8 / kThreads;
+    u32x4 v[PER];
+    __device__ __forceinline__ void load(const T *p, long ld, int r0, int rmax, int k0, int K, bool vec_ok) {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            int id = tid + kThreads * i;
+            int r = id >> 3, c = id & 7;
+            int gr = r0 + r, gk = k0 + c * VEC;
+            if (gr < rmax && gk < K) {
+                const T *src = p + (long)gr * ld + gk;
+                if (vec_ok) v[i] = *(const u32x4 *)src;
+                else v[i] = load_chunk_guarded<T>(src, 1, K - gk);
+            } else {
+                v[i] = (u32x4){0, 0, 0, 0};
+            }
+        }
+    }
+    __device__ __forceinline__ void store(char *lds) const {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            int id = tid + kThreads * i;
+            *(u32x4 *)(lds + lds_off(id >> 3, id & 7)) = v[i];
+        }
+    }
+};
+
+// Operand tile from an MN-contiguous array [K][rows]: VEC x VEC sub-blocks, transposed in registers.
+template <typename T, int R>
+struct LoadMN {
+    static constexpr int VEC = 16 / sizeof(T);
+    static constexpr int RB = R / VEC;                 // sub-blocks along the row axis
+    static constexpr int NSUB = 8 * RB;
+    static constexpr int PER = (NSUB + kThreads - 1) / kThreads;
+    u32x4 v[PER][VEC];
+    __device__ __forceinline__ void load(const T *p, long ld, int r0, int rmax, int k0, int K, bool vec_ok) {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            int id = tid + kThreads * i;
+            int kb = id / RB, rb = id % RB;
+            int gr = r0 + rb * VEC;
+#pragma unroll
+            for (int kk = 0; kk < VEC; kk++) {
+                int gk = k0 + kb * VEC + kk;
+                if (id < NSUB && gk < K && gr < rmax) {
+                    const T *src = p + (long)gk * ld + gr;
+                    if (vec_ok && gr + VEC <= rmax) v[i][kk] = *(const u32x4 *)src;
+                    else v[i][kk] = load_chunk_guarded<T>(src, 1, rmax - gr);
+                } else {
+                    v[i][kk] = (u32x4){0, 0, 0, 0};
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void store(char *lds) const {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            int id = tid + kThreads * i;
+            if (id >= NSUB) continue;
+            int kb = id / RB, rb = id % RB;
+            T in[VEC][VEC];
+#pragma unroll
+            for (int kk = 0; kk < VEC; kk++) __builtin_memcpy(in[kk], &v[i][kk], 16);
+#pragma unroll
+            for (int j = 0; j < VEC; j++) {
+                T out[VEC];
+#pragma unroll
+                for (int kk = 0; kk < VEC; kk++) out[kk] = in[kk][j];
+                u32x4 w;
+                __builtin_memcpy(&w, out, 16);
+                *(u32x4 *)(lds + lds_off(rb * VEC + j, kb)) = w;
+            }
+        }
+    }
+};
+
+template <typename T, int R, int TR>
+struct Loader;
+template <typename T, int R>
+struct Loader<T, R, 0> : LoadK<T, R> {};
+template <typename T, int R>
+struct Loader<T, R, 1> : LoadMN<T, R> {};
+
+// ── Epilogues ────────────────────────────────────────────────────────────────
+// Each returns the value that enters the per-column sum (bias gradient), or 0.
+
+template <int EPI, typename T>
+__device__ __forceinline__ float epilogue(const GemmDesc &d, int m, int n, float acc, float &lossp) {
+    T *C = (T *)d.C;
+    long ci = (long)m * d.ldc + n;
+    if constexpr (EPI == EPI_STORE) {
+        float v = d.scale * acc;
+        C[ci] = (T)v;
+        return v;
+    } else if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RELU) {
+        float z;
+        if constexpr (sizeof(T) == 2) z = q16(q16(acc) + (float)((const T *)d.bias)[n]);
+        else z = acc + ((const float *)d.bias)[n];
+        if constexpr (EPI == EPI_BIAS_RELU) C[ci] = relu_tag((T)z);
+        else C[ci] = (T)z;
+        return 0.0f;
+    } else if constexpr (EPI == EPI_MSE) {
+        float p = q16(q16(acc) + (float)((const T *)d.bias)[n]);
+        float t = (float)((const T *)d.aux)[(long)m * d.ldaux + n];
+        float diff = p - t;
+        lossp += diff * diff;
+        float dd = q16(diff);
+        C[ci] = (T)dd;
+        return dd;
+    } else if constexpr (EPI == EPI_MASK) {
+        T h = ((const T *)d.aux)[(long)m * d.ldaux + n];
+        float v = relu_dead(h) ? 0.0f : d.scale * acc;
+        C[ci] = (T)v;
+        return v;
+    } else {  // EPI_SGD
+        float g = d.scale * acc;
+        if (d.gout) d.gout[ci] = g;
+        float w = d.W32[ci];
+        w = w - d.lr * g;
+        d.W32[ci] = w;
+        if (d.W16) ((half_t *)d.W16)[ci] = (half_t)w;
+        return 0.0f;
+    }
+}
+
+template <typename T, int BM, int BN, int TA, int TB, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmDesc d) {
+    using MF = Mfma<T>;
+    using vec_t = typename MF::vec_t;
+    constexpr int VEC = MF::VEC;
+    constexpr int BK = 8 * VEC;
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    constexpr int STAGE = (BM + BN) * 128;
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+
+    const int tiles_n = (d.N + BN - 1) / BN;
+    const int tiles_m = (d.M + BM - 1) / BM;
+    const int ntiles = tiles_m * tiles_n;
+    int L = blockIdx.x;
+    // XCD-aware remap: workgroups are dealt round-robin over the 8 XCDs; give each XCD a
+    // contiguous run of logical tiles so its L2 holds a compact block of A rows and B rows.
+    if ((ntiles & 7) == 0) L = (L & 7) * (ntiles >> 3) + (L >> 3);
+    // Grouped order: 4 tile-rows sweep all tile-columns before moving on.
+    constexpr int G = 4;
+    int group = L / (G * tiles_n);
+    int gm0 = group * G;
+    int gsz = min(G, tiles_m - gm0);
+    int rem = L - group * G * tiles_n;
+    int tm = gm0 + rem % gsz, tn = rem / gsz;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+
+    const T *A = (const T *)d.A;
+    const T *B = (const T *)d.B;
+    const bool avec = (d.lda % VEC) == 0 && ((uintptr_t)A & 15) == 0 && (TA == 1 || (d.K % VEC) == 0);
+    const bool bvec = (d.ldb % VEC) == 0 && ((uintptr_t)B & 15) == 0 && (TB == 1 || (d.K % VEC) == 0);
+
+    Loader<T, BM, TA> la;
+    Loader<T, BN, TB> lb;
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
+
+    const int nk = (d.K + BK - 1) / BK;
+    la.load(A, d.lda, m0, d.M, 0, d.K, avec);
+    lb.load(B, d.ldb, n0, d.N, 0, d.K, bvec);
+    la.store(smem);
+    lb.store(smem + BM * 128);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; kt++) {
+        char *cur = smem + (kt & 1) * STAGE;
+        char *nxt = smem + ((kt + 1) & 1) * STAGE;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            la.load(A, d.lda, m0, d.M, (kt + 1) * BK, d.K, avec);
+            lb.load(B, d.ldb, n0, d.N, (kt + 1) * BK, d.K, bvec);
+        }
+        const char *sa = cur, *sb = cur + BM * 128;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int c = 2 * s + (lane >> 5);
+            vec_t a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) a[i] = *(const vec_t *)(sa + lds_off(wm0 + i * 32 + (lane & 31), c));
+#pragma unroll
+            for (int j = 0; j < FN; j++) b[j] = *(const vec_t *)(sb + lds_off(wn0 + j * 32 + (lane & 31), c));
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) MF::mma(a[i], b[j], acc[i][j]);
+        }
+        if (more) {
+            la.store(nxt);
+            lb.store(nxt + BM * 128);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue. 32x32 accumulator layout: element r of lane l is
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    float lossp = 0.0f;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        float cs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (m < d.M && n < d.N) cs += epilogue<EPI, T>(d, m, n, acc[i][j][r], lossp);
+            }
+        }
+        if (d.colsum) {
+            cs += __shfl_xor(cs, 32, 64);
+            if (lane < 32 && n < d.N) atomicAdd(d.colsum + n, cs);
+        }
+    }
+    if constexpr (EPI == EPI_MSE) {
+        lossp = wave_sum(lossp);
+        if (lane == 0) atomicAdd(d.lossacc, lossp);
+    }
+}
+
+template <typename T, int BM, int TA, int TB, int EPI>
+static hipError_t launch_t(const GemmDesc &d, hipStream_t s) {
+    int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI>), dim3(tiles), dim3(kThreads), 0, s, d);
+    return hipGetLastError();
+}
+
+template <typename T, int TA, int TB, int EPI>
+static hipError_t launch_tile(const GemmDesc &d, hipStream_t s) {
+    int tile = d.tile;
+    if (tile == 0) {
+        long t256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
+        long t128 = (long)((d.M + 127) / 128) * ((d.N + 127) / 128);
+        tile = t256 >= 224 ? 256 : (t128 >= 192 ? 128 : 64);
+    }
+    switch (tile) {
+        case 256: return launch_t<T, 256, TA, TB, EPI>(d, s);
+        case 128: return launch_t<T, 128, TA, TB, EPI>(d, s);
+        default: return launch_t<T, 64, TA, TB, EPI>(d, s);
+    }
+}
+
+template <typename T, int TA, int TB>
+static hipError_t launch_epi(const GemmDesc &d, hipStream_t s) {
+    switch (d.epi) {
+        case EPI_STORE: return launch_tile<T, TA, TB, EPI_STORE>(d, s);
+        case EPI_BIAS: return launch_tile<T, TA, TB, EPI_BIAS>(d, s);
+        case EPI_BIAS_RELU: return launch_tile<T, TA, TB, EPI_BIAS_RELU>(d, s);
+        case EPI_MSE:
+            if constexpr (sizeof(T) == 2) return launch_tile<T, TA, TB, EPI_MSE>(d, s);
+            else return hipErrorInvalidValue;
+        case EPI_MASK: return launch_tile<T, TA, TB, EPI_MASK>(d, s);
+        case EPI_SGD: return launch_tile<T, TA, TB, EPI_SGD>(d, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename T>
+static hipError_t launch_layout(const GemmDesc &d, hipStream_t s) {
+    int code = d.ta * 2 + d.tb;
+    switch (code) {
+        case 0: return launch_epi<T, 0, 0>(d, s);
+        case 1: return launch_epi<T, 0, 1>(d, s);
+        case 2: return launch_epi<T, 1, 0>(d, s);
+        default: return launch_epi<T, 1, 1>(d, s);
+    }
+}
+
+hipError_t gemm_launch(const GemmDesc &d, hipStream_t s) {
+    if (d.M <= 0 || d.N <= 0) return hipSuccess;
+    if (d.K < 0) return hipErrorInvalidValue;
+    if (d.dtype == GEMM_F16) return launch_layout<half_t>(d, s);
+    if (d.dtype == GEMM_F32) return launch_layout<float>(d, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace ah

@@ -1,0 +1,24 @@
+// rowops.h — host launchers for row reductions, elementwise and chain kernels.
+#pragma once
+#include "ah_common.h"
+
+namespace ah {
+
+constexpr int kChainStatsRows = 128;  // rows per pass-1 block (chunk partials folded per column)
+constexpr int kChainGradRows = 64;    // rows per pass-2 block
+
+hipError_t fill_f32(float *p, long n, float v, hipStream_t s);
+hipError_t cast_f32_f16(const float *src, half_t *dst, long n, hipStream_t s);
+hipError_t sgd_update(float *p, const float *g, long n, float lr, float scale, half_t *p16, float *gout,
+                      hipStream_t s);
+hipError_t colsum_add(const float *G, int M, int N, long ld, float *out, hipStream_t s);
+hipError_t softmax_ce(const float *z, const int32_t *labels, int B, int C, float a, float *dz, float *rowloss,
+                      hipStream_t s);
+hipError_t sum_scale(const float *v, int n, float a, float *out, hipStream_t s);
+hipError_t mse_finalize(const float *acc, float scale, float *out, hipStream_t s);
+
+long chain_workspace_floats(int R, int Cc);
+hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work, float *dX, float *dg, float *loss,
+                      hipStream_t s);
+
+}  // namespace ah

@@ -1,0 +1,339 @@
+// rowops.hip — row reductions, loss-gradient epilogues and small elementwise kernels (gfx950).
+//
+// Softmax cross-entropy: one wave64 per row, shuffle reductions for the row max, the tie count and
+// the exp-sum; the backward follows the reference's op-by-op rules so the gradient through the row
+// max (tensor/gradient_ruleset.go:307-320, no stop-gradient in the reference) is reproduced.
+//
+// Movement chain (config 5): two streaming passes over X in its stored [R, Cc] layout. A Y-row is an
+// X-column, so lanes own columns and walk rows: every wave load is a contiguous 1 KiB row segment
+// (float4 per lane) and no transpose is ever materialized. Pass 1 keeps online (max, tie count,
+// sum e, sum e^2) per column; a per-column finalize folds the row chunks and evaluates the
+// backward's per-row scalars; pass 2 re-reads X and writes dX in the same layout.
+#include <float.h>
+#include "ah_common.h"
+#include "rowops.h"
+
+namespace ah {
+
+#define AH_INV_LN2 ((float)(1.0 / 0.693147180559945309417232121458176568))
+#define AH_LN2 ((float)0.693147180559945309417232121458176568)
+
+// ── small elementwise kernels ───────────────────────────────────────────────
+
+__global__ void fill_f32_kernel(float *p, long n, float v) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    long stride = (long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) p[i] = v;
+}
+
+__global__ void cast_f32_f16_kernel(const float *src, half_t *dst, long n) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    long stride = (long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) dst[i] = (half_t)src[i];
+}
+
+// p -= lr * (scale * g); optional f16 copy and gradient output. Parameter.SGDStep (nn.go:69-76).
+__global__ void sgd_kernel(float *p, const float *g, long n, float lr, float scale, half_t *p16, float *gout) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    long stride = (long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        float gv = scale * g[i];
+        if (gout) gout[i] = gv;
+        float w = p[i] - lr * gv;
+        p[i] = w;
+        if (p16) p16[i] = (half_t)w;
+    }
+}
+
+// colsum[n] += sum_m G[m, n]   (bias gradient: Expand rule, tensor/gradient_ruleset.go:207-233)
+__global__ __launch_bounds__(256) void colsum_kernel(const float *G, int M, int N, long ld, int rows_per_block,
+                                                      float *out) {
+    __shared__ float red[4][64];
+    int col = blockIdx.x * 64 + (threadIdx.x & 63);
+    int sub = threadIdx.x >> 6;
+    int r0 = blockIdx.y * rows_per_block;
+    int r1 = min(M, r0 + rows_per_block);
+    float acc = 0.0f;
+    if (col < N)
+        for (int r = r0 + sub; r < r1; r += 4) acc += G[(long)r * ld + col];
+    red[sub][threadIdx.x & 63] = acc;
+    __syncthreads();
+    if (sub == 0 && col < N) {
+        float v = ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
+        atomicAdd(out + col, v);
+    }
+}
+
+// ── softmax cross-entropy ───────────────────────────────────────────────────
+// loss = Sum(onehot * logp) * a,  a = f32(-1/B); see the oracle's ora_softmax_ce for the op list.
+__global__ __launch_bounds__(256) void softmax_ce_kernel(const float *z, const int32_t *labels, int B, int C,
+                                                          float a, float *dz, float *rowloss) {
+    int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    int lane = threadIdx.x & 63;
+    if (row >= B) return;
+    const float *zr = z + (long)row * C;
+    int lab = labels[row];
+    float m = -FLT_MAX;
+    for (int c = lane; c < C; c += 64) m = fmaxf(m, zr[c]);
+    m = wave_max(m);
+    float tie = 0.0f, s = 0.0f;
+    for (int c = lane; c < C; c += 64) {
+        float v = zr[c];
+        tie += (v == m) ? 1.0f : 0.0f;
+        s += exp2f((v - m) * AH_INV_LN2);
+    }
+    tie = wave_sum(tie);
+    s = wave_sum(s);
+    float ls = log2f(s) * AH_LN2;
+    if (lane == 0) rowloss[row] = (lab >= 0 && lab < C) ? ((zr[lab] - m) - ls) : 0.0f;
+    float gls = (lab >= 0 && lab < C) ? -a : 0.0f;       // Sum_c -(a*onehot)
+    float glog2 = gls * AH_LN2;
+    float gs = glog2 * (1.0f / (s * AH_LN2));
+    float gm = 0.0f;
+    for (int c = lane; c < C; c += 64) {
+        float v = zr[c];
+        float e = exp2f((v - m) * AH_INV_LN2);
+        float glogp = (c == lab) ? a : 0.0f;
+        float gzs = glogp + ((gs * e) * AH_LN2) * AH_INV_LN2;
+        gm += -gzs;
+        dz[(long)row * C + c] = gzs;
+    }
+    gm = wave_sum(gm);
+    float share = gm * (1.0f / tie);
+    for (int c = lane; c < C; c += 64)
+        if (zr[c] == m) dz[(long)row * C + c] += share;
+}
+
+// out[0] = (Sum_i v[i]) * a   (single block, fixed-order tree)
+__global__ __launch_bounds__(256) void sum_scale_kernel(const float *v, int n, float a, float *out) {
+    __shared__ float red[256];
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) acc += v[i];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = red[0] * a;
+}
+
+// MSE loss finalize: f16 reduce narrowing f16(acc) (codegen/lower.go:712) then * scale in f32.
+__global__ void mse_finalize_kernel(const float *acc, float scale, float *out) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) out[0] = q16(acc[0]) * scale;
+}
+
+// ── config 5: movement + row-reduce chain ───────────────────────────────────
+
+struct ColStat {
+    float m, t, s, q;
+};
+
+__device__ __forceinline__ void stat_push(ColStat &st, float y) {
+    if (y > st.m) {
+        float f = exp2f((st.m - y) * AH_INV_LN2);
+        st.s = st.s * f + 1.0f;
+        st.q = st.q * (f * f) + 1.0f;
+        st.m = y;
+        st.t = 1.0f;
+    } else {
+        float e = exp2f((y - st.m) * AH_INV_LN2);
+        st.s += e;
+        st.q += e * e;
+        st.t += (y == st.m) ? 1.0f : 0.0f;
+    }
+}
+
+__device__ __forceinline__ ColStat stat_merge(const ColStat &a, const ColStat &b) {
+    ColStat r;
+    r.m = fmaxf(a.m, b.m);
+    float fa = exp2f((a.m - r.m) * AH_INV_LN2), fb = exp2f((b.m - r.m) * AH_INV_LN2);
+    if (a.s == 0.0f) fa = 0.0f;
+    if (b.s == 0.0f) fb = 0.0f;
+    r.s = a.s * fa + b.s * fb;
+    r.q = a.q * (fa * fa) + b.q * (fb * fb);
+    r.t = (a.m == r.m ? a.t : 0.0f) + (b.m == r.m ? b.t : 0.0f);
+    return r;
+}
+
+// Pass 1. Block = 4 waves over the same 256 columns (lane owns 4 consecutive columns);
+// blockIdx.y selects a chunk of `rch` rows, waves interleave rows within it.
+__global__ __launch_bounds__(256) void chain_stats_kernel(const float *X, int R, int Cc, int rch, ColStat *part) {
+    __shared__ ColStat sh[4][256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c0 = blockIdx.x * 256 + lane * 4;
+    const int r0 = blockIdx.y * rch, r1 = min(R, r0 + rch);
+    ColStat st[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) st[u] = ColStat{-FLT_MAX, 0.0f, 0.0f, 0.0f};
+    if (c0 < Cc) {
+        int r = r0 + wave;
+        for (; r + 12 < r1; r += 16) {
+            floatx4 v0 = *(const floatx4 *)(X + (long)r * Cc + c0);
+            floatx4 v1 = *(const floatx4 *)(X + (long)(r + 4) * Cc + c0);
+            floatx4 v2 = *(const floatx4 *)(X + (long)(r + 8) * Cc + c0);
+            floatx4 v3 = *(const floatx4 *)(X + (long)(r + 12) * Cc + c0);
+#pragma unroll
+            for (int u = 0; u < 4; u++) { stat_push(st[u], v0[u]); stat_push(st[u], v1[u]); stat_push(st[u], v2[u]); stat_push(st[u], v3[u]); }
+        }
+        for (; r < r1; r += 4) {
+            floatx4 v = *(const floatx4 *)(X + (long)r * Cc + c0);
+#pragma unroll
+            for (int u = 0; u < 4; u++) stat_push(st[u], v[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) sh[wave][lane * 4 + u] = st[u];
+    __syncthreads();
+    int col = blockIdx.x * 256 + threadIdx.x;
+    if (col < Cc) {
+        ColStat a = stat_merge(stat_merge(sh[0][threadIdx.x], sh[1][threadIdx.x]),
+                               stat_merge(sh[2][threadIdx.x], sh[3][threadIdx.x]));
+        part[(long)blockIdx.y * Cc + col] = a;
+    }
+}
+
+// Per-column finalize: fold chunk partials, then the reference backward's per-row scalars.
+// coef[col] = {m, rs, g*r, gsq, gs, share, dg, loss_row}
+__global__ __launch_bounds__(256) void chain_finalize_kernel(const ColStat *part, int nchunks, int R, int Cc,
+                                                              const float *g, float *coef, float *dg) {
+    int col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= Cc) return;
+    ColStat a = part[col];
+    for (int k = 1; k < nchunks; k++) a = stat_merge(a, part[(long)k * Cc + col]);
+    const float eps = 1e-6f;
+    const float rR = 1.0f / (float)R;
+    float rs = 1.0f / a.s;
+    float sumS = a.s * rs;             // Sum_j e_j * rs
+    float sq = a.q * (rs * rs);        // Sum_j (e_j * rs)^2
+    float q = sq * rR;
+    float T = sqrtf(q + eps);
+    float r = 1.0f / T;
+    float gi = g[col];
+    float gR = gi * sumS;
+    float gT = ((-gR) * r) * r;
+    float gu = gT * (1.0f / (2.0f * T));
+    float gsq = gu * rR;
+    float gRs = (gi * r) * a.s + 2.0f * gsq * (rs * a.q);
+    float gs = ((-gRs) * rs) * rs;
+    float gm = -(AH_LN2 * AH_INV_LN2) * (rs * gRs + gs * a.s);
+    float share = gm * (1.0f / a.t);
+    float *cf = coef + (long)col * 8;
+    cf[0] = a.m; cf[1] = rs; cf[2] = gi * r; cf[3] = gsq;
+    cf[4] = gs; cf[5] = share; cf[6] = r * sumS; cf[7] = gi * (r * sumS);
+    dg[col] = r * sumS;
+}
+
+// Pass 2: dX[j, i] from X[j, i] and the per-column scalars.
+__global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, int Cc, int rch, const float *coef,
+                                                          float *dX) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c0 = blockIdx.x * 256 + lane * 4;
+    if (c0 >= Cc) return;
+    float m[4], rs[4], gr[4], gsq[4], gs[4], sh[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const floatx4 a = *(const floatx4 *)(coef + (long)(c0 + u) * 8);
+        const floatx4 b = *(const floatx4 *)(coef + (long)(c0 + u) * 8 + 4);
+        m[u] = a[0]; rs[u] = a[1]; gr[u] = a[2]; gsq[u] = a[3]; gs[u] = b[0]; sh[u] = b[1];
+    }
+    const int r0 = blockIdx.y * rch, r1 = min(R, r0 + rch);
+    for (int r = r0 + wave; r < r1; r += 4) {
+        floatx4 v = *(const floatx4 *)(X + (long)r * Cc + c0);
+        floatx4 o;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            float y = v[u];
+            float e = exp2f((y - m[u]) * AH_INV_LN2);
+            float S = e * rs[u];
+            float t2 = gsq[u] * S;
+            float gS = (gr[u] + t2) + t2;
+            float ge = gS * rs[u] + gs[u];
+            float gzs = ((ge * e) * AH_LN2) * AH_INV_LN2;
+            o[u] = gzs + ((y == m[u]) ? sh[u] : 0.0f);
+        }
+        __builtin_nontemporal_store(o, (floatx4 *)(dX + (long)r * Cc + c0));
+    }
+}
+
+// loss = Sum_i coef[i].loss_row
+__global__ __launch_bounds__(256) void chain_loss_kernel(const float *coef, int Cc, float *out) {
+    __shared__ float red[256];
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < Cc; i += 256) acc += coef[(long)i * 8 + 7];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = red[0];
+}
+
+// ── host launchers ──────────────────────────────────────────────────────────
+
+static int grid_for(long n) {
+    long g = (n + 255) / 256;
+    return (int)(g < 2048 ? (g < 1 ? 1 : g) : 2048);
+}
+
+hipError_t fill_f32(float *p, long n, float v, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+hipError_t cast_f32_f16(const float *src, half_t *dst, long n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
+    return hipGetLastError();
+}
+hipError_t sgd_update(float *p, const float *g, long n, float lr, float scale, half_t *p16, float *gout,
+                      hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(sgd_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, g, n, lr, scale, p16, gout);
+    return hipGetLastError();
+}
+hipError_t colsum_add(const float *G, int M, int N, long ld, float *out, hipStream_t s) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    int rpb = 64;
+    dim3 grid((N + 63) / 64, (M + rpb - 1) / rpb);
+    hipLaunchKernelGGL(colsum_kernel, grid, dim3(256), 0, s, G, M, N, ld, rpb, out);
+    return hipGetLastError();
+}
+hipError_t softmax_ce(const float *z, const int32_t *labels, int B, int C, float a, float *dz, float *rowloss,
+                      hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(softmax_ce_kernel, dim3((B + 3) / 4), dim3(256), 0, s, z, labels, B, C, a, dz, rowloss);
+    return hipGetLastError();
+}
+hipError_t sum_scale(const float *v, int n, float a, float *out, hipStream_t s) {
+    hipLaunchKernelGGL(sum_scale_kernel, dim3(1), dim3(256), 0, s, v, n, a, out);
+    return hipGetLastError();
+}
+hipError_t mse_finalize(const float *acc, float scale, float *out, hipStream_t s) {
+    hipLaunchKernelGGL(mse_finalize_kernel, dim3(1), dim3(64), 0, s, acc, scale, out);
+    return hipGetLastError();
+}
+
+long chain_workspace_floats(int R, int Cc) {
+    int nch = (R + kChainStatsRows - 1) / kChainStatsRows;
+    return (long)nch * Cc * 4 + (long)Cc * 8;
+}
+
+hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work, float *dX, float *dg, float *loss,
+                      hipStream_t s) {
+    if (Cc % 4 != 0 || R <= 0) return hipErrorInvalidValue;
+    int nch = (R + kChainStatsRows - 1) / kChainStatsRows;
+    ColStat *part = (ColStat *)work;
+    float *coef = work + (long)nch * Cc * 4;
+    dim3 g1((Cc + 255) / 256, nch);
+    hipLaunchKernelGGL(chain_stats_kernel, g1, dim3(256), 0, s, X, R, Cc, kChainStatsRows, part);
+    hipLaunchKernelGGL(chain_finalize_kernel, dim3((Cc + 255) / 256), dim3(256), 0, s, part, nch, R, Cc, g, coef, dg);
+    int nch2 = (R + kChainGradRows - 1) / kChainGradRows;
+    dim3 g2((Cc + 255) / 256, nch2);
+    hipLaunchKernelGGL(chain_grad_kernel, g2, dim3(256), 0, s, X, R, Cc, kChainGradRows, coef, dX);
+    hipLaunchKernelGGL(chain_loss_kernel, dim3(1), dim3(256), 0, s, coef, Cc, loss);
+    return hipGetLastError();
+}
+
+}  // namespace ah

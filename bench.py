@@ -1,0 +1,169 @@
+"""Benchmark of anneal's training hot path on one MI355X.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+
+One "step" is one full training step of a BASELINE config (forward, backward, SGD) with inputs and
+parameters resident in HBM. Prints ONE JSON line: steps/s for the config, the roofline of its dominant
+kernel (timed live with hipEvents on the library's stream during the timed steps), per-kernel timings,
+and a CPU baseline (the oracle restatement, timed on a bounded sample on the host cores).
+The default workload is config 3 (f16 GEMM-bound MLP), the config the north-star roofline target names.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F16 = 2.5e15     # MI355X dense f16/bf16 MFMA, FLOP/s
+PEAK_F32 = 157.3e12   # MI355X f32 matrix/vector, FLOP/s
+PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
+
+
+def config_workload(cfg: int):
+    """Returns (trainer kind, dims, lr, batch, inputs dict, kernels [(name, kind, amount)], meta)."""
+    from anneal_amd import _lib as L
+    from anneal_amd import data
+    if cfg == 3:
+        B, D0, D1, D2, D3 = 4096, 1024, 4096, 4096, 1024
+        p = data.mlp3_inputs(B, D0, D1, D2, D3)
+        f = lambda m, n, k: ("flop16", 2.0 * m * n * k)  # noqa: E731
+        ks = [("zero", "bytes", 4 * (D1 + D2 + D3 + 1)), ("fc1", *f(B, D1, D0)), ("fc2", *f(B, D2, D1)),
+              ("fc3_mse", *f(B, D3, D2)), ("dH2", *f(B, D2, D3)), ("dW3", *f(D3, D2, B)), ("dH1", *f(B, D1, D2)),
+              ("dW2", *f(D2, D1, B)), ("dW1", *f(D1, D0, B)), ("sgd_b3", "bytes", 16 * D3),
+              ("sgd_b2", "bytes", 16 * D2), ("sgd_b1", "bytes", 16 * D1), ("loss", "bytes", 8)]
+        meta = {"workload": "config3_f16_mlp_1024-4096-4096-1024_b4096_mse_sgd", "batch": B,
+                "flop_per_step": sum(a for _, k, a in ks if k.startswith("flop")), "dtype": "f16"}
+        return L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], 1e-3, B, p, ks, meta
+    if cfg == 5:
+        R, Cc = 8192, 4096
+        p = data.chain_inputs(R, Cc)
+        ks = [("chain_stats", "bytes", 4.0 * R * Cc), ("chain_finalize", "bytes", 0.0),
+              ("chain_grad", "bytes", 8.0 * R * Cc), ("chain_loss", "bytes", 0.0)]
+        meta = {"workload": "config5_chain_8192x4096_permute_pad_shrink_softmax_rmsnorm", "batch": Cc,
+                "bytes_per_step": 8.0 * R * Cc + 8 * Cc, "dtype": "f32"}
+        return L.TRAIN_CHAIN, [R, Cc], 0.0, R, p, ks, meta
+    raise SystemExit(f"bench: config {cfg} is a parity-test case; bench lines cover configs 3 and 5")
+
+
+def cpu_baseline(cfg: int, inputs: dict):
+    """Oracle (CPU restatement, OpenMP over the host cores) on a bounded sample of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    threads = O.load().ora_num_threads()
+    if cfg == 3:
+        from anneal_amd.data import f16_quantize
+        Bs = 128
+        q = {k: v for k, v in inputs.items()}
+        q["x"], q["t"] = f16_quantize(inputs["x"][:Bs]), f16_quantize(inputs["t"][:Bs])
+        t0 = time.perf_counter()
+        O.mlp3_step(q, 1e-3)
+        dt = time.perf_counter() - t0
+        full = dt * (4096 / Bs)
+        return {"value": 1.0 / full, "unit": "train steps/s", "cores": threads, "kind": "port",
+                "sample": f"one oracle step at batch {Bs} of 4096 (full layer widths), {dt:.1f} s, "
+                          f"scaled x{4096 // Bs} to a full step"}
+    if cfg == 5:
+        X = inputs["X"][:, :256].copy()
+        t0 = time.perf_counter()
+        O.chain_step(X, inputs["g"][:256].copy())
+        dt = time.perf_counter() - t0
+        return {"value": 1.0 / (dt * 16), "unit": "train steps/s", "cores": threads, "kind": "port",
+                "sample": f"256 of 4096 Y-rows (full length 8192), {dt:.2f} s, scaled x16"}
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    from anneal_amd.backend import Device, Trainer
+    kind, dims, lr, batch, p, kernels, meta = config_workload(args.config)
+    dev = Device(0)
+    caps = dev.caps()
+    t = Trainer(dev, kind, dims, lr)
+    for k, v in p.items():
+        t.set(k, v)
+    nk = t.kernel_count(batch)
+    assert nk == len(kernels), (nk, len(kernels))
+    for _ in range(args.warmup):
+        t.step(batch)
+    dev.sync()
+    # Calibration (outside the timed region): each kernel's average duration over 3 steps.
+    per = []
+    for i in range(nk):
+        t.probe(i)
+        for _ in range(3):
+            t.step(batch)
+        ms, n = t.probe_read()
+        per.append(ms / max(n, 1))
+    t.probe(-1)
+    dom = int(np.argmax(per))
+    # Timed region: K steps, the dominant kernel bracketed by hipEvents on the library stream.
+    t.probe(dom)
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        t.step(batch)
+    dev.sync()
+    elapsed = time.perf_counter() - t0
+    dom_ms, dom_n = t.probe_read()
+    t.probe(-1)
+    dom_avg_s = dom_ms / max(dom_n, 1) / 1e3
+
+    name, kk, amount = kernels[dom]
+    if kk.startswith("flop"):
+        peak = PEAK_F16 if kk == "flop16" else PEAK_F32
+        roof = {"bound": "mfma", "achieved": amount / dom_avg_s / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": amount / dom_avg_s / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["traffic"] = None
+    roof["kernel"] = name
+    roof["avg_us"] = dom_avg_s * 1e6
+
+    kinfo = []
+    for (kname, kkind, amt), ms in zip(kernels, per):
+        e = {"name": kname, "avg_us": round(ms * 1e3, 2)}
+        if kkind.startswith("flop"):
+            tf = amt / (ms / 1e3) / 1e12 if ms > 0 else 0.0
+            e.update(tflops=round(tf, 1), frac=round(tf * 1e12 / (PEAK_F16 if kkind == "flop16" else PEAK_F32), 3))
+        elif amt > 0:
+            gbs = amt / (ms / 1e3) / 1e9 if ms > 0 else 0.0
+            e.update(gbs=round(gbs, 1), frac=round(gbs * 1e9 / PEAK_HBM, 3))
+        kinfo.append(e)
+
+    sps = args.steps / elapsed
+    out = {
+        "metric": "train steps/s + per-kernel TFLOP/s or HBM GB/s vs peak, 1xMI355X",
+        "value": sps, "unit": "train steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": meta["dtype"], "data": "synthetic (splitmix64 seed 0, anneal_amd/data.py)",
+        "config": {"workload": meta["workload"], "batch": meta["batch"], "parallelism": "single-gpu"},
+        "roofline": roof, "kernels": kinfo, "device": caps["arch"], "cu_count": caps["cu_count"],
+    }
+    if "flop_per_step" in meta:
+        out["step_tflops"] = meta["flop_per_step"] * sps / 1e12
+    out["cpu_baseline"] = None if args.no_cpu else cpu_baseline(args.config, p)
+    t.close()
+    dev.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

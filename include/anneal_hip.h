@@ -1,0 +1,210 @@
+/*
+ * anneal_hip.h — C ABI of libanneal_hip.so, the MI355X (gfx950) backend for anneal's training hot path.
+ *
+ * Plain C types only (pointers, sizes, int codes). Every call returns AH_OK (0) or an AH_ERR_* code;
+ * the message of the last failure on the calling thread is available from ah_last_error().
+ * A device handle serializes all work onto one HIP stream; calls on one handle are not re-entrant
+ * (the reference funnels every call onto a single owner thread: backend/webgpu/open.go:68-80).
+ *
+ * Each declaration names the reference interface it replaces (paths inside georgebuilds/anneal).
+ */
+#ifndef ANNEAL_HIP_H
+#define ANNEAL_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AH_OK 0
+#define AH_ERR_INVALID 1     /* bad argument / shape / handle */
+#define AH_ERR_HIP 2         /* HIP runtime error */
+#define AH_ERR_UNSUPPORTED 3 /* dtype or feature the device lacks (fail closed, executor.go:42-50) */
+#define AH_ERR_COMPILE 4     /* hiprtc compilation failed */
+#define AH_ERR_NOMEM 5
+
+/* Buffer element types; numbering follows the reference's dtype set used on the device boundary
+ * (backend/webgpu/executor.go:470-528): f16 is 2 bytes, every other type travels in 4 bytes. */
+enum { AH_F32 = 0, AH_F16 = 1, AH_BF16 = 2, AH_I32 = 3, AH_BOOL = 4, AH_U32 = 5 };
+
+typedef struct ah_device ah_device;
+typedef struct ah_kernel ah_kernel;
+typedef struct ah_graph ah_graph;
+typedef struct ah_trainer ah_trainer;
+
+typedef struct {
+    int32_t has_f16;     /* shader-f16 equivalent (always 1 on gfx950) */
+    int32_t has_bf16;
+    int32_t cu_count;
+    int32_t wavefront;   /* 64 */
+    int64_t hbm_bytes;
+    int64_t lds_bytes_per_block;
+    char arch[64];       /* e.g. "gfx950:sramecc+:xnack-" */
+} ah_caps;
+
+/* ── 1. device ───────────────────────────────────────────────────────────────
+ * Replaces webgpu.Open (backend/webgpu/open.go:89) and Executor.Close (backend/device.go:12). */
+const char *ah_last_error(void);
+int ah_open(int ordinal, ah_device **out);
+void ah_close(ah_device *dev);
+int ah_get_caps(ah_device *dev, ah_caps *out);
+int ah_sync(ah_device *dev);
+
+/* ── 2. buffers and the dtype codec ──────────────────────────────────────────
+ * Replaces the per-Run CreateBuffer / WriteBuffer / readBuffer of backend/webgpu/executor.go:83-179,397-468
+ * and the codec of executor.go:470-528 / uop/dtype.go:392-487 (f32->f16 round-to-nearest-even with the
+ * reference's NaN and overflow rules; bf16 = top 16 bits carried in a 4-byte slot). */
+int ah_buf_alloc(ah_device *dev, int64_t n_elems, int32_t dtype, void **dptr);
+int ah_buf_free(ah_device *dev, void *dptr);
+int ah_upload(ah_device *dev, void *dptr, const float *src, int64_t n, int32_t dtype);
+int ah_download(ah_device *dev, float *dst, const void *dptr, int64_t n, int32_t dtype);
+int ah_upload_bytes(ah_device *dev, void *dptr, const void *src, int64_t nbytes);
+int ah_download_bytes(ah_device *dev, void *dst, const void *dptr, int64_t nbytes);
+uint16_t ah_f32_to_f16(float f);   /* uop/dtype.go:392 Float32ToFloat16 */
+float ah_f16_to_f32(uint16_t h);   /* uop/dtype.go:447 Float16ToFloat32 */
+
+/* ── 3./4. modules and launches ──────────────────────────────────────────────
+ * Replaces CreateShaderModule + pipeline creation + Dispatch (backend/webgpu/executor.go:254-395).
+ * `source` is either HIP C++ source (compiled once by hiprtc for gfx950, cached by source hash) or a
+ * template key "tmpl:<name>;k=v;..." selecting a hand-written kernel.
+ * Kernel arguments: n_ptrs device pointers (data0 = output, data1.. = inputs, PARAM order as in
+ * codegen/wgsl.go:58-76), then n_scalars int32 values (the params_n uniform of symbolic kernels). */
+int ah_module_get(ah_device *dev, const char *source, const char *entry, ah_kernel **out);
+int ah_launch(ah_device *dev, ah_kernel *k, const uint32_t grid[3], const uint32_t block[3],
+              void *const *ptrs, int32_t n_ptrs, const int32_t *scalars, int32_t n_scalars);
+
+/* ── 5. timing ───────────────────────────────────────────────────────────────
+ * Replaces Benchmarker.Benchmark's wall-clock loop (backend/webgpu/benchmark.go:18-208) with hipEvents. */
+typedef struct {
+    double min_us, median_us, max_us, mean_us, stddev_us, cv;   /* backend/device.go:16-24 */
+} ah_bench_result;
+
+/* ── 6. graphs (JIT replay) ──────────────────────────────────────────────────
+ * Replaces tensor.JIT's replay of captured ExecItems (tensor/jit.go:178-215): everything enqueued on the
+ * device stream between begin and end is captured and can be replayed without host scheduling. */
+int ah_graph_begin(ah_device *dev);
+int ah_graph_end(ah_device *dev, ah_graph **out);
+int ah_graph_replay(ah_device *dev, ah_graph *g);
+void ah_graph_destroy(ah_graph *g);
+
+/* ── Executor mirror (backend.Executor / Benchmarker / SymbolicExecutor, backend/device.go:10-37) ──
+ * Items follow schedule.ExecItem (schedule/exec.go:6-32): bufs[0] is the output, bufs[1..] inputs in
+ * PARAM order; slot >= 0 marks a slot shared by non-overlapping lifetimes, -1 a leaf or final output.
+ * Final outputs are the bufs[0] that no later item reads; they are returned widened to f32 (4-byte
+ * integer types as raw bits), keyed by uop_idx, in ah_output arrays owned by the library. */
+typedef struct {
+    uint32_t uop_idx;
+    int64_t size;        /* elements; 0 when the leading dim is symbolic */
+    int32_t dtype;
+    int32_t slot;
+    int32_t rank;
+    const int64_t *shape;
+} ah_buffer_desc;
+
+typedef struct {
+    const char *source;           /* HIP source or "tmpl:" key (replaces the WGSL string field) */
+    const ah_buffer_desc *bufs;
+    int32_t n_bufs;
+    const char *const *sym_vars;
+    int32_t n_sym_vars;
+    int32_t local_size[3];
+    int32_t workgroup_count[3];
+} ah_exec_item;
+
+typedef struct {
+    uint32_t uop_idx;
+    const float *data;
+    int64_t n;
+} ah_input;
+
+typedef struct {
+    uint32_t uop_idx;
+    float *data;
+    int64_t n;
+} ah_output;
+
+int ah_run(ah_device *dev, const ah_exec_item *items, int32_t n_items, const ah_input *inputs, int32_t n_inputs,
+           ah_output **outputs, int32_t *n_outputs);                       /* Executor.Run, device.go:11 */
+int ah_run_symbolic(ah_device *dev, const ah_exec_item *items, int32_t n_items, const ah_input *inputs,
+                    int32_t n_inputs, const char *const *bind_names, const int64_t *bind_values,
+                    int32_t n_bind, ah_output **outputs, int32_t *n_outputs); /* RunSymbolic, device.go:35-37 */
+int ah_benchmark(ah_device *dev, const ah_exec_item *item, int32_t warmup, int32_t iterations,
+                 ah_bench_result *out);                                     /* Benchmark, device.go:27-29 */
+void ah_outputs_free(ah_output *outputs, int32_t n);
+
+/* ── Hot-path kernels, callable directly ────────────────────────────────────── */
+
+/* GEMM-shaped REDUCE(ADD, MUL) with fused epilogue (tensor/reduce.go:105-166 as scheduled for
+ * Linear.Forward nn.go:154-162 and the backward rules gradient_ruleset.go:137-140,207-233,285-306).
+ * C[m,n] = epi(sum_k A(m,k) B(n,k)); A stored [M,K] (ta=0) or [K,M] (ta=1); B [N,K] (tb=0) or [K,N] (tb=1). */
+enum { AH_EPI_STORE = 0, AH_EPI_BIAS = 1, AH_EPI_BIAS_RELU = 2, AH_EPI_MSE = 3, AH_EPI_MASK = 4, AH_EPI_SGD = 5 };
+typedef struct {
+    int32_t dtype;          /* AH_F32 or AH_F16 (operands); accumulation is always f32 */
+    int32_t epi;
+    int32_t ta, tb;
+    int32_t M, N, K;
+    const void *A;
+    const void *B;
+    int64_t lda, ldb;
+    void *C;
+    int64_t ldc;
+    const void *bias;
+    const void *aux;
+    int64_t ldaux;
+    float scale;
+    float *colsum;
+    float *W32;
+    void *W16;
+    float lr;
+    float *gout;
+    float *lossacc;
+    int32_t tile;           /* 0 = auto, 64, 128, 256 */
+} ah_gemm_desc;
+int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
+
+/* Softmax cross-entropy forward+backward composed from reference ops (one wave64 per row):
+ * m=Max, zs=z-m, e=Exp(zs), s=Sum e, logp=zs-Log(s), loss=Sum(onehot*logp)*(-1/B); dz includes the
+ * row-max path with its tie split (tensor/gradient_ruleset.go:307-320). */
+int ah_softmax_ce(ah_device *dev, const float *z, const int32_t *labels, int32_t B, int32_t C, float *dz,
+                  float *loss);
+
+/* Config-5 chain: Y = Shrink(Pad(Permute(X,(1,0)))), S = softmax(Y, 1),
+ * out = S * recip(sqrt(mean(S*S,1) + 1e-6)) * g; loss = Sum(out); returns dX [R,Cc], dg [Cc]. */
+int ah_chain_step(ah_device *dev, const float *X, const float *g, int32_t R, int32_t Cc, float *dX, float *dg,
+                  float *loss);
+
+/* ── Device-resident training steps (one BASELINE config each) ───────────────
+ * Replaces the reference step pattern: graph build -> tensor.Backward -> one tensor.Realize per gradient
+ * -> host SGD (examples/mlp.go:112-142, tensor/nn/nn.go:69-106). Parameters stay resident as f32 masters
+ * (plus f16 copies for f16 configs); SGD runs on the device inside the backward kernels. */
+enum {
+    AH_TRAIN_MLP_CE = 1,    /* dims {Bmax, D, H, C}: configs 1 and 4 */
+    AH_TRAIN_CONVNET = 2,   /* dims {N, Hin, C1, C2, NC}: config 2 */
+    AH_TRAIN_MLP3_F16 = 3,  /* dims {B, D0, D1, D2, D3}: config 3 */
+    AH_TRAIN_CHAIN = 4,     /* dims {R, Cc}: config 5 */
+};
+/* Slot numbering per kind (host arrays are f32 unless noted; labels are int32):
+ *  MLP_CE : 0 x, 1 labels, 2 W1, 3 b1, 4 W2, 5 b2, 6 loss, 7 dW1, 8 db1, 9 dW2, 10 db2
+ *  CONVNET: 0 x, 1 labels, 2 cw1, 3 cb1, 4 cw2, 5 cb2, 6 fw, 7 fb, 8 loss, 9 dcw1, 10 dcb1, 11 dcw2,
+ *           12 dcb2, 13 dfw, 14 dfb
+ *  MLP3   : 0 x, 1 t, 2 W1, 3 b1, 4 W2, 5 b2, 6 W3, 7 b3, 8 loss, 9 dW1, 10 db1, 11 dW2, 12 db2,
+ *           13 dW3, 14 db3
+ *  CHAIN  : 0 X, 1 g, 2 loss, 3 dX, 4 dg
+ * Gradient slots are filled only by steps run with AH_STEP_STORE_GRADS. */
+#define AH_STEP_STORE_GRADS 1
+#define AH_STEP_GRAPH 2      /* capture the step once per batch size as a hipGraph and replay it (tensor.JIT) */
+int ah_trainer_create(ah_device *dev, int32_t kind, const int64_t *dims, int32_t n_dims, float lr,
+                      ah_trainer **out);
+void ah_trainer_destroy(ah_trainer *t);
+int ah_trainer_set(ah_trainer *t, int32_t slot, const void *host, int64_t n);
+int ah_trainer_get(ah_trainer *t, int32_t slot, void *host, int64_t n);
+int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags);
+/* Per-kernel probe: hipEvents around the index-th kernel launch of every following step. */
+int ah_trainer_probe(ah_trainer *t, int32_t kernel_index);
+int ah_trainer_probe_read(ah_trainer *t, double *total_ms, int64_t *count);
+int ah_trainer_kernel_count(ah_trainer *t, int64_t batch, int32_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

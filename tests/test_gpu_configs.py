@@ -1,0 +1,138 @@
+"""Config-level parity: one device-resident training step per BASELINE config vs the CPU oracle (GPU).
+
+Small and medium shapes run the oracle directly; full-size shapes the oracle cannot finish in seconds
+are checked through size-independent properties (train-step invariants) and a float64 restatement.
+Tolerances: f32 configs 1e-4 norm-wise on gradients and loss; f16 config 2e-2 after one SGD step.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from anneal_amd import _lib as L
+from anneal_amd import data
+from anneal_amd.backend import Trainer
+
+pytestmark = pytest.mark.gpu
+
+
+def check_update(got, old, new, tol):
+    """Updated parameter vs the oracle's: the update lr*g within tol (norm-wise), plus the f32 rounding
+    of the stored weight itself (a few ulps of |W|)."""
+    got, old, new = (np.asarray(a, np.float64).ravel() for a in (got, old, new))
+    step = np.max(np.abs(new - old))
+    allowed = tol * step + 4 * np.finfo(np.float32).eps * np.max(np.abs(new))
+    return np.max(np.abs(got - new)) <= allowed
+
+
+def run_mlp_ce(dev, p, B, lr, graph=False):
+    D, H, Cn = p["W1"].shape[1], p["W1"].shape[0], p["W2"].shape[0]
+    t = Trainer(dev, L.TRAIN_MLP_CE, [B, D, H, Cn], lr)
+    for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+        t.set(k, p[k])
+    t.step(B, store_grads=True, graph=graph)
+    out = {"loss": t.get("loss", 1)[0]}
+    for k, n in (("dW1", H * D), ("db1", H), ("dW2", Cn * H), ("db2", Cn), ("W1", H * D), ("b1", H),
+                 ("W2", Cn * H), ("b2", Cn)):
+        out[k] = t.get(k, n)
+    t.close()
+    return out
+
+
+def check_mlp(out, p, lr, tol=1e-4):
+    wl, g, new = O.mlp_ce_step(p, lr)
+    assert abs(out["loss"] - wl) <= tol * max(1, abs(wl))
+    for k in ("dW1", "db1", "dW2", "db2"):
+        assert O.relerr(out[k], g[k].ravel()) < tol, k
+    for k in ("W1", "b1", "W2", "b2"):
+        assert check_update(out[k], p[k], new[k], tol), k
+
+
+def test_config1_mlp_step(dev):
+    p = data.mlp_ce_inputs(64, 784, 128, 10)
+    check_mlp(run_mlp_ce(dev, p, 64, 0.01), p, 0.01)
+
+
+@pytest.mark.parametrize("N", [1, 7, 256])
+def test_config4_dynmlp_step_graph_replay(dev, N):
+    p = data.mlp_ce_inputs(N, 512, 2048, 512, x_lo=-1.0, x_hi=1.0)
+    check_mlp(run_mlp_ce(dev, p, N, 0.01, graph=True), p, 0.01)
+
+
+def test_config4_one_capture_many_batches(dev):
+    """One trainer sized for 4096 replays captured graphs for N in {1, 7, 256}; each equals an eager step."""
+    Bmax = 4096
+    p = data.mlp_ce_inputs(Bmax, 512, 2048, 512, x_lo=-1.0, x_hi=1.0)
+    tg = Trainer(dev, L.TRAIN_MLP_CE, [Bmax, 512, 2048, 512], 0.0)
+    te = Trainer(dev, L.TRAIN_MLP_CE, [Bmax, 512, 2048, 512], 0.0)
+    for t in (tg, te):
+        for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+            t.set(k, p[k])
+    for N in (1, 7, 256, 4096):
+        for _ in range(3):
+            tg.step(N, store_grads=True, graph=True)
+        te.step(N, store_grads=True)
+        for k, n in (("dW1", 2048 * 512), ("dW2", 512 * 2048), ("loss", 1)):
+            assert O.relerr(tg.get(k, n), te.get(k, n)) < 1e-6, (N, k)
+    tg.close()
+    te.close()
+
+
+def test_config2_convnet_step(dev):
+    p = data.convnet_inputs()
+    lr = 0.01
+    wl, g, new = O.convnet_step(p, lr)
+    t = Trainer(dev, L.TRAIN_CONVNET, [32, 28, 8, 16, 10], lr)
+    for k in ("x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+        t.set(k, p[k])
+    t.step(32, store_grads=True)
+    assert abs(t.get("loss", 1)[0] - wl) < 1e-4 * max(1, abs(wl))
+    for k in ("dcw1", "dcb1", "dcw2", "dcb2", "dfw", "dfb"):
+        assert O.relerr(t.get(k, g[k].size), g[k].ravel()) < 1e-4, k
+    for k in ("cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+        assert check_update(t.get(k, new[k].size), p[k], new[k], 1e-4), k
+    t.close()
+
+
+def test_config2_tie_split_bit_exact(dev):
+    """All-equal pooling windows (ReLU zeros) must split the adjoint exactly like the oracle."""
+    p = data.convnet_inputs(N=4, seed=3)
+    p["x"] = np.zeros_like(p["x"])                 # every conv output equals its bias -> many ties
+    p["cb1"] = np.array([0.5, -0.5, 0, 0.25, 0, -1, 1, 0], np.float32)
+    wl, g, _ = O.convnet_step(p, 0.0)
+    t = Trainer(dev, L.TRAIN_CONVNET, [4, 28, 8, 16, 10], 0.0)
+    for k in ("x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+        t.set(k, p[k])
+    t.step(4, store_grads=True)
+    for k in ("dcw1", "dcb1", "dcw2", "dcb2"):
+        assert O.relerr(t.get(k, g[k].size), g[k].ravel()) < 1e-4, k
+    t.close()
+
+
+def run_mlp3(dev, p, lr):
+    B, D0 = p["x"].shape
+    D1, D2, D3 = p["W1"].shape[0], p["W2"].shape[0], p["W3"].shape[0]
+    t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], lr)
+    for k in ("x", "t", "W1", "b1", "W2", "b2", "W3", "b3"):
+        t.set(k, p[k])
+    t.step(B, store_grads=True)
+    out = {"loss": t.get("loss", 1)[0]}
+    for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3", "W1", "b1", "W2", "b2", "W3", "b3"):
+        out[k] = t.get(k, p[k.lstrip("d")].size if k.startswith("d") else p[k].size)
+    t.close()
+    return out
+
+
+@pytest.mark.parametrize("shape", [(256, 128, 256, 256, 128), (512, 256, 512, 384, 256)])
+def test_config3_f16_mlp_step_vs_oracle(dev, shape):
+    B, D0, D1, D2, D3 = shape
+    p = data.mlp3_inputs(B, D0, D1, D2, D3)
+    q = dict(p)
+    q["x"], q["t"] = data.f16_quantize(p["x"]), data.f16_quantize(p["t"])
+    lr = 1e-3
+    wl, g, new = O.mlp3_step(q, lr)
+    out = run_mlp3(dev, p, lr)
+    assert (np.isinf(out["loss"]) and np.isinf(wl)) or abs(out["loss"] - wl) < 2e-2 * abs(wl)
+    for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3"):
+        assert O.relerr(out[k], g[k].ravel()) < 2e-2, k
+    for k in ("W1", "b1", "W2", "b2", "W3", "b3"):
+        assert check_update(out[k], p[k], new[k], 2e-2), k

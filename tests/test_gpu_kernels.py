@@ -1,0 +1,151 @@
+"""Kernel-level parity of the HIP hot path against the oracle / f64 restatements (GPU).
+
+Tolerances: f32 contractions and reductions 1e-4 norm-wise relative error
+(max|a-b| / max|b|); f16 outputs within one f16 ulp of the f64-accumulated value rounded at the same
+points; index/tie work bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from anneal_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(99)
+
+
+def q16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def store_operand(X, trans):
+    return np.ascontiguousarray(X.T if trans else X)
+
+
+GEMM_CASES = [
+    # dtype, ta, tb, M, N, K, tile
+    (L.AH_F32, 0, 0, 64, 128, 784, 0), (L.AH_F32, 0, 1, 64, 128, 10, 0), (L.AH_F32, 1, 1, 10, 128, 64, 0),
+    (L.AH_F32, 1, 0, 70, 33, 37, 64), (L.AH_F32, 0, 0, 300, 260, 130, 128), (L.AH_F32, 1, 1, 256, 256, 96, 256),
+    (L.AH_F16, 0, 0, 256, 256, 256, 0), (L.AH_F16, 0, 1, 130, 200, 72, 64), (L.AH_F16, 1, 1, 96, 160, 300, 128),
+    (L.AH_F16, 1, 0, 512, 512, 128, 256), (L.AH_F16, 0, 0, 33, 17, 24, 64),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: "dt%d_ta%d_tb%d_%dx%dx%d_t%d" % c)
+def test_gemm_store_and_bias_relu(dev, case):
+    dt, ta, tb, M, N, K, tile = case
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    B = RNG.standard_normal((N, K)).astype(np.float32)
+    bias = RNG.standard_normal(N).astype(np.float32)
+    if dt == L.AH_F16:
+        A, B, bias = q16(A), q16(B), q16(bias)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    As, Bs = store_operand(A, ta), store_operand(B, tb)
+    npdt = np.float16 if dt == L.AH_F16 else np.float32
+    dA, dB = dev.buffer(As.astype(npdt), dt), dev.buffer(Bs.astype(npdt), dt)
+    dbias = dev.buffer(bias.astype(npdt), dt)
+    dC = dev.buffer(M * N, dt)
+    common = dict(dtype=dt, ta=ta, tb=tb, M=M, N=N, K=K, A=dA, B=dB, lda=As.shape[1], ldb=Bs.shape[1], C_out=dC,
+                  ldc=N, tile=tile)
+    dev.gemm(epi=L.EPI_STORE, scale=0.5, **common)
+    C = dC.read().astype(np.float32).reshape(M, N)
+    if dt == L.AH_F32:
+        assert O.relerr(C, 0.5 * ref) < 1e-5
+    else:
+        np.testing.assert_allclose(C, q16(0.5 * ref), rtol=2e-3, atol=2e-3 * np.abs(ref).max())
+    dev.gemm(epi=L.EPI_BIAS_RELU, bias=dbias, **common)
+    H = dC.read().astype(np.float32).reshape(M, N)
+    if dt == L.AH_F32:
+        z = ref + bias
+        assert O.relerr(H, np.maximum(z, 0)) < 1e-5
+    else:
+        z = q16(q16(ref) + bias)
+        np.testing.assert_allclose(H, np.maximum(z, 0), rtol=2e-3, atol=2e-3 * np.abs(z).max())
+    dead = np.signbit(H) & (H == 0)
+    assert np.array_equal(dead, z < 0), "ReLU tag (-0 for z<0) mismatch"
+    for b in (dA, dB, dbias, dC):
+        b.free()
+
+
+@pytest.mark.parametrize("dt", [L.AH_F32, L.AH_F16])
+def test_gemm_mask_colsum_and_sgd(dev, dt):
+    M, N, K = 192, 160, 96
+    npdt = np.float16 if dt == L.AH_F16 else np.float32
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    Bm = RNG.standard_normal((K, N)).astype(np.float32)       # stored [K,N] (tb = 1)
+    if dt == L.AH_F16:
+        A, Bm = q16(A), q16(Bm)
+    Hact = RNG.standard_normal((M, N)).astype(np.float32)
+    Hact = np.where(Hact < 0, np.float32(-0.0), Hact).astype(npdt)
+    ref = A.astype(np.float64) @ Bm.astype(np.float64)
+    masked = np.where(np.signbit(Hact.astype(np.float32)) & (Hact == 0), 0.0, 2.0 * ref)
+    dA, dB, dH = dev.buffer(A.astype(npdt), dt), dev.buffer(Bm.astype(npdt), dt), dev.buffer(Hact, dt)
+    dC = dev.buffer(M * N, dt)
+    cs = dev.buffer(np.zeros(N, np.float32), L.AH_F32)
+    dev.gemm(dtype=dt, epi=L.EPI_MASK, ta=0, tb=1, M=M, N=N, K=K, A=dA, B=dB, lda=K, ldb=N, C_out=dC, ldc=N,
+             aux=dH, ldaux=N, scale=2.0, colsum=cs)
+    C = dC.read().astype(np.float32).reshape(M, N)
+    tol = 1e-5 if dt == L.AH_F32 else 2e-3
+    assert O.relerr(C, masked) < tol
+    assert O.relerr(cs.read(), masked.sum(0)) < 1e-4
+    # SGD epilogue: W -= lr * (scale * A^T-contraction); dW[n,k] = sum_m G[m,n] X[m,k]
+    G, X = A, RNG.standard_normal((M, 48)).astype(np.float32)
+    if dt == L.AH_F16:
+        X = q16(X)
+    W = RNG.standard_normal((K, 48)).astype(np.float32)
+    dG, dX = dev.buffer(G.astype(npdt), dt), dev.buffer(X.astype(npdt), dt)
+    dW, dg = dev.buffer(W, L.AH_F32), dev.buffer(K * 48, L.AH_F32)
+    dW16 = dev.buffer(K * 48, L.AH_F16)
+    dev.gemm(dtype=dt, epi=L.EPI_SGD, ta=1, tb=1, M=K, N=48, K=M, A=dG, B=dX, lda=K, ldb=48, ldc=48, scale=0.25,
+             W32=dW, W16=dW16, lr=0.1, gout=dg)
+    gref = 0.25 * (G.astype(np.float64).T @ X.astype(np.float64))
+    assert O.relerr(dg.read().reshape(K, 48), gref) < (1e-5 if dt == L.AH_F32 else 1e-4)
+    Wn = dW.read().reshape(K, 48)
+    assert O.relerr(Wn - W, -0.1 * gref) < 1e-4
+    np.testing.assert_array_equal(dW16.read(), Wn.astype(np.float16).ravel())
+
+
+def test_gemm_mse_epilogue(dev):
+    M, N, K = 128, 96, 64
+    A, B = q16(RNG.standard_normal((M, K))), q16(RNG.standard_normal((N, K)) * 0.2)
+    bias, T = q16(RNG.standard_normal(N) * 0.1), q16(RNG.standard_normal((M, N)))
+    dA, dB = dev.buffer(A.astype(np.float16), L.AH_F16), dev.buffer(B.astype(np.float16), L.AH_F16)
+    db, dT = dev.buffer(bias.astype(np.float16), L.AH_F16), dev.buffer(T.astype(np.float16), L.AH_F16)
+    dD = dev.buffer(M * N, L.AH_F16)
+    cs, la = dev.buffer(np.zeros(N, np.float32), L.AH_F32), dev.buffer(np.zeros(1, np.float32), L.AH_F32)
+    dev.gemm(dtype=L.AH_F16, epi=L.EPI_MSE, ta=0, tb=0, M=M, N=N, K=K, A=dA, B=dB, lda=K, ldb=K, C_out=dD, ldc=N,
+             bias=db, aux=dT, ldaux=N, colsum=cs, lossacc=la)
+    P = q16(q16(A.astype(np.float64) @ B.astype(np.float64).T) + bias)
+    d = q16(P - T)
+    got = dD.read().astype(np.float32).reshape(M, N)
+    assert np.mean(got == d) > 0.99 and O.relerr(got, d) < 2e-3
+    assert O.relerr(cs.read(), d.astype(np.float64).sum(0)) < 1e-3
+    assert abs(la.read()[0] - ((P - T).astype(np.float64) ** 2).sum()) < 1e-3 * ((P - T) ** 2).sum()
+
+
+@pytest.mark.parametrize("B,C", [(64, 10), (7, 512), (4096, 512), (3, 1)])
+def test_softmax_ce_kernel(dev, B, C):
+    z = (RNG.standard_normal((B, C)) * 3).astype(np.float32)
+    z[0, : min(C, 3)] = z[0].max() + 1.0          # a tied maximum
+    lab = RNG.integers(0, C, B).astype(np.int32)
+    wl, wdz = O.softmax_ce(z, lab)
+    dz_, dl_, dd, dloss = dev.buffer(z), dev.buffer(lab, L.AH_I32), dev.buffer(B * C), dev.buffer(1)
+    dev.softmax_ce(dz_, dl_, B, C, dd, dloss)
+    assert O.relerr(dd.read().reshape(B, C), wdz) < 1e-5
+    assert abs(dloss.read()[0] - wl) <= 1e-5 * max(1.0, abs(wl))
+
+
+@pytest.mark.parametrize("R,Cc", [(64, 32), (257, 260), (1024, 512)])
+def test_chain_kernel_vs_oracle(dev, R, Cc):
+    X = RNG.standard_normal((R, Cc)).astype(np.float32)
+    X[5, :] = X.max() + 0.5                             # every row of Y gets a tie candidate
+    X[9, :] = X[5, :]
+    g = (1 + 0.02 * RNG.standard_normal(Cc)).astype(np.float32)
+    wl, wdX, wdg = O.chain_step(X, g)
+    dXb, dgb, dX, dg, dl = dev.buffer(X), dev.buffer(g), dev.buffer(R * Cc), dev.buffer(Cc), dev.buffer(1)
+    dev.chain_step(dXb, dgb, R, Cc, dX, dg, dl)
+    assert O.relerr(dX.read().reshape(R, Cc), wdX) < 1e-4
+    assert O.relerr(dg.read(), wdg) < 1e-5
+    assert abs(dl.read()[0] - wl) < 1e-5 * abs(wl)
+    for b in (dXb, dgb, dX, dg, dl):
+        b.free()
