@@ -49,6 +49,7 @@ struct GemmDesc {
 
 #ifdef __HIP_PLATFORM_AMD__
 hipError_t gemm_launch(const GemmDesc &d, hipStream_t s);
+bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err);
 #endif
 
 }  // namespace ah

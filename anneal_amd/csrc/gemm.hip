@@ -4,8 +4,8 @@
 // (BM/2) x (BN/2) sub-tile built from 32x32 MFMA blocks (f16: v_mfma_f32_32x32x16_f16,
 // f32: v_mfma_f32_32x32x2f32). K advances in stages of 8 16-byte chunks per row (64 halves or
 // 32 floats); two LDS stages are double-buffered so global loads of stage k+1 overlap the MFMAs of
-// stage k. LDS rows are 128 B with an XOR swizzle of the 16-byte chunk index by (row & 7), so
-// the ds_read_b128 fragment reads of 8 consecutive rows fall in distinct bank groups.
+// stage k. LDS rows are 128 B, paired into XOR-swizzled 256-byte super-rows (see lds_off).
+// This generic path serves f32 operands and f16 shapes the direct-to-LDS kernel (gemm16.hip) rejects.
 //
 // Operands stored MN-contiguous ([K][M] / [K][N]) are transposed on the way into LDS: each
 // thread loads a VEC x VEC sub-block with VEC coalesced 16-byte loads and writes VEC K-contiguous
@@ -15,12 +15,19 @@
 // reduces (codegen/lower.go:667-716); products of f16 inputs are exact in f32.
 #include "ah_common.h"
 #include "gemm.h"
+#include "gemm_epi.h"
 
 namespace ah {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ int lds_off(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// Two 128-byte rows form a 256-byte super-row whose 16-byte slots are XOR-swizzled by the super-row
+// index: ds_read_b128 fragment reads (16 consecutive rows, one chunk) and the row-major stores hit 16
+// distinct slots of the 64-bank LDS.
+__device__ __forceinline__ int lds_off(int r, int c) {
+    const int q = r >> 1;
+    return q * 256 + (((((r & 1) << 3) | c) ^ (q & 15)) << 4);
+}
 
 template <typename T>
 struct Mfma;
@@ -150,48 +157,6 @@ template <typename T, int R>
 struct Loader<T, R, 0> : LoadK<T, R> {};
 template <typename T, int R>
 struct Loader<T, R, 1> : LoadMN<T, R> {};
-
-// ── Epilogues ────────────────────────────────────────────────────────────────
-// Each returns the value that enters the per-column sum (bias gradient), or 0.
-
-template <int EPI, typename T>
-__device__ __forceinline__ float epilogue(const GemmDesc &d, int m, int n, float acc, float &lossp) {
-    T *C = (T *)d.C;
-    long ci = (long)m * d.ldc + n;
-    if constexpr (EPI == EPI_STORE) {
-        float v = d.scale * acc;
-        C[ci] = (T)v;
-        return v;
-    } else if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RELU) {
-        float z;
-        if constexpr (sizeof(T) == 2) z = q16(q16(acc) + (float)((const T *)d.bias)[n]);
-        else z = acc + ((const float *)d.bias)[n];
-        if constexpr (EPI == EPI_BIAS_RELU) C[ci] = relu_tag((T)z);
-        else C[ci] = (T)z;
-        return 0.0f;
-    } else if constexpr (EPI == EPI_MSE) {
-        float p = q16(q16(acc) + (float)((const T *)d.bias)[n]);
-        float t = (float)((const T *)d.aux)[(long)m * d.ldaux + n];
-        float diff = p - t;
-        lossp += diff * diff;
-        float dd = q16(diff);
-        C[ci] = (T)dd;
-        return dd;
-    } else if constexpr (EPI == EPI_MASK) {
-        T h = ((const T *)d.aux)[(long)m * d.ldaux + n];
-        float v = relu_dead(h) ? 0.0f : d.scale * acc;
-        C[ci] = (T)v;
-        return v;
-    } else {  // EPI_SGD
-        float g = d.scale * acc;
-        if (d.gout) d.gout[ci] = g;
-        float w = d.W32[ci];
-        w = w - d.lr * g;
-        d.W32[ci] = w;
-        if (d.W16) ((half_t *)d.W16)[ci] = (half_t)w;
-        return 0.0f;
-    }
-}
 
 template <typename T, int BM, int BN, int TA, int TB, int EPI>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmDesc d) {
@@ -348,7 +313,11 @@ static hipError_t launch_layout(const GemmDesc &d, hipStream_t s) {
 hipError_t gemm_launch(const GemmDesc &d, hipStream_t s) {
     if (d.M <= 0 || d.N <= 0) return hipSuccess;
     if (d.K < 0) return hipErrorInvalidValue;
-    if (d.dtype == GEMM_F16) return launch_layout<half_t>(d, s);
+    if (d.dtype == GEMM_F16) {
+        hipError_t e = hipSuccess;
+        if (gemm16_try_launch(d, s, &e)) return e;
+        return launch_layout<half_t>(d, s);
+    }
     if (d.dtype == GEMM_F32) return launch_layout<float>(d, s);
     return hipErrorInvalidValue;
 }
