@@ -77,6 +77,8 @@ SIGNATURES = {
     "ah_module_get": (C.c_int, [_P, C.c_char_p, C.c_char_p, C.POINTER(_P)]),
     "ah_launch": (C.c_int, [_P, _P, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(_P), C.c_int32,
                             C.POINTER(C.c_int32), C.c_int32]),
+    "ah_timer_start": (C.c_int, [_P]),
+    "ah_timer_stop": (C.c_int, [_P, C.POINTER(C.c_double)]),
     "ah_graph_begin": (C.c_int, [_P]),
     "ah_graph_end": (C.c_int, [_P, C.POINTER(_P)]),
     "ah_graph_replay": (C.c_int, [_P, _P]),

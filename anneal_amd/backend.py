@@ -69,6 +69,15 @@ class Device:
     def sync(self) -> None:
         L.check(self.lib.ah_sync(self.h))
 
+    def timer_start(self) -> None:
+        L.check(self.lib.ah_timer_start(self.h))
+
+    def timer_stop(self) -> float:
+        """Milliseconds of device-stream time since timer_start (waits for the stream)."""
+        ms = C.c_double()
+        L.check(self.lib.ah_timer_stop(self.h, C.byref(ms)))
+        return ms.value
+
     def gemm(self, *, dtype, epi, ta, tb, M, N, K, A, B, lda, ldb, C_out=None, ldc=0, bias=None, aux=None,
              ldaux=0, scale=1.0, colsum=None, W32=None, W16=None, lr=0.0, gout=None, lossacc=None, tile=0):
         p = lambda b: None if b is None else b.ptr  # noqa: E731

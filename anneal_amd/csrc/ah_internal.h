@@ -44,6 +44,7 @@ struct ah_device {
     hipDeviceProp_t props{};
     std::unordered_map<std::string, ah_kernel *> modules;
     std::string arch;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
 };
 
 struct ah_graph {

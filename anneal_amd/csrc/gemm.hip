@@ -236,30 +236,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmDesc d) {
         __syncthreads();
     }
 
-    // Epilogue. 32x32 accumulator layout: element r of lane l is
-    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-    float lossp = 0.0f;
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int n = n0 + wn0 + j * 32 + (lane & 31);
-        float cs = 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (m < d.M && n < d.N) cs += epilogue<EPI, T>(d, m, n, acc[i][j][r], lossp);
-            }
-        }
-        if (d.colsum) {
-            cs += __shfl_xor(cs, 32, 64);
-            if (lane < 32 && n < d.N) atomicAdd(d.colsum + n, cs);
-        }
-    }
-    if constexpr (EPI == EPI_MSE) {
-        lossp = wave_sum(lossp);
-        if (lane == 0) atomicAdd(d.lossacc, lossp);
-    }
+    epilogue_tile<EPI, T, FM, FN>(d, acc, m0 + wm0, n0 + wn0, lane);
 }
 
 template <typename T, int BM, int TA, int TB, int EPI>

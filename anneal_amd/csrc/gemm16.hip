@@ -90,11 +90,14 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
     }
 }
 
-template <int BM, int BN, int TA, int TB, int EPI>
+// VEPI: every wave tile is in bounds and the epilogue arrays admit vector access, so the LDS-staged
+// vector epilogue is used (chosen on the host; a kernel holding both epilogues spills registers).
+template <int BM, int BN, int TA, int TB, int EPI, bool VEPI>
 __global__ __launch_bounds__(kThreads) void gemm16_kernel(GemmDesc d) {
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
     constexpr int ABYTES = BM * 128, BBYTES = BN * 128, STAGE = ABYTES + BBYTES;
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+    static_assert(4 * WM * 256 <= 2 * STAGE, "epilogue staging must fit the operand LDS");
 
     const int tiles_n = (d.N + BN - 1) / BN;
     const int tiles_m = (d.M + BM - 1) / BM;
@@ -158,28 +161,13 @@ __global__ __launch_bounds__(kThreads) void gemm16_kernel(GemmDesc d) {
         }
     }
 
-    // Epilogue: element r of lane l of a 32x32 block is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-    float lossp = 0.0f;
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int n = n0 + wn0 + j * 32 + (lane & 31);
-        float cs = 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (m < d.M && n < d.N) cs += epilogue<EPI, half_t>(d, m, n, acc[i][j][r], lossp);
-            }
-        }
-        if (d.colsum) {
-            cs += __shfl_xor(cs, 32, 64);
-            if (lane < 32 && n < d.N) atomicAdd(d.colsum + n, cs);
-        }
-    }
-    if constexpr (EPI == EPI_MSE) {
-        lossp = wave_sum(lossp);
-        if (lane == 0) atomicAdd(d.lossacc, lossp);
+    const int mb = m0 + wm0, nb = n0 + wn0;
+    if constexpr (VEPI) {
+        // Epilogue through the (now idle) operand LDS: each wave owns FM*32 rows x 64 f32 columns.
+        __syncthreads();
+        epilogue_lds<EPI, half_t, FM, FN>(d, acc, mb, nb, lane, smem + wave * (WM * 256));
+    } else {
+        epilogue_tile<EPI, half_t, FM, FN>(d, acc, mb, nb, lane);
     }
 }
 
@@ -192,7 +180,11 @@ static bool operand_ok(const void *p, long ld, int rows) {
 template <int BM, int TA, int TB, int EPI>
 static hipError_t launch(const GemmDesc &d, hipStream_t s) {
     int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI>), dim3(tiles), dim3(kThreads), 0, s, d);
+    const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
+                        (uintptr_t)d.W16 | (uintptr_t)d.gout;
+    const bool vepi = d.M % BM == 0 && d.N % BM == 0 && d.ldc % 4 == 0 && d.ldaux % 4 == 0 && (a & 15) == 0;
+    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true>), dim3(tiles), dim3(kThreads), 0, s, d);
+    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false>), dim3(tiles), dim3(kThreads), 0, s, d);
     return hipGetLastError();
 }
 

@@ -126,7 +126,9 @@ struct MlpCeTrainer : ah_trainer {
         rc |= alloc(&dZ1, (size_t)Bmax * H); rc |= alloc(&rowloss, Bmax); rc |= alloc(&acc, H + C);
         rc |= alloc(&loss, 1); rc |= alloc(&gW1, (size_t)H * D); rc |= alloc(&gb1, H);
         rc |= alloc(&gW2, (size_t)C * H); rc |= alloc(&gb2, C);
-        return rc ? AH_ERR_HIP : AH_OK;
+        if (rc) return AH_ERR_HIP;
+        AH_HIP(hipMemset(acc, 0, sizeof(float) * (H + C)));
+        return AH_OK;
     }
     int set(int slot, const void *h, int64_t n) override {
         struct { void *p; int64_t n; } t[] = {{x, (int64_t)Bmax * D}, {lab, Bmax}, {W1, (int64_t)H * D}, {b1, H},
@@ -149,7 +151,6 @@ struct MlpCeTrainer : ah_trainer {
         const bool sg = flags & AH_STEP_STORE_GRADS;
         const float a = (float)(-1.0 / (double)B);
         float *db1 = acc, *db2 = acc + H;
-        LAUNCH("zero", fill_f32(acc, H + C, 0.0f, s));
         GemmDesc g1 = gdesc(GEMM_F32, EPI_BIAS_RELU, 0, 0, B, H, D, x, D, W1, D, H1, H);
         g1.bias = b1;
         LAUNCH("fc1", gemm_launch(g1, s));
@@ -167,9 +168,11 @@ struct MlpCeTrainer : ah_trainer {
         GemmDesc g5 = gdesc(GEMM_F32, EPI_SGD, 1, 1, H, D, B, dZ1, H, x, D, nullptr, D);
         g5.W32 = W1; g5.lr = lr; g5.gout = sg ? gW1 : nullptr;
         LAUNCH("dW1", gemm_launch(g5, s));
-        LAUNCH("sgd_b2", sgd_update(b2, db2, C, lr, 1.0f, nullptr, sg ? gb2 : nullptr, s));
-        LAUNCH("sgd_b1", sgd_update(b1, db1, H, lr, 1.0f, nullptr, sg ? gb1 : nullptr, s));
-        LAUNCH("loss", sum_scale(rowloss, B, a, loss, s));
+        TailArgs ta{};
+        ta.seg[0] = {b2, nullptr, db2, sg ? gb2 : nullptr, C, 1.0f};
+        ta.seg[1] = {b1, nullptr, db1, sg ? gb1 : nullptr, H, 1.0f};
+        ta.nseg = 2; ta.lr = lr; ta.loss_mode = 2; ta.loss_scale = a; ta.rowloss = rowloss; ta.nrow = B; ta.loss_out = loss;
+        LAUNCH("tail", step_tail(ta, s));
         return AH_OK;
     }
 };
@@ -198,7 +201,9 @@ struct Mlp3Trainer : ah_trainer {
         rc |= alloc(&acc, D1 + D2 + D3 + 1); rc |= alloc(&loss, 1);
         rc |= alloc(&gW1, (size_t)D1 * D0); rc |= alloc(&gW2, (size_t)D2 * D1); rc |= alloc(&gW3, (size_t)D3 * D2);
         rc |= alloc(&gb1, D1); rc |= alloc(&gb2, D2); rc |= alloc(&gb3, D3);
-        return rc ? AH_ERR_HIP : AH_OK;
+        if (rc) return AH_ERR_HIP;
+        AH_HIP(hipMemset(acc, 0, sizeof(float) * (D1 + D2 + D3 + 1)));
+        return AH_OK;
     }
     int max_batch() const override { return B; }
     int set(int slot, const void *h, int64_t n) override {
@@ -242,7 +247,6 @@ struct Mlp3Trainer : ah_trainer {
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
         float *db1 = acc, *db2 = acc + D1, *db3 = acc + D1 + D2, *lacc = acc + D1 + D2 + D3;
-        LAUNCH("zero", fill_f32(acc, D1 + D2 + D3 + 1, 0.0f, s));
         GemmDesc g = gdesc(GEMM_F16, EPI_BIAS_RELU, 0, 0, B, D1, D0, X, D0, W1h, D0, H1, D1);
         g.bias = b1h;
         LAUNCH("fc1", gemm_launch(g, s));
@@ -267,10 +271,12 @@ struct Mlp3Trainer : ah_trainer {
         g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D1, D0, B, dZ1, D1, X, D0, nullptr, D0);
         g.scale = bs; g.W32 = W1; g.W16 = W1h; g.lr = lr; g.gout = sg ? gW1 : nullptr;
         LAUNCH("dW1", gemm_launch(g, s));
-        LAUNCH("sgd_b3", sgd_update(b3, db3, D3, lr, bs, b3h, sg ? gb3 : nullptr, s));
-        LAUNCH("sgd_b2", sgd_update(b2, db2, D2, lr, bs, b2h, sg ? gb2 : nullptr, s));
-        LAUNCH("sgd_b1", sgd_update(b1, db1, D1, lr, bs, b1h, sg ? gb1 : nullptr, s));
-        LAUNCH("loss", mse_finalize(lacc, sc, loss, s));
+        TailArgs ta{};
+        ta.seg[0] = {b3, b3h, db3, sg ? gb3 : nullptr, D3, bs};
+        ta.seg[1] = {b2, b2h, db2, sg ? gb2 : nullptr, D2, bs};
+        ta.seg[2] = {b1, b1h, db1, sg ? gb1 : nullptr, D1, bs};
+        ta.nseg = 3; ta.lr = lr; ta.loss_mode = 1; ta.lossacc = lacc; ta.loss_scale = sc; ta.loss_out = loss;
+        LAUNCH("tail", step_tail(ta, s));
         return AH_OK;
     }
 };
@@ -330,7 +336,9 @@ struct ConvNetTrainer : ah_trainer {
         rc |= alloc(&dZ1, (size_t)N * C1 * Hin * Hin); rc |= alloc(&rowloss, N); rc |= alloc(&acc, NC);
         rc |= alloc(&loss, 1); rc |= alloc(&gcw1, (size_t)C1 * 9); rc |= alloc(&gcb1, C1);
         rc |= alloc(&gcw2, (size_t)C2 * C1 * 9); rc |= alloc(&gcb2, C2); rc |= alloc(&gfw, (size_t)NC * F); rc |= alloc(&gfb, NC);
-        return rc ? AH_ERR_HIP : AH_OK;
+        if (rc) return AH_ERR_HIP;
+        AH_HIP(hipMemset(acc, 0, sizeof(float) * NC));
+        return AH_OK;
     }
     struct Slot { void *p; int64_t n; };
     Slot slot_of(int i) {
@@ -355,7 +363,6 @@ struct ConvNetTrainer : ah_trainer {
         hipStream_t s = dev->stream;
         const bool sg = flags & AH_STEP_STORE_GRADS;
         const float a = (float)(-1.0 / (double)B);
-        LAUNCH("zero", fill_f32(acc, NC, 0.0f, s));
         LAUNCH("conv1", conv_fwd_relu_pool(x, B, 1, Hin, cw1, cb1, C1, H1, Pl1, s));
         LAUNCH("conv2", conv_fwd_relu_pool(Pl1, B, C1, P1, cw2, cb2, C2, H2, Pl2, s));
         GemmDesc g = gdesc(GEMM_F32, EPI_BIAS, 0, 0, B, NC, F, Pl2, F, fw, F, lg, NC);
@@ -373,8 +380,10 @@ struct ConvNetTrainer : ah_trainer {
         LAUNCH("conv2_dw", conv_bwd_w_sgd(Pl1, dZ2, B, C1, P1, C2, cw2, cb2, lr, sg ? gcw2 : nullptr, sg ? gcb2 : nullptr, s));
         LAUNCH("pool1_bwd", pool_relu_bwd(dP1, H1, Pl1, B * C1, Hin, dZ1, s));
         LAUNCH("conv1_dw", conv_bwd_w_sgd(x, dZ1, B, 1, Hin, C1, cw1, cb1, lr, sg ? gcw1 : nullptr, sg ? gcb1 : nullptr, s));
-        LAUNCH("sgd_fb", sgd_update(fb, acc, NC, lr, 1.0f, nullptr, sg ? gfb : nullptr, s));
-        LAUNCH("loss", sum_scale(rowloss, B, a, loss, s));
+        TailArgs ta{};
+        ta.seg[0] = {fb, nullptr, acc, sg ? gfb : nullptr, NC, 1.0f};
+        ta.nseg = 1; ta.lr = lr; ta.loss_mode = 2; ta.loss_scale = a; ta.rowloss = rowloss; ta.nrow = B; ta.loss_out = loss;
+        LAUNCH("tail", step_tail(ta, s));
         return AH_OK;
     }
 };

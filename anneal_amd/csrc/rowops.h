@@ -17,6 +17,27 @@ hipError_t softmax_ce(const float *z, const int32_t *labels, int B, int C, float
 hipError_t sum_scale(const float *v, int n, float a, float *out, hipStream_t s);
 hipError_t mse_finalize(const float *acc, float scale, float *out, hipStream_t s);
 
+struct TailSeg {
+    float *p;        // f32 master parameter
+    half_t *p16;     // optional f16 copy
+    float *acc;      // gradient accumulator (re-zeroed)
+    float *gout;     // optional gradient output
+    long n;
+    float scale;     // gradient = scale * acc
+};
+struct TailArgs {
+    TailSeg seg[4];
+    int nseg;
+    float lr;
+    int loss_mode;   // 0 none, 1 f16-narrowed accumulator * loss_scale, 2 sum(rowloss) * loss_scale
+    float *lossacc;
+    float loss_scale;
+    const float *rowloss;
+    int nrow;
+    float *loss_out;
+};
+hipError_t step_tail(const TailArgs &t, hipStream_t s);
+
 long chain_workspace_floats(int R, int Cc);
 hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work, float *dX, float *dg, float *loss,
                       hipStream_t s);

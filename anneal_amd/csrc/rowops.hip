@@ -10,6 +10,8 @@
 // sum e, sum e^2) per column; a per-column finalize folds the row chunks and evaluates the
 // backward's per-row scalars; pass 2 re-reads X and writes dX in the same layout.
 #include <float.h>
+
+#include <algorithm>
 #include "ah_common.h"
 #include "rowops.h"
 
@@ -268,6 +270,53 @@ __global__ __launch_bounds__(256) void chain_loss_kernel(const float *coef, int 
         __syncthreads();
     }
     if (threadIdx.x == 0) out[0] = red[0];
+}
+
+// ── step tail: bias SGD for several parameters + loss finalize, in one launch ─────
+// Each accumulator element is read and re-zeroed by the same thread, leaving the accumulators
+// ready for the next step's atomics (no separate zero-fill launch).
+__global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
+    if (blockIdx.x == 0) {
+        if (t.loss_mode == 1) {
+            if (threadIdx.x == 0) {
+                t.loss_out[0] = q16(t.lossacc[0]) * t.loss_scale;   // f16(acc) narrowing, lower.go:712
+                t.lossacc[0] = 0.0f;
+            }
+        } else if (t.loss_mode == 2) {
+            __shared__ float red[256];
+            float acc = 0.0f;
+            for (int i = threadIdx.x; i < t.nrow; i += 256) acc += t.rowloss[i];
+            red[threadIdx.x] = acc;
+            __syncthreads();
+            for (int o = 128; o > 0; o >>= 1) {
+                if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+                __syncthreads();
+            }
+            if (threadIdx.x == 0) t.loss_out[0] = red[0] * t.loss_scale;
+        }
+    }
+    long total = 0;
+    for (int s = 0; s < t.nseg; s++) total += t.seg[s].n;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+        long k = i;
+        int s = 0;
+        while (k >= t.seg[s].n) { k -= t.seg[s].n; s++; }
+        const TailSeg &g = t.seg[s];
+        const float gv = g.scale * g.acc[k];
+        g.acc[k] = 0.0f;
+        if (g.gout) g.gout[k] = gv;
+        const float w = g.p[k] - t.lr * gv;
+        g.p[k] = w;
+        if (g.p16) g.p16[k] = (half_t)w;
+    }
+}
+
+hipError_t step_tail(const TailArgs &t, hipStream_t s) {
+    long total = 0;
+    for (int i = 0; i < t.nseg; i++) total += t.seg[i].n;
+    int blocks = (int)std::min<long>(std::max<long>((total + 255) / 256, 1), 1024);
+    hipLaunchKernelGGL(tail_kernel, dim3(blocks), dim3(256), 0, s, t);
+    return hipGetLastError();
 }
 
 // ── host launchers ──────────────────────────────────────────────────────────

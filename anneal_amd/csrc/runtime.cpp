@@ -123,6 +123,8 @@ void ah_close(ah_device *d) {
         delete kv.second->tmpl;
         delete kv.second;
     }
+    if (d->t0) hipEventDestroy(d->t0);
+    if (d->t1) hipEventDestroy(d->t1);
     hipStreamDestroy(d->stream);
     delete d;
 }
@@ -273,6 +275,28 @@ int ah_launch(ah_device *d, ah_kernel *k, const uint32_t grid[3], const uint32_t
     for (auto &s : sv) args.push_back(&s);
     AH_HIP(hipModuleLaunchKernel(k->function, grid[0], grid[1], grid[2], block[0], block[1], block[2], 0, d->stream,
                                  args.data(), nullptr));
+    return AH_OK;
+}
+
+// ── timing ──────────────────────────────────────────────────────────────────
+
+int ah_timer_start(ah_device *d) {
+    if (!d) return set_error(AH_ERR_INVALID, "ah_timer_start: null device");
+    if (!d->t0) {
+        AH_HIP(hipEventCreate(&d->t0));
+        AH_HIP(hipEventCreate(&d->t1));
+    }
+    AH_HIP(hipEventRecord(d->t0, d->stream));
+    return AH_OK;
+}
+
+int ah_timer_stop(ah_device *d, double *ms) {
+    if (!d || !ms || !d->t0) return set_error(AH_ERR_INVALID, "ah_timer_stop: timer not started");
+    AH_HIP(hipEventRecord(d->t1, d->stream));
+    AH_HIP(hipEventSynchronize(d->t1));
+    float f = 0.0f;
+    AH_HIP(hipEventElapsedTime(&f, d->t0, d->t1));
+    *ms = f;
     return AH_OK;
 }
 

@@ -34,10 +34,9 @@ def config_workload(cfg: int):
         B, D0, D1, D2, D3 = 4096, 1024, 4096, 4096, 1024
         p = data.mlp3_inputs(B, D0, D1, D2, D3)
         f = lambda m, n, k: ("flop16", 2.0 * m * n * k)  # noqa: E731
-        ks = [("zero", "bytes", 4 * (D1 + D2 + D3 + 1)), ("fc1", *f(B, D1, D0)), ("fc2", *f(B, D2, D1)),
-              ("fc3_mse", *f(B, D3, D2)), ("dH2", *f(B, D2, D3)), ("dW3", *f(D3, D2, B)), ("dH1", *f(B, D1, D2)),
-              ("dW2", *f(D2, D1, B)), ("dW1", *f(D1, D0, B)), ("sgd_b3", "bytes", 16 * D3),
-              ("sgd_b2", "bytes", 16 * D2), ("sgd_b1", "bytes", 16 * D1), ("loss", "bytes", 8)]
+        ks = [("fc1", *f(B, D1, D0)), ("fc2", *f(B, D2, D1)), ("fc3_mse", *f(B, D3, D2)), ("dH2", *f(B, D2, D3)),
+              ("dW3", *f(D3, D2, B)), ("dH1", *f(B, D1, D2)), ("dW2", *f(D2, D1, B)), ("dW1", *f(D1, D0, B)),
+              ("tail", "bytes", 14 * (D1 + D2 + D3))]
         meta = {"workload": "config3_f16_mlp_1024-4096-4096-1024_b4096_mse_sgd", "batch": B,
                 "flop_per_step": sum(a for _, k, a in ks if k.startswith("flop")), "dtype": "f16"}
         return L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], 1e-3, B, p, ks, meta

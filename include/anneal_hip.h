@@ -79,6 +79,10 @@ typedef struct {
     double min_us, median_us, max_us, mean_us, stddev_us, cv;   /* backend/device.go:16-24 */
 } ah_bench_result;
 
+/* Wall time of everything enqueued on the device stream between start and stop (hipEvents). */
+int ah_timer_start(ah_device *dev);
+int ah_timer_stop(ah_device *dev, double *ms);
+
 /* ── 6. graphs (JIT replay) ──────────────────────────────────────────────────
  * Replaces tensor.JIT's replay of captured ExecItems (tensor/jit.go:178-215): everything enqueued on the
  * device stream between begin and end is captured and can be replayed without host scheduling. */
