@@ -308,7 +308,9 @@ struct ChainTrainer : ah_trainer {
         return set_error(AH_ERR_INVALID, "CHAIN: bad get slot %d / size", slot);
     }
     int enqueue(int64_t, int) override {
-        LAUNCH("chain", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream));
+        LAUNCH("chain_stats", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream, 0));
+        LAUNCH("chain_finalize", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream, 1));
+        LAUNCH("chain_grad", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream, 2));
         return AH_OK;
     }
 };

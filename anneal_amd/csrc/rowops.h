@@ -40,6 +40,6 @@ hipError_t step_tail(const TailArgs &t, hipStream_t s);
 
 long chain_workspace_floats(int R, int Cc);
 hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work, float *dX, float *dg, float *loss,
-                      hipStream_t s);
+                      hipStream_t s, int phase = -1);
 
 }  // namespace ah

@@ -127,6 +127,11 @@ __global__ void mse_finalize_kernel(const float *acc, float scale, float *out) {
 
 // ── config 5: movement + row-reduce chain ───────────────────────────────────
 
+// exp2 of a non-positive argument as the bare v_exp_f32: results below 2^-126 flush to zero (they are
+// below f32's normal range and change no sum they enter; exp2f's denormal fix-up costs ~5 VALU ops
+// per element, which is most of these streaming kernels' per-element work).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 struct ColStat {
     float m, t, s, q;
 };
@@ -159,7 +164,8 @@ __device__ __forceinline__ ColStat stat_merge(const ColStat &a, const ColStat &b
 }
 
 // Pass 1. Block = 4 waves over the same 256 columns (lane owns 4 consecutive columns);
-// blockIdx.y selects a chunk of `rch` rows, waves interleave rows within it.
+// blockIdx.y selects a chunk of `rch` rows, waves interleave rows within it. Each wave issues 8 row
+// loads (8 KiB) before consuming any, so enough bytes are in flight to cover HBM latency.
 __global__ __launch_bounds__(256) void chain_stats_kernel(const float *X, int R, int Cc, int rch, ColStat *part) {
     __shared__ ColStat sh[4][256];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -170,13 +176,32 @@ __global__ __launch_bounds__(256) void chain_stats_kernel(const float *X, int R,
     for (int u = 0; u < 4; u++) st[u] = ColStat{-FLT_MAX, 0.0f, 0.0f, 0.0f};
     if (c0 < Cc) {
         int r = r0 + wave;
-        for (; r + 12 < r1; r += 16) {
-            floatx4 v0 = *(const floatx4 *)(X + (long)r * Cc + c0);
-            floatx4 v1 = *(const floatx4 *)(X + (long)(r + 4) * Cc + c0);
-            floatx4 v2 = *(const floatx4 *)(X + (long)(r + 8) * Cc + c0);
-            floatx4 v3 = *(const floatx4 *)(X + (long)(r + 12) * Cc + c0);
+        for (; r + 28 < r1; r += 32) {
+            floatx4 v[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++) { stat_push(st[u], v0[u]); stat_push(st[u], v1[u]); stat_push(st[u], v2[u]); stat_push(st[u], v3[u]); }
+            for (int j = 0; j < 8; j++) v[j] = *(const floatx4 *)(X + (long)(r + 4 * j) * Cc + c0);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                // Rescale once per 8 rows to the batch max, then accumulate without branches
+                // (the element equal to the new max contributes exp2(0) = 1 exactly, as in stat_push).
+                float mb = v[0][u];
+#pragma unroll
+                for (int j = 1; j < 8; j++) mb = fmaxf(mb, v[j][u]);
+                if (mb > st[u].m) {
+                    const float f = exp2f((st[u].m - mb) * AH_INV_LN2);
+                    st[u].s *= f;
+                    st[u].q *= f * f;
+                    st[u].t = 0.0f;
+                    st[u].m = mb;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float e = fast_exp2((v[j][u] - st[u].m) * AH_INV_LN2);
+                    st[u].s += e;
+                    st[u].q += e * e;
+                    st[u].t += (v[j][u] == st[u].m) ? 1.0f : 0.0f;
+                }
+            }
         }
         for (; r < r1; r += 4) {
             floatx4 v = *(const floatx4 *)(X + (long)r * Cc + c0);
@@ -195,41 +220,73 @@ __global__ __launch_bounds__(256) void chain_stats_kernel(const float *X, int R,
     }
 }
 
-// Per-column finalize: fold chunk partials, then the reference backward's per-row scalars.
-// coef[col] = {m, rs, g*r, gsq, gs, share, dg, loss_row}
+// Per-column finalize: fold the chunk partials, then the reference backward's per-row scalars.
+// Block = 32 columns x 8 partial groups: group p folds partials p, p+8, ... (coalesced 512-byte rows),
+// the 8 group results are merged in a fixed order (deterministic), then one thread per column
+// evaluates the scalars. coef[col] = {m, rs, g*r, gsq, gs, share, dg, loss_row}; lossp[block] is the
+// block's sum of loss_row (summed by the gradient pass).
+constexpr int kFinCols = 32;
 __global__ __launch_bounds__(256) void chain_finalize_kernel(const ColStat *part, int nchunks, int R, int Cc,
-                                                              const float *g, float *coef, float *dg) {
-    int col = blockIdx.x * 256 + threadIdx.x;
-    if (col >= Cc) return;
-    ColStat a = part[col];
-    for (int k = 1; k < nchunks; k++) a = stat_merge(a, part[(long)k * Cc + col]);
-    const float eps = 1e-6f;
-    const float rR = 1.0f / (float)R;
-    float rs = 1.0f / a.s;
-    float sumS = a.s * rs;             // Sum_j e_j * rs
-    float sq = a.q * (rs * rs);        // Sum_j (e_j * rs)^2
-    float q = sq * rR;
-    float T = sqrtf(q + eps);
-    float r = 1.0f / T;
-    float gi = g[col];
-    float gR = gi * sumS;
-    float gT = ((-gR) * r) * r;
-    float gu = gT * (1.0f / (2.0f * T));
-    float gsq = gu * rR;
-    float gRs = (gi * r) * a.s + 2.0f * gsq * (rs * a.q);
-    float gs = ((-gRs) * rs) * rs;
-    float gm = -(AH_LN2 * AH_INV_LN2) * (rs * gRs + gs * a.s);
-    float share = gm * (1.0f / a.t);
-    float *cf = coef + (long)col * 8;
-    cf[0] = a.m; cf[1] = rs; cf[2] = gi * r; cf[3] = gsq;
-    cf[4] = gs; cf[5] = share; cf[6] = r * sumS; cf[7] = gi * (r * sumS);
-    dg[col] = r * sumS;
+                                                              const float *g, float *coef, float *dg, float *lossp) {
+    __shared__ ColStat sh[8][kFinCols];
+    __shared__ float lsum[kFinCols];
+    const int cl = threadIdx.x % kFinCols, grp = threadIdx.x / kFinCols;
+    const int col = blockIdx.x * kFinCols + cl;
+    ColStat a{-FLT_MAX, 0.0f, 0.0f, 0.0f};
+    if (col < Cc)
+        for (int k = grp; k < nchunks; k += 8) a = stat_merge(a, part[(long)k * Cc + col]);
+    sh[grp][cl] = a;
+    __syncthreads();
+    if (grp == 0) {
+        float lrow = 0.0f;
+        if (col < Cc) {
+#pragma unroll
+            for (int k = 1; k < 8; k++) a = stat_merge(a, sh[k][cl]);
+            const float eps = 1e-6f;
+            const float rR = 1.0f / (float)R;
+            float rs = 1.0f / a.s;
+            float sumS = a.s * rs;             // Sum_j e_j * rs
+            float sq = a.q * (rs * rs);        // Sum_j (e_j * rs)^2
+            float q = sq * rR;
+            float T = sqrtf(q + eps);
+            float r = 1.0f / T;
+            float gi = g[col];
+            float gR = gi * sumS;
+            float gT = ((-gR) * r) * r;
+            float gu = gT * (1.0f / (2.0f * T));
+            float gsq = gu * rR;
+            float gRs = (gi * r) * a.s + 2.0f * gsq * (rs * a.q);
+            float gs = ((-gRs) * rs) * rs;
+            float gm = -(AH_LN2 * AH_INV_LN2) * (rs * gRs + gs * a.s);
+            float share = gm * (1.0f / a.t);
+            float *cf = coef + (long)col * 8;
+            lrow = gi * (r * sumS);
+            *(floatx4 *)cf = floatx4{a.m, rs, gi * r, gsq};
+            *(floatx4 *)(cf + 4) = floatx4{gs, share, r * sumS, lrow};
+            dg[col] = r * sumS;
+        }
+        lsum[cl] = lrow;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float acc = 0.0f;
+        for (int k = 0; k < kFinCols; k++) acc += lsum[k];
+        lossp[blockIdx.x] = acc;
+    }
 }
 
-// Pass 2: dX[j, i] from X[j, i] and the per-column scalars.
+// Pass 2: dX[j, i] from X[j, i] and the per-column scalars; each wave loads its 4 rows before
+// computing. Block (0, 0) also sums the finalize blocks' loss partials in a fixed order.
 __global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, int Cc, int rch, const float *coef,
-                                                          float *dX) {
+                                                          float *dX, const float *lossp, int nlossp, float *loss) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+        float acc = 0.0f;
+        for (int i = lane; i < nlossp; i += 64) acc += lossp[i];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+        if (lane == 0) loss[0] = acc;
+    }
     const int c0 = blockIdx.x * 256 + lane * 4;
     if (c0 >= Cc) return;
     float m[4], rs[4], gr[4], gsq[4], gs[4], sh[4];
@@ -240,36 +297,29 @@ __global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, 
         m[u] = a[0]; rs[u] = a[1]; gr[u] = a[2]; gsq[u] = a[3]; gs[u] = b[0]; sh[u] = b[1];
     }
     const int r0 = blockIdx.y * rch, r1 = min(R, r0 + rch);
-    for (int r = r0 + wave; r < r1; r += 4) {
-        floatx4 v = *(const floatx4 *)(X + (long)r * Cc + c0);
-        floatx4 o;
+    for (int rb = r0 + wave; rb < r1; rb += 16) {
+        floatx4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            float y = v[u];
-            float e = exp2f((y - m[u]) * AH_INV_LN2);
-            float S = e * rs[u];
-            float t2 = gsq[u] * S;
-            float gS = (gr[u] + t2) + t2;
-            float ge = gS * rs[u] + gs[u];
-            float gzs = ((ge * e) * AH_LN2) * AH_INV_LN2;
-            o[u] = gzs + ((y == m[u]) ? sh[u] : 0.0f);
+        for (int j = 0; j < 4; j++)
+            if (rb + 4 * j < r1) v[j] = __builtin_nontemporal_load((const floatx4 *)(X + (long)(rb + 4 * j) * Cc + c0));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (rb + 4 * j >= r1) break;
+            floatx4 o;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float y = v[j][u];
+                float e = fast_exp2((y - m[u]) * AH_INV_LN2);
+                float S = e * rs[u];
+                float t2 = gsq[u] * S;
+                float gS = (gr[u] + t2) + t2;
+                float ge = gS * rs[u] + gs[u];
+                float gzs = ((ge * e) * AH_LN2) * AH_INV_LN2;
+                o[u] = gzs + ((y == m[u]) ? sh[u] : 0.0f);
+            }
+            __builtin_nontemporal_store(o, (floatx4 *)(dX + (long)(rb + 4 * j) * Cc + c0));
         }
-        __builtin_nontemporal_store(o, (floatx4 *)(dX + (long)r * Cc + c0));
     }
-}
-
-// loss = Sum_i coef[i].loss_row
-__global__ __launch_bounds__(256) void chain_loss_kernel(const float *coef, int Cc, float *out) {
-    __shared__ float red[256];
-    float acc = 0.0f;
-    for (int i = threadIdx.x; i < Cc; i += 256) acc += coef[(long)i * 8 + 7];
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) out[0] = red[0];
 }
 
 // ── step tail: bias SGD for several parameters + loss finalize, in one launch ─────
@@ -366,22 +416,26 @@ hipError_t mse_finalize(const float *acc, float scale, float *out, hipStream_t s
 
 long chain_workspace_floats(int R, int Cc) {
     int nch = (R + kChainStatsRows - 1) / kChainStatsRows;
-    return (long)nch * Cc * 4 + (long)Cc * 8;
+    return (long)nch * Cc * 4 + (long)Cc * 8 + (Cc + kFinCols - 1) / kFinCols;
 }
 
 hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work, float *dX, float *dg, float *loss,
-                      hipStream_t s) {
+                      hipStream_t s, int phase) {
     if (Cc % 4 != 0 || R <= 0) return hipErrorInvalidValue;
-    int nch = (R + kChainStatsRows - 1) / kChainStatsRows;
+    const int nch = (R + kChainStatsRows - 1) / kChainStatsRows;
+    const int nfin = (Cc + kFinCols - 1) / kFinCols;
     ColStat *part = (ColStat *)work;
     float *coef = work + (long)nch * Cc * 4;
-    dim3 g1((Cc + 255) / 256, nch);
-    hipLaunchKernelGGL(chain_stats_kernel, g1, dim3(256), 0, s, X, R, Cc, kChainStatsRows, part);
-    hipLaunchKernelGGL(chain_finalize_kernel, dim3((Cc + 255) / 256), dim3(256), 0, s, part, nch, R, Cc, g, coef, dg);
-    int nch2 = (R + kChainGradRows - 1) / kChainGradRows;
-    dim3 g2((Cc + 255) / 256, nch2);
-    hipLaunchKernelGGL(chain_grad_kernel, g2, dim3(256), 0, s, X, R, Cc, kChainGradRows, coef, dX);
-    hipLaunchKernelGGL(chain_loss_kernel, dim3(1), dim3(256), 0, s, coef, Cc, loss);
+    float *lossp = coef + (long)Cc * 8;
+    if (phase < 0 || phase == 0)
+        hipLaunchKernelGGL(chain_stats_kernel, dim3((Cc + 255) / 256, nch), dim3(256), 0, s, X, R, Cc, kChainStatsRows, part);
+    if (phase < 0 || phase == 1)
+        hipLaunchKernelGGL(chain_finalize_kernel, dim3(nfin), dim3(256), 0, s, part, nch, R, Cc, g, coef, dg, lossp);
+    if (phase < 0 || phase == 2) {
+        int nch2 = (R + kChainGradRows - 1) / kChainGradRows;
+        hipLaunchKernelGGL(chain_grad_kernel, dim3((Cc + 255) / 256, nch2), dim3(256), 0, s, X, R, Cc, kChainGradRows,
+                           coef, dX, lossp, nfin, loss);
+    }
     return hipGetLastError();
 }
 

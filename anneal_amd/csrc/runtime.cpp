@@ -234,8 +234,10 @@ int ah_module_get(ah_device *d, const char *source, const char *entry, ah_kernel
             return set_error(AH_ERR_COMPILE, "hiprtcCreateProgram failed");
         }
         std::string arch = "--offload-arch=" + d->arch.substr(0, d->arch.find(':'));
-        const char *opts[] = {arch.c_str(), "-O3", "-std=c++17"};
-        hiprtcResult rc = hiprtcCompileProgram(prog, 3, opts);
+        // No packed FP32 VALU ops in generated code either (same flag as the library build).
+        const char *opts[] = {arch.c_str(), "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+                              "-packed-fp32-ops"};
+        hiprtcResult rc = hiprtcCompileProgram(prog, 7, opts);
         if (rc != HIPRTC_SUCCESS) {
             size_t ls = 0;
             hiprtcGetProgramLogSize(prog, &ls);

@@ -1,0 +1,58 @@
+"""Blocked numpy restatement of ora_mlp3_f16_step (oracle/anneal_oracle.c) for full config-3 sizes.
+
+TEST INFRASTRUCTURE ONLY. The C oracle's serial loops need about a minute for one full config-3 step
+(584 GFLOP); this restatement keeps the oracle's f16 rounding points (f16 leaves, f16(f16(acc)+b)
+narrowing, f16 loss accumulator, f16 Sub before the MSE gradient) and differs only in f32 summation
+order (BLAS sgemm instead of the serial k-loop). test_oracle_np_matches_c_oracle pins it to the C
+oracle at small sizes; full-size GPU parity uses it at the config-3 tolerance (2e-2).
+"""
+import numpy as np
+
+
+def q16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def mlp3_step_np(p: dict, lr: float):
+    """Same contract as oracle_lib.mlp3_step: x, t f16-representable; returns (loss, grads, new params)."""
+    x, t = np.asarray(p["x"], np.float32), np.asarray(p["t"], np.float32)
+    prm = {k: np.asarray(p[k], np.float32).copy() for k in ("W1", "b1", "W2", "b2", "W3", "b3")}
+    w1, w2, w3 = q16(prm["W1"]), q16(prm["W2"]), q16(prm["W3"])
+    c1, c2, c3 = q16(prm["b1"]), q16(prm["b2"]), q16(prm["b3"])
+    B, D3 = x.shape[0], w3.shape[0]
+    Z1 = q16(q16(x @ w1.T) + c1)
+    H1 = np.maximum(Z1, 0)
+    Z2 = q16(q16(H1 @ w2.T) + c2)
+    H2 = np.maximum(Z2, 0)
+    P = q16(q16(H2 @ w3.T) + c3)
+    scale = np.float32(1.0 / (float(B) * float(D3)))
+    d32 = P - t
+    acc = np.float32(np.sum(d32.astype(np.float64) ** 2))
+    loss = float(q16(acc) * scale)
+    d = q16(d32)
+    gP = scale * d + scale * d
+    g = {}
+    g["db3"] = gP.sum(0, dtype=np.float64).astype(np.float32)
+    g["dW3"] = gP.T @ H2
+    dH2 = np.where(Z2 == H2, gP @ w3, np.float32(0))
+    g["db2"] = dH2.sum(0, dtype=np.float64).astype(np.float32)
+    g["dW2"] = dH2.T @ H1
+    dH1 = np.where(Z1 == H1, dH2 @ w2, np.float32(0))
+    g["db1"] = dH1.sum(0, dtype=np.float64).astype(np.float32)
+    g["dW1"] = dH1.T @ x
+    new = {k: (v - np.float32(lr) * g["d" + k]).astype(np.float32) for k, v in prm.items()}
+    return loss, g, new
+
+
+def chain_dX_f64(X, g):
+    """Closed-form f64 gradient of Sum(S * recip(sqrt(mean(S^2)+1e-6)) * g) w.r.t. X (S = softmax over
+    X's columns). In exact arithmetic the row-max path contributes nothing (softmax is shift
+    invariant); in f32 its tie share is a rounding residue, so column-max elements are judged here."""
+    R = X.shape[0]
+    Y = X.astype(np.float64).T
+    e = np.exp(Y - Y.max(1, keepdims=True))
+    S = e / e.sum(1, keepdims=True)
+    r = 1.0 / np.sqrt((S * S).mean(1, keepdims=True) + 1e-6)
+    G = np.asarray(g, np.float64)[:, None]
+    dS = G * r - G * S.sum(1, keepdims=True) * r ** 3 * S / R
+    return (S * (dS - (S * dS).sum(1, keepdims=True))).T

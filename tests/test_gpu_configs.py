@@ -136,3 +136,49 @@ def test_config3_f16_mlp_step_vs_oracle(dev, shape):
         assert O.relerr(out[k], g[k].ravel()) < 2e-2, k
     for k in ("W1", "b1", "W2", "b2", "W3", "b3"):
         assert check_update(out[k], p[k], new[k], 2e-2), k
+
+
+def test_config3_full_size_vs_numpy_restatement(dev):
+    """Full config-3 shape (4096x1024 -> 4096 -> 4096 -> 1024): one step vs the blocked numpy
+    restatement of the oracle (pinned to the C oracle on CPU). The f16 loss accumulator overflows at
+    this size in the reference semantics (loss = +Inf), so gradients and updates carry the check."""
+    import warnings
+    from oracle_np import mlp3_step_np
+    p = data.mlp3_inputs()
+    q = dict(p)
+    q["x"], q["t"] = data.f16_quantize(p["x"]), data.f16_quantize(p["t"])
+    lr = 1e-3
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", RuntimeWarning)
+        wl, g, new = mlp3_step_np(q, lr)
+    out = run_mlp3(dev, p, lr)
+    assert (np.isinf(out["loss"]) and np.isinf(wl)) or abs(out["loss"] - wl) < 2e-2 * abs(wl)
+    for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3"):
+        assert O.relerr(out[k], g[k].ravel()) < 2e-2, k
+    for k in ("W1", "b1", "W2", "b2", "W3", "b3"):
+        assert check_update(out[k], p[k], new[k], 2e-2), k
+
+
+def test_config5_full_size_trainer_vs_oracle(dev):
+    """Config 5 at its full shape X[8192,4096] through the device-resident trainer (the bench path),
+    twice in a row (the second step reuses every workspace), vs the oracle."""
+    R, Cc = 8192, 4096
+    p = data.chain_inputs(R, Cc)
+    wl, wdX, wdg = O.chain_step(p["X"], p["g"])
+    from oracle_np import chain_dX_f64
+    exact = chain_dX_f64(p["X"], p["g"])
+    mask = np.zeros((R, Cc), bool)
+    mask[p["X"].argmax(0), np.arange(Cc)] = True
+    den = np.max(np.abs(wdX))
+    ora_err = np.max(np.abs(wdX - exact)[mask]) / den
+    t = Trainer(dev, L.TRAIN_CHAIN, [R, Cc], 0.0)
+    t.set("X", p["X"])
+    t.set("g", p["g"])
+    for _ in range(2):
+        t.step(R, store_grads=True)
+        assert abs(t.get("loss", 1)[0] - wl) <= 1e-4 * abs(wl)
+        got = t.get("dX", R * Cc).reshape(R, Cc)
+        assert np.max(np.abs(got - wdX)[~mask]) / den < 1e-4
+        assert np.max(np.abs(got - exact)[mask]) / den <= ora_err + 1e-4
+        assert O.relerr(t.get("dg", Cc), wdg) < 1e-5
+    t.close()
