@@ -55,7 +55,7 @@ class ah_gemm_desc(C.Structure):
                 ("C", C.c_void_p), ("ldc", C.c_int64), ("bias", C.c_void_p), ("aux", C.c_void_p),
                 ("ldaux", C.c_int64), ("scale", C.c_float), ("colsum", C.c_void_p), ("W32", C.c_void_p),
                 ("W16", C.c_void_p), ("lr", C.c_float), ("gout", C.c_void_p), ("lossacc", C.c_void_p),
-                ("tile", C.c_int32)]
+                ("tile", C.c_int32), ("variant", C.c_int32)]
 
 
 # name -> (restype, argtypes)
@@ -91,6 +91,7 @@ SIGNATURES = {
     "ah_benchmark": (C.c_int, [_P, C.POINTER(ah_exec_item), C.c_int32, C.c_int32, C.POINTER(ah_bench_result)]),
     "ah_outputs_free": (None, [C.POINTER(ah_output), C.c_int32]),
     "ah_gemm": (C.c_int, [_P, C.POINTER(ah_gemm_desc)]),
+    "ah_gemm_tune": (C.c_int, [_P, C.POINTER(ah_gemm_desc), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
     "ah_softmax_ce": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P]),
     "ah_chain_step": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P]),
     "ah_trainer_create": (C.c_int, [_P, C.c_int32, C.POINTER(C.c_int64), C.c_int32, C.c_float, C.POINTER(_P)]),

@@ -78,14 +78,26 @@ class Device:
         L.check(self.lib.ah_timer_stop(self.h, C.byref(ms)))
         return ms.value
 
-    def gemm(self, *, dtype, epi, ta, tb, M, N, K, A, B, lda, ldb, C_out=None, ldc=0, bias=None, aux=None,
-             ldaux=0, scale=1.0, colsum=None, W32=None, W16=None, lr=0.0, gout=None, lossacc=None, tile=0):
+    @staticmethod
+    def _gemm_desc(dtype, epi, ta, tb, M, N, K, A, B, lda, ldb, C_out=None, ldc=0, bias=None, aux=None, ldaux=0,
+                   scale=1.0, colsum=None, W32=None, W16=None, lr=0.0, gout=None, lossacc=None, tile=0, variant=0):
         p = lambda b: None if b is None else b.ptr  # noqa: E731
-        d = L.ah_gemm_desc(dtype=dtype, epi=epi, ta=ta, tb=tb, M=M, N=N, K=K, A=p(A), B=p(B), lda=lda, ldb=ldb,
-                           C=p(C_out), ldc=ldc, bias=p(bias), aux=p(aux), ldaux=ldaux, scale=scale,
-                           colsum=p(colsum), W32=p(W32), W16=p(W16), lr=lr, gout=p(gout), lossacc=p(lossacc),
-                           tile=tile)
+        return L.ah_gemm_desc(dtype=dtype, epi=epi, ta=ta, tb=tb, M=M, N=N, K=K, A=p(A), B=p(B), lda=lda, ldb=ldb,
+                              C=p(C_out), ldc=ldc, bias=p(bias), aux=p(aux), ldaux=ldaux, scale=scale,
+                              colsum=p(colsum), W32=p(W32), W16=p(W16), lr=lr, gout=p(gout), lossacc=p(lossacc),
+                              tile=tile, variant=variant)
+
+    def gemm(self, **kw):
+        """One contraction with a fused epilogue (keyword arguments mirror ah_gemm_desc)."""
+        d = self._gemm_desc(**kw)
         L.check(self.lib.ah_gemm(self.h, C.byref(d)))
+
+    def gemm_tune(self, iterations: int = 3, **kw):
+        """Times every f16 variant of the contraction and caches the fastest; returns (variant, mean us)."""
+        d = self._gemm_desc(**kw)
+        v, us = C.c_int32(), C.c_double()
+        L.check(self.lib.ah_gemm_tune(self.h, C.byref(d), iterations, C.byref(v), C.byref(us)))
+        return v.value, us.value
 
     def softmax_ce(self, z: DeviceBuffer, labels: DeviceBuffer, B: int, Cn: int, dz: DeviceBuffer,
                    loss: DeviceBuffer) -> None:

@@ -45,6 +45,9 @@ struct ah_device {
     std::unordered_map<std::string, ah_kernel *> modules;
     std::string arch;
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    // f16 GEMM variant chosen by ah_gemm_tune per (ta, tb, M, N, K); used when a launch asks for
+    // variant 0 (the role of BEAM's cache, codegen/beam.go:118-169).
+    std::unordered_map<std::string, int> gemm_variant;
 };
 
 struct ah_graph {

@@ -35,7 +35,7 @@ static std::unordered_map<std::string, std::string> parse_params(const std::stri
     return out;
 }
 
-// "tmpl:gemm;dtype=f16;epi=bias_relu;ta=0;tb=0;M=4096;N=4096;K=1024"
+// "tmpl:gemm;dtype=f16;epi=bias_relu;ta=0;tb=0;M=4096;N=4096;K=1024[;variant=3]"
 // PARAM order: data0 = C, data1 = A, data2 = B, data3 = bias (bias epilogues) or aux (mask).
 // M may be "sym": it is then taken from the first symbolic scalar (the bound batch size).
 int template_create(const std::string &source, TemplateKernel **out) {
@@ -64,6 +64,8 @@ int template_create(const std::string &source, TemplateKernel **out) {
         base.N = (int)geti("N", -1);
         base.K = (int)geti("K", -1);
         base.scale = 1.0f;
+        base.variant = (int)geti("variant", 0);
+        if (base.variant < 0 || base.variant > 9) return set_error(AH_ERR_INVALID, "tmpl gemm: variant %d", base.variant);
         if ((!msym && base.M < 0) || base.N <= 0 || base.K < 0) return set_error(AH_ERR_INVALID, "tmpl gemm: M/N/K required");
         auto *t = new TemplateKernel();
         t->key = source;

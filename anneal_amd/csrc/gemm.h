@@ -45,11 +45,10 @@ struct GemmDesc {
     float *gout;      // EPI_SGD gradient output [M,N] (row stride ldc), optional
     float *lossacc;   // EPI_MSE scalar accumulator
     int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
+    int variant;      // f16 kernel variant (0 = auto; see gemm16.hip launch_tile), the tuning hook
 };
 
-#ifdef __HIP_PLATFORM_AMD__
 hipError_t gemm_launch(const GemmDesc &d, hipStream_t s);
 bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err);
-#endif
 
 }  // namespace ah

@@ -25,8 +25,6 @@ typedef half_t h8 __attribute__((ext_vector_type(8)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s4 lds_s4;
 
-constexpr int kThreads = 256;
-
 // Byte offset of (row r, 16-byte chunk c) in a K-contiguous tile whose rows hold BK halves:
 // 256-byte super-rows of 256/(2*BK) rows, 16-byte slots XOR-swizzled by the super-row index.
 template <int BK>
@@ -42,11 +40,32 @@ __device__ __forceinline__ int mnoff(int k, int m) {
     return k * (R * 2) + (((m >> 4) ^ ((k & 3) << 1)) << 5) + ((m & 15) << 1);
 }
 
+// One 16-byte-per-lane global->LDS DMA issued from inline asm: the compiler's wait-count model does
+// not see it, so it adds no conservative waits (an LDS-DMA the compiler knows about makes it wait
+// for every outstanding LDS read at the next use of any of them). The kernel orders these loads
+// with its own explicit s_waitcnt vmcnt.
+__device__ __forceinline__ void dma16(const char *g, const char *lds) {
+    const uint32_t l = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(l))
+                 : "memory", "m0");
+}
+
+// L2 prefetch of one 128-byte line: a 4-byte-per-lane LDS-DMA into a junk LDS slot that nothing
+// reads (a load into a VGPR would need that register reserved against the load's late write-back).
+__device__ __forceinline__ void prefetch_line(const char *g, const char *junk) {
+    const uint32_t l = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)junk;
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(l))
+                 : "memory", "m0");
+}
+
 // Per-lane global byte offsets for the 1 KiB blocks this wave fetches (stage-independent part).
-template <int R, int T, int BK>
+template <int R, int T, int BK, int NW>
 struct Fetch {
     static constexpr int NB = R * BK * 2 / 1024;   // 1 KiB blocks per tile
-    static constexpr int PER = NB / 4;             // blocks per wave
+    static constexpr int PER = NB / NW;            // blocks per wave
+    static_assert(PER * NW == NB, "tile blocks must split evenly over the waves");
     uint32_t off[PER];
     __device__ __forceinline__ void init(long ld, int r0, int rmax, int wave, int lane) {
 #pragma unroll
@@ -78,7 +97,28 @@ struct Fetch {
         __builtin_amdgcn_global_load_lds((const void *)(base + adv + off[j]), (void *)(tile + (wave * PER + j) * 1024),
                                          16, 0, 0);
     }
+    __device__ __forceinline__ void issue_asm(const char *base, long ld, int k0, char *tile, int wave) const {
+        const long adv = T == 0 ? (long)k0 * 2 : (long)k0 * ld * 2;
+#pragma unroll
+        for (int j = 0; j < PER; j++) dma16(base + adv + off[j], tile + (wave * PER + j) * 1024);
+    }
 };
+
+// L2 prefetch of one operand's stage (k = k0 .. k0+63): the stage is R lines of 128 bytes (a
+// K-contiguous row holds 64 halves = one line; an MN-contiguous k-row of R halves holds R/64 lines).
+// Line i of the stage is touched by thread i (callers pass i < R, ragged rows clamped).
+template <int R, int T>
+__device__ __forceinline__ void prefetch_stage(const char *base, long ld, int r0, int rmax, int k0, int i,
+                                               const char *junk) {
+    if constexpr (T == 0) {
+        const int row = min(r0 + i, rmax - 1);
+        prefetch_line(base + ((long)row * ld + k0) * 2, junk);
+    } else {
+        constexpr int LPR = R / 64;
+        const int col = min(r0 + (i % LPR) * 64, rmax - 1);
+        prefetch_line(base + ((long)(k0 + i / LPR) * ld + col) * 2, junk);
+    }
+}
 
 template <int R, int T, int BK>
 __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
@@ -99,14 +139,26 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
 // VEPI: every wave tile is in bounds and the epilogue arrays admit vector access, so the LDS-staged
 // vector epilogue is used (chosen on the host; a kernel holding both epilogues spills registers).
 // BK: k per LDS stage (32 or 64); NS: LDS stages in flight (the fetch of stage k+NS-1 is issued
-// while stage k is contracted).
-template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS>
-__global__ __launch_bounds__(kThreads) void gemm16_kernel(GemmDesc d) {
-    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+// while stage k is contracted). WVM x WVN waves share the tile: with 2x2 each wave holds a 128x128
+// accumulator (one wave per SIMD); with 4x2 on a 256x256 tile each wave holds 64x128 and two waves
+// share a SIMD, so one wave's MFMAs cover the other's LDS reads and barrier waits.
+// FETCH: where a stage's global->LDS fetches are issued. 0: as one group after the first k-step's
+// fragment reads; 1: spread between the MFMAs; 2: as one group right after the stage barrier, before
+// any fragment read. (An LDS-DMA issue makes the compiler wait for every outstanding LDS read at the
+// next MFMA, so with 0 and 1 the fragment reads of k-step s+1 are waited on before the MFMAs of s.)
+// 3: like 2, but the DMAs are issued from inline asm (no compiler-inserted waits) and every thread
+// also prefetches one line of stage kt+NS into L2, so the DMA of that stage one iteration later hits
+// L2 instead of waiting on the Infinity Cache or HBM. Needs k=64 stages and 2*BM threads.
+template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH>
+__global__ __launch_bounds__(64 * WVM * WVN) void gemm16_kernel(GemmDesc d) {
+    constexpr int NW = WVM * WVN;
+    constexpr int WM = BM / WVM, WN = BN / WVN, FM = WM / 32, FN = WN / 32;
     constexpr int ABYTES = BM * BK * 2, BBYTES = BN * BK * 2, STAGE = ABYTES + BBYTES;
     constexpr int KS = BK / 16;                                           // MFMA k-steps per stage
-    constexpr int PERSTAGE = Fetch<BM, TA, BK>::PER + Fetch<BN, TB, BK>::PER;
-    constexpr int SMEM = (NS * STAGE > 4 * WM * 256) ? NS * STAGE : 4 * WM * 256;
+    constexpr int PERSTAGE = Fetch<BM, TA, BK, NW>::PER + Fetch<BN, TB, BK, NW>::PER;
+    constexpr int SMEM0 = (NS * STAGE > NW * WM * 256) ? NS * STAGE : NW * WM * 256;
+    constexpr int SMEM = FETCH == 3 ? SMEM0 + NW * 256 : SMEM0;       // + per-wave prefetch junk slots
+    static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
     __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
     const int tiles_n = (d.N + BN - 1) / BN;
@@ -122,10 +174,10 @@ __global__ __launch_bounds__(kThreads) void gemm16_kernel(GemmDesc d) {
     const int m0 = (gm0 + rem % gsz) * BM, n0 = (rem / gsz) * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    const int wm0 = (wave / WVN) * WM, wn0 = (wave % WVN) * WN;
 
-    Fetch<BM, TA, BK> fa;
-    Fetch<BN, TB, BK> fb;
+    Fetch<BM, TA, BK, NW> fa;
+    Fetch<BN, TB, BK, NW> fb;
     fa.init(d.lda, m0, d.M, wave, lane);
     fb.init(d.ldb, n0, d.N, wave, lane);
     const char *Ab = (const char *)d.A, *Bb = (const char *)d.B;
@@ -137,16 +189,34 @@ __global__ __launch_bounds__(kThreads) void gemm16_kernel(GemmDesc d) {
         for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
 
     const int nk = d.K / BK;
+    static_assert(FETCH != 3 || (BK == 64 && 64 * NW == 2 * BM && BM == BN), "prefetch mapping: one line per thread");
+    const char *junk = smem + SMEM0 + wave * 256;
+    // prefetch: the first half of the waves covers A's stage lines, the second half B's. The branch
+    // is on a scalar (wave-uniform) value, so each wave issues exactly one prefetch load per stage,
+    // which the vmcnt accounting of the loop relies on.
+    const bool pf_a = __builtin_amdgcn_readfirstlane(wave) < NW / 2;
+    auto prefetch = [&](int k0) {
+        if (pf_a) prefetch_stage<BM, TA>(Ab, d.lda, m0, d.M, k0, tid, junk);
+        else prefetch_stage<BN, TB>(Bb, d.ldb, n0, d.N, k0, tid - BM, junk);
+    };
 #pragma unroll
     for (int p = 0; p < NS - 1; p++) {
         const int kp = min(p, nk - 1) * BK;
-        fa.issue(Ab, d.lda, kp, smem + p * STAGE, wave);
-        fb.issue(Bb, d.ldb, kp, smem + p * STAGE + ABYTES, wave);
+        if constexpr (FETCH == 3) {
+            fa.issue_asm(Ab, d.lda, kp, smem + p * STAGE, wave);
+            fb.issue_asm(Bb, d.ldb, kp, smem + p * STAGE + ABYTES, wave);
+        } else {
+            fa.issue(Ab, d.lda, kp, smem + p * STAGE, wave);
+            fb.issue(Bb, d.ldb, kp, smem + p * STAGE + ABYTES, wave);
+        }
     }
+    if constexpr (FETCH == 3) prefetch(min(NS - 1, nk - 1) * BK);
     for (int kt = 0; kt < nk; kt++) {
-        // stage kt has landed once at most the NS-2 younger stages are still in flight
+        // stage kt has landed once at most the NS-2 younger stages (and, with prefetching, the one
+        // younger prefetch line) are still in flight
 #ifndef AH_EXP_NOBARRIER
-        asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE) : "memory");
+        if constexpr (FETCH == 3) asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE + 1) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE) : "memory");
         __syncthreads();
 #endif
         const char *sa = smem + (kt % NS) * STAGE, *sb = sa + ABYTES;
@@ -154,6 +224,18 @@ __global__ __launch_bounds__(kThreads) void gemm16_kernel(GemmDesc d) {
         // tail re-fetches the last stage into idle buffers, keeping the loop one basic block).
         char *nxt = smem + ((kt + NS - 1) % NS) * STAGE;
         const int kn = min(kt + NS - 1, nk - 1) * BK;
+        if constexpr (FETCH == 2) {
+#ifndef AH_EXP_NOFETCH
+            fa.issue(Ab, d.lda, kn, nxt, wave);
+            fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
+#endif
+            __builtin_amdgcn_sched_barrier(0);
+        } else if constexpr (FETCH == 3) {
+            fa.issue_asm(Ab, d.lda, kn, nxt, wave);
+            fb.issue_asm(Bb, d.ldb, kn, nxt + ABYTES, wave);
+            prefetch(min(kt + NS, nk - 1) * BK);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         h8 a[2][FM], b[2][FN];
 #pragma unroll
         for (int i = 0; i < FM; i++) a[0][i] = frag<BM, TA, BK>(sa, wm0 + i * 32, 0, lane);
@@ -165,12 +247,10 @@ __global__ __launch_bounds__(kThreads) void gemm16_kernel(GemmDesc d) {
         // and stall MFMA issue); MFMAs of different k-steps, which share accumulators, never mix.
         __builtin_amdgcn_sched_barrier(0);
         constexpr int NM = FM * FN;
-        constexpr int PA = Fetch<BM, TA, BK>::PER;
+        constexpr int PA = Fetch<BM, TA, BK, NW>::PER;
         constexpr int FPS = (PERSTAGE + KS - 1) / KS;                      // fetches per k-step
-        // Spreading pays on the 256x256 tile (16 MFMAs per k-step); on 128x128 (4 per k-step) the
-        // fences cost more than they hide, so its fetches go out as one group.
-        constexpr bool SPREAD = NM >= 16;
-        if constexpr (!SPREAD) {
+        constexpr bool SPREAD = FETCH == 1;
+        if constexpr (FETCH == 0) {
 #ifndef AH_EXP_NOFETCH
             fa.issue(Ab, d.lda, kn, nxt, wave);
             fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
@@ -218,29 +298,49 @@ static bool operand_ok(const void *p, long ld, int rows) {
     return T == 0 || (rows % 8) == 0;
 }
 
-template <int BM, int TA, int TB, int EPI>
+template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, int TA, int TB, int EPI>
 static hipError_t launch(const GemmDesc &d, hipStream_t s) {
     int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
     const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
                         (uintptr_t)d.W16 | (uintptr_t)d.gout;
     const bool vepi = d.M % BM == 0 && d.N % BM == 0 && d.ldc % 4 == 0 && d.ldaux % 4 == 0 && (a & 15) == 0;
-    // k=64 per stage, 2 stages (256x256: 128 KiB; 128x128: 64 KiB). Deeper pipelines with k=32
-    // stages measured slower: each stage ends in a workgroup barrier, and halving the stage doubles them.
-    constexpr int BK = 64;
-    constexpr int NS = 2;
-    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS>), dim3(tiles), dim3(kThreads), 0, s, d);
-    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS>), dim3(tiles), dim3(kThreads), 0, s, d);
+    constexpr int NT = 64 * WVM * WVN;
+    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH>), dim3(tiles), dim3(NT), 0, s, d);
+    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS, WVM, WVN, FETCH>), dim3(tiles), dim3(NT), 0, s, d);
     return hipGetLastError();
 }
 
+// Variants (GemmDesc::variant), k=64 LDS stages, 2 in flight:
+//   1 = 128x128 tile, 4 waves, fetch mode 0          2 = 256x256, 4 waves (2x2), fetch mode 1
+//   3 = 256x256, 8 waves (4x2), fetch mode 1         4 = 256x256, 8 waves, fetch mode 2
+//   5 = 128x128, 4 waves, fetch mode 2               6 = 256x256, 4 waves, fetch mode 2
+//   7 = 256x256, 8 waves, k=32 stages, 5 in flight (160 KiB), fetch mode 2
+//   8 = 256x256, 8 waves, fetch mode 3 (asm DMA + L2 prefetch)
+//   9 = 128x128, 4 waves, fetch mode 3
+// 0 picks by shape.
+constexpr int kMaxVariant = 9;
 template <int TA, int TB, int EPI>
 static hipError_t launch_tile(const GemmDesc &d, hipStream_t s) {
-    int tile = d.tile;
-    if (tile == 0) {
-        long t256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
-        tile = t256 >= 224 ? 256 : 128;
+    int v = d.variant;
+    if (v == 0) {
+        int tile = d.tile;
+        if (tile == 0) {
+            long t256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
+            tile = t256 >= 224 ? 256 : 128;
+        }
+        v = tile == 256 ? 3 : 1;
     }
-    return tile == 256 ? launch<256, TA, TB, EPI>(d, s) : launch<128, TA, TB, EPI>(d, s);
+    switch (v) {
+        case 1: return launch<128, 2, 2, 64, 2, 0, TA, TB, EPI>(d, s);
+        case 2: return launch<256, 2, 2, 64, 2, 1, TA, TB, EPI>(d, s);
+        case 4: return launch<256, 4, 2, 64, 2, 2, TA, TB, EPI>(d, s);
+        case 5: return launch<128, 2, 2, 64, 2, 2, TA, TB, EPI>(d, s);
+        case 6: return launch<256, 2, 2, 64, 2, 2, TA, TB, EPI>(d, s);
+        case 7: return launch<256, 4, 2, 32, 5, 2, TA, TB, EPI>(d, s);
+        case 8: return launch<256, 4, 2, 64, 2, 3, TA, TB, EPI>(d, s);
+        case 9: return launch<128, 2, 2, 64, 2, 3, TA, TB, EPI>(d, s);
+        default: return launch<256, 4, 2, 64, 2, 1, TA, TB, EPI>(d, s);
+    }
 }
 
 template <int TA, int TB>
@@ -261,8 +361,9 @@ static hipError_t launch_epi(const GemmDesc &d, hipStream_t s) {
 // Returns true (and launches) when the shape/alignment admits the direct-to-LDS f16 kernel.
 bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
     using namespace g16;
-    if (d.dtype != GEMM_F16 || d.K <= 0 || d.K % 64) return false;
+    if (d.dtype != GEMM_F16 || d.K <= 0 || d.K % 64) return false;   // every variant's stage divides 64
     if (d.tile != 0 && d.tile != 128 && d.tile != 256) return false;
+    if (d.variant < 0 || d.variant > kMaxVariant) return false;
     bool ok = (d.ta ? operand_ok<1>(d.A, d.lda, d.M) : operand_ok<0>(d.A, d.lda, d.M)) &&
               (d.tb ? operand_ok<1>(d.B, d.ldb, d.N) : operand_ok<0>(d.B, d.ldb, d.N));
     if (!ok) return false;

@@ -101,6 +101,56 @@ static int copy_in_f16(ah_device *d, half_t *dst, const float *src, size_t n) {
     return copy_in(d, dst, h.data(), n * 2);
 }
 
+// ── GEMM variant tuning ─────────────────────────────────────────────────────
+
+constexpr int kGemm16Variants = 9;
+
+static std::string tune_key(const GemmDesc &g) {
+    char b[96];
+    snprintf(b, sizeof b, "%d/%d/%d/%d/%d/%d", g.dtype, g.ta, g.tb, g.M, g.N, g.K);
+    return b;
+}
+
+// Launch with the tuned variant when the caller left the choice open.
+static hipError_t gemm_run(ah_device *dev, GemmDesc g, hipStream_t s) {
+    if (g.variant == 0 && g.dtype == GEMM_F16) {
+        auto it = dev->gemm_variant.find(tune_key(g));
+        if (it != dev->gemm_variant.end()) g.variant = it->second;
+    }
+    return gemm_launch(g, s);
+}
+
+// Times every f16 variant of g (as given: its epilogue runs on whatever outputs g names) and caches
+// the fastest for g's shape.
+static int tune_gemm(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us) {
+    if (g.dtype != GEMM_F16) return set_error(AH_ERR_UNSUPPORTED, "gemm tuning covers the f16 kernels");
+    if (iters <= 0) return set_error(AH_ERR_INVALID, "gemm tuning: iterations must be > 0");
+    hipEvent_t e0, e1;
+    AH_HIP(hipEventCreate(&e0));
+    AH_HIP(hipEventCreate(&e1));
+    int bv = 0;
+    float bt = 0.0f;
+    hipError_t err = hipSuccess;
+    for (int v = 1; v <= kGemm16Variants && err == hipSuccess; v++) {
+        g.variant = v;
+        err = gemm_launch(g, dev->stream);
+        if (err == hipSuccess) err = hipEventRecord(e0, dev->stream);
+        for (int i = 0; i < iters && err == hipSuccess; i++) err = gemm_launch(g, dev->stream);
+        if (err == hipSuccess) err = hipEventRecord(e1, dev->stream);
+        if (err == hipSuccess) err = hipEventSynchronize(e1);
+        float ms = 0.0f;
+        if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+        if (err == hipSuccess && (bv == 0 || ms < bt)) { bv = v; bt = ms; }
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (err != hipSuccess) return fail_hip(err, "gemm tuning");
+    dev->gemm_variant[tune_key(g)] = bv;
+    if (best) *best = bv;
+    if (best_us) *best_us = bt * 1000.0 / iters;
+    return AH_OK;
+}
+
 static GemmDesc gdesc(int dtype, int epi, int ta, int tb, int M, int N, int K, const void *A, long lda,
                       const void *B, long ldb, void *C, long ldc) {
     GemmDesc g;
@@ -153,21 +203,21 @@ struct MlpCeTrainer : ah_trainer {
         float *db1 = acc, *db2 = acc + H;
         GemmDesc g1 = gdesc(GEMM_F32, EPI_BIAS_RELU, 0, 0, B, H, D, x, D, W1, D, H1, H);
         g1.bias = b1;
-        LAUNCH("fc1", gemm_launch(g1, s));
+        LAUNCH("fc1", gemm_run(dev, g1, s));
         GemmDesc g2 = gdesc(GEMM_F32, EPI_BIAS, 0, 0, B, C, H, H1, H, W2, H, Z2, C);
         g2.bias = b2;
-        LAUNCH("fc2", gemm_launch(g2, s));
+        LAUNCH("fc2", gemm_run(dev, g2, s));
         LAUNCH("softmax_ce", softmax_ce(Z2, lab, B, C, a, dZ2, rowloss, s));
         LAUNCH("db2", colsum_add(dZ2, B, C, C, db2, s));
         GemmDesc g3 = gdesc(GEMM_F32, EPI_MASK, 0, 1, B, H, C, dZ2, C, W2, H, dZ1, H);
         g3.aux = H1; g3.ldaux = H; g3.colsum = db1;
-        LAUNCH("dH1", gemm_launch(g3, s));
+        LAUNCH("dH1", gemm_run(dev, g3, s));
         GemmDesc g4 = gdesc(GEMM_F32, EPI_SGD, 1, 1, C, H, B, dZ2, C, H1, H, nullptr, H);
         g4.W32 = W2; g4.lr = lr; g4.gout = sg ? gW2 : nullptr;
-        LAUNCH("dW2", gemm_launch(g4, s));
+        LAUNCH("dW2", gemm_run(dev, g4, s));
         GemmDesc g5 = gdesc(GEMM_F32, EPI_SGD, 1, 1, H, D, B, dZ1, H, x, D, nullptr, D);
         g5.W32 = W1; g5.lr = lr; g5.gout = sg ? gW1 : nullptr;
-        LAUNCH("dW1", gemm_launch(g5, s));
+        LAUNCH("dW1", gemm_run(dev, g5, s));
         TailArgs ta{};
         ta.seg[0] = {b2, nullptr, db2, sg ? gb2 : nullptr, C, 1.0f};
         ta.seg[1] = {b1, nullptr, db1, sg ? gb1 : nullptr, H, 1.0f};
@@ -203,7 +253,7 @@ struct Mlp3Trainer : ah_trainer {
         rc |= alloc(&gb1, D1); rc |= alloc(&gb2, D2); rc |= alloc(&gb3, D3);
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * (D1 + D2 + D3 + 1)));
-        return AH_OK;
+        return tune();
     }
     int max_batch() const override { return B; }
     int set(int slot, const void *h, int64_t n) override {
@@ -240,6 +290,63 @@ struct Mlp3Trainer : ah_trainer {
         if (n > t[slot].n) return set_error(AH_ERR_INVALID, "MLP3: slot %d too small", slot);
         return copy_out(dev, h, t[slot].p, (size_t)n * 4);
     }
+    // The step's eight contractions, in launch order (fc1 fc2 fc3_mse dH2 dW3 dH1 dW2 dW1).
+    static constexpr int kGemms = 8;
+    GemmDesc gemm(int i, bool sg) const {
+        const float sc = (float)(1.0 / ((double)B * (double)D3));
+        const float bs = 2.0f * sc;
+        float *db1 = acc, *db2 = acc + D1, *db3 = acc + D1 + D2, *lacc = acc + D1 + D2 + D3;
+        GemmDesc g;
+        switch (i) {
+            case 0: g = gdesc(GEMM_F16, EPI_BIAS_RELU, 0, 0, B, D1, D0, X, D0, W1h, D0, H1, D1); g.bias = b1h; break;
+            case 1: g = gdesc(GEMM_F16, EPI_BIAS_RELU, 0, 0, B, D2, D1, H1, D1, W2h, D1, H2, D2); g.bias = b2h; break;
+            case 2:
+                g = gdesc(GEMM_F16, EPI_MSE, 0, 0, B, D3, D2, H2, D2, W3h, D2, Dd, D3);
+                g.bias = b3h; g.aux = T; g.ldaux = D3; g.colsum = db3; g.lossacc = lacc;
+                break;
+            case 3:
+                g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D2, D3, Dd, D3, W3h, D2, dZ2, D2);
+                g.aux = H2; g.ldaux = D2; g.colsum = db2;
+                break;
+            case 4:
+                g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D3, D2, B, Dd, D3, H2, D2, nullptr, D2);
+                g.scale = bs; g.W32 = W3; g.W16 = W3h; g.lr = lr; g.gout = sg ? gW3 : nullptr;
+                break;
+            case 5:
+                g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D1, D2, dZ2, D2, W2h, D1, dZ1, D1);
+                g.aux = H1; g.ldaux = D1; g.colsum = db1;
+                break;
+            case 6:
+                g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D2, D1, B, dZ2, D2, H1, D1, nullptr, D1);
+                g.scale = bs; g.W32 = W2; g.W16 = W2h; g.lr = lr; g.gout = sg ? gW2 : nullptr;
+                break;
+            default:
+                g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D1, D0, B, dZ1, D1, X, D0, nullptr, D0);
+                g.scale = bs; g.W32 = W1; g.W16 = W1h; g.lr = lr; g.gout = sg ? gW1 : nullptr;
+                break;
+        }
+        return g;
+    }
+    // Variant selection for the step's contractions (BEAM over the f16 kernels): each is timed with
+    // a store epilogue into scratch, so tuning touches no parameter, accumulator or activation.
+    int tune() {
+        size_t most = 0;
+        for (int i = 0; i < kGemms; i++) {
+            GemmDesc g = gemm(i, false);
+            most = std::max(most, (size_t)g.M * g.N);
+        }
+        half_t *scratch = nullptr;
+        AH_HIP(hipMalloc(&scratch, most * sizeof(half_t)));
+        int rc = AH_OK;
+        for (int i = 0; i < kGemms && rc == AH_OK; i++) {
+            GemmDesc g = gemm(i, false);
+            if (dev->gemm_variant.count(tune_key(g))) continue;
+            g.epi = EPI_STORE; g.C = scratch; g.ldc = g.N; g.colsum = nullptr; g.lossacc = nullptr;
+            rc = tune_gemm(dev, g, 3, nullptr, nullptr);
+        }
+        hipFree(scratch);
+        return rc;
+    }
     int enqueue(int64_t batch, int flags) override {
         if (batch != B) return set_error(AH_ERR_INVALID, "MLP3: batch %lld != %d", (long long)batch, B);
         hipStream_t s = dev->stream;
@@ -247,30 +354,8 @@ struct Mlp3Trainer : ah_trainer {
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
         float *db1 = acc, *db2 = acc + D1, *db3 = acc + D1 + D2, *lacc = acc + D1 + D2 + D3;
-        GemmDesc g = gdesc(GEMM_F16, EPI_BIAS_RELU, 0, 0, B, D1, D0, X, D0, W1h, D0, H1, D1);
-        g.bias = b1h;
-        LAUNCH("fc1", gemm_launch(g, s));
-        g = gdesc(GEMM_F16, EPI_BIAS_RELU, 0, 0, B, D2, D1, H1, D1, W2h, D1, H2, D2);
-        g.bias = b2h;
-        LAUNCH("fc2", gemm_launch(g, s));
-        g = gdesc(GEMM_F16, EPI_MSE, 0, 0, B, D3, D2, H2, D2, W3h, D2, Dd, D3);
-        g.bias = b3h; g.aux = T; g.ldaux = D3; g.colsum = db3; g.lossacc = lacc;
-        LAUNCH("fc3_mse", gemm_launch(g, s));
-        g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D2, D3, Dd, D3, W3h, D2, dZ2, D2);
-        g.aux = H2; g.ldaux = D2; g.colsum = db2;
-        LAUNCH("dH2", gemm_launch(g, s));
-        g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D3, D2, B, Dd, D3, H2, D2, nullptr, D2);
-        g.scale = bs; g.W32 = W3; g.W16 = W3h; g.lr = lr; g.gout = sg ? gW3 : nullptr;
-        LAUNCH("dW3", gemm_launch(g, s));
-        g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D1, D2, dZ2, D2, W2h, D1, dZ1, D1);
-        g.aux = H1; g.ldaux = D1; g.colsum = db1;
-        LAUNCH("dH1", gemm_launch(g, s));
-        g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D2, D1, B, dZ2, D2, H1, D1, nullptr, D1);
-        g.scale = bs; g.W32 = W2; g.W16 = W2h; g.lr = lr; g.gout = sg ? gW2 : nullptr;
-        LAUNCH("dW2", gemm_launch(g, s));
-        g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D1, D0, B, dZ1, D1, X, D0, nullptr, D0);
-        g.scale = bs; g.W32 = W1; g.W16 = W1h; g.lr = lr; g.gout = sg ? gW1 : nullptr;
-        LAUNCH("dW1", gemm_launch(g, s));
+        static const char *names[kGemms] = {"fc1", "fc2", "fc3_mse", "dH2", "dW3", "dH1", "dW2", "dW1"};
+        for (int i = 0; i < kGemms; i++) LAUNCH(names[i], gemm_run(dev, gemm(i, sg), s));
         TailArgs ta{};
         ta.seg[0] = {b3, b3h, db3, sg ? gb3 : nullptr, D3, bs};
         ta.seg[1] = {b2, b2h, db2, sg ? gb2 : nullptr, D2, bs};
@@ -369,14 +454,14 @@ struct ConvNetTrainer : ah_trainer {
         LAUNCH("conv2", conv_fwd_relu_pool(Pl1, B, C1, P1, cw2, cb2, C2, H2, Pl2, s));
         GemmDesc g = gdesc(GEMM_F32, EPI_BIAS, 0, 0, B, NC, F, Pl2, F, fw, F, lg, NC);
         g.bias = fb;
-        LAUNCH("fc", gemm_launch(g, s));
+        LAUNCH("fc", gemm_run(dev, g, s));
         LAUNCH("softmax_ce", softmax_ce(lg, lab, B, NC, a, dlg, rowloss, s));
         LAUNCH("dfb", colsum_add(dlg, B, NC, NC, acc, s));
         g = gdesc(GEMM_F32, EPI_STORE, 0, 1, B, F, NC, dlg, NC, fw, F, dP2, F);
-        LAUNCH("dP2", gemm_launch(g, s));
+        LAUNCH("dP2", gemm_run(dev, g, s));
         g = gdesc(GEMM_F32, EPI_SGD, 1, 1, NC, F, B, dlg, NC, Pl2, F, nullptr, F);
         g.W32 = fw; g.lr = lr; g.gout = sg ? gfw : nullptr;
-        LAUNCH("dfw", gemm_launch(g, s));
+        LAUNCH("dfw", gemm_run(dev, g, s));
         LAUNCH("pool2_bwd", pool_relu_bwd(dP2, H2, Pl2, B * C2, P1, dZ2, s));
         LAUNCH("conv2_dx", conv_bwd_x(dZ2, cw2, B, C1, P1, C2, dP1, s));
         LAUNCH("conv2_dw", conv_bwd_w_sgd(Pl1, dZ2, B, C1, P1, C2, cw2, cb2, lr, sg ? gcw2 : nullptr, sg ? gcb2 : nullptr, s));
@@ -507,15 +592,34 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d) {
     if ((d->epi == AH_EPI_MASK || d->epi == AH_EPI_MSE) && !d->aux) return set_error(AH_ERR_INVALID, "ah_gemm: epilogue needs aux");
     if (d->epi == AH_EPI_MSE && (d->dtype != AH_F16 || !d->lossacc)) return set_error(AH_ERR_INVALID, "ah_gemm: MSE epilogue is f16 with lossacc");
     if (d->tile != 0 && d->tile != 64 && d->tile != 128 && d->tile != 256) return set_error(AH_ERR_INVALID, "ah_gemm: tile %d", d->tile);
+    if (d->variant < 0 || d->variant > 9) return set_error(AH_ERR_INVALID, "ah_gemm: variant %d", d->variant);
     GemmDesc g;
     memset(&g, 0, sizeof g);
     g.dtype = d->dtype == AH_F16 ? GEMM_F16 : GEMM_F32;
     g.epi = d->epi; g.ta = d->ta; g.tb = d->tb; g.M = d->M; g.N = d->N; g.K = d->K;
     g.A = d->A; g.B = d->B; g.lda = d->lda; g.ldb = d->ldb; g.C = d->C; g.ldc = d->ldc; g.bias = d->bias;
     g.aux = d->aux; g.ldaux = d->ldaux; g.scale = d->scale; g.colsum = d->colsum; g.W32 = d->W32; g.W16 = d->W16;
-    g.lr = d->lr; g.gout = d->gout; g.lossacc = d->lossacc; g.tile = d->tile;
-    AH_HIP(gemm_launch(g, dev->stream));
+    g.lr = d->lr; g.gout = d->gout; g.lossacc = d->lossacc; g.tile = d->tile; g.variant = d->variant;
+    AH_HIP(gemm_run(dev, g, dev->stream));
     return AH_OK;
+}
+
+int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us) {
+    if (!dev || !d) return set_error(AH_ERR_INVALID, "ah_gemm_tune: null argument");
+    if (d->dtype != AH_F16) return set_error(AH_ERR_UNSUPPORTED, "ah_gemm_tune: f16 contractions only");
+    if (d->M <= 0 || d->N <= 0 || d->K <= 0 || !d->A || !d->B) return set_error(AH_ERR_INVALID, "ah_gemm_tune: bad shape/pointer");
+    if (d->epi == AH_EPI_SGD ? !d->W32 : !d->C) return set_error(AH_ERR_INVALID, "ah_gemm_tune: missing output");
+    GemmDesc g;
+    memset(&g, 0, sizeof g);
+    g.dtype = GEMM_F16;
+    g.epi = d->epi; g.ta = d->ta; g.tb = d->tb; g.M = d->M; g.N = d->N; g.K = d->K;
+    g.A = d->A; g.B = d->B; g.lda = d->lda; g.ldb = d->ldb; g.C = d->C; g.ldc = d->ldc; g.bias = d->bias;
+    g.aux = d->aux; g.ldaux = d->ldaux; g.scale = d->scale; g.colsum = d->colsum; g.W32 = d->W32; g.W16 = d->W16;
+    g.lr = d->lr; g.gout = d->gout; g.lossacc = d->lossacc;
+    int bv = 0;
+    int rc = tune_gemm(dev, g, iterations, &bv, best_us);
+    if (rc == AH_OK && best_variant) *best_variant = bv;
+    return rc;
 }
 
 int ah_softmax_ce(ah_device *dev, const float *z, const int32_t *labels, int32_t B, int32_t C, float *dz, float *loss) {

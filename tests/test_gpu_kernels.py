@@ -149,3 +149,74 @@ def test_chain_kernel_vs_oracle(dev, R, Cc):
     assert abs(dl.read()[0] - wl) < 1e-5 * abs(wl)
     for b in (dXb, dgb, dX, dg, dl):
         b.free()
+
+
+F16_VARIANTS = list(range(1, 10))   # every gemm16 variant (gemm16.hip launch_tile)
+VARIANT_SHAPES = [
+    # ta, tb, M, N, K: full tiles, ragged edges (scalar epilogue), short K, both layouts
+    (0, 0, 512, 512, 192), (0, 1, 520, 300, 128), (1, 1, 264, 520, 64), (1, 0, 256, 256, 320),
+]
+
+
+@pytest.mark.parametrize("variant", F16_VARIANTS)
+@pytest.mark.parametrize("shape", VARIANT_SHAPES, ids=lambda s: "ta%d_tb%d_%dx%dx%d" % s)
+def test_gemm16_variants_store_mask_sgd(dev, variant, shape):
+    """Every f16 kernel variant (tile, wave layout, fetch mode) against an f64 contraction of the
+    same f16 operands, through the STORE, MASK+colsum and SGD epilogues."""
+    ta, tb, M, N, K = shape
+    A = q16(RNG.standard_normal((M, K)))
+    B = q16(RNG.standard_normal((N, K)))
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    As, Bs = store_operand(A, ta), store_operand(B, tb)
+    dA, dB = dev.buffer(As.astype(np.float16), L.AH_F16), dev.buffer(Bs.astype(np.float16), L.AH_F16)
+    dC = dev.buffer(M * N, L.AH_F16)
+    common = dict(dtype=L.AH_F16, ta=ta, tb=tb, M=M, N=N, K=K, A=dA, B=dB, lda=As.shape[1], ldb=Bs.shape[1],
+                  ldc=N, variant=variant)
+    dev.gemm(epi=L.EPI_STORE, scale=1.0, C_out=dC, **common)
+    C = dC.read().astype(np.float32).reshape(M, N)
+    np.testing.assert_allclose(C, q16(ref), rtol=2e-3, atol=2e-3 * np.abs(ref).max())
+    Hact = RNG.standard_normal((M, N)).astype(np.float32)
+    Hact = np.where(Hact < 0, np.float32(-0.0), Hact).astype(np.float16)
+    dH = dev.buffer(Hact, L.AH_F16)
+    cs = dev.buffer(np.zeros(N, np.float32), L.AH_F32)
+    dev.gemm(epi=L.EPI_MASK, scale=0.5, C_out=dC, aux=dH, ldaux=N, colsum=cs, **common)
+    masked = np.where(np.signbit(Hact.astype(np.float32)) & (Hact == 0), 0.0, 0.5 * ref)
+    assert O.relerr(dC.read().astype(np.float32).reshape(M, N), masked) < 2e-3
+    assert O.relerr(cs.read(), masked.sum(0)) < 1e-4
+    W = RNG.standard_normal((M, N)).astype(np.float32)
+    dW, dg, dW16 = dev.buffer(W, L.AH_F32), dev.buffer(M * N, L.AH_F32), dev.buffer(M * N, L.AH_F16)
+    dev.gemm(epi=L.EPI_SGD, scale=0.25, W32=dW, W16=dW16, lr=0.1, gout=dg, **common)
+    assert O.relerr(dg.read().reshape(M, N), 0.25 * ref) < 1e-5
+    Wn = dW.read().reshape(M, N)
+    assert O.relerr(Wn - W, -0.025 * ref) < 1e-4
+    np.testing.assert_array_equal(dW16.read(), Wn.astype(np.float16).ravel())
+    for b in (dA, dB, dC, dH, cs, dW, dg, dW16):
+        b.free()
+
+
+@pytest.mark.parametrize("shape", [(0, 0, 512, 384, 256), (1, 1, 256, 512, 192), (0, 1, 300, 260, 128)],
+                         ids=lambda s: "ta%d_tb%d_%dx%dx%d" % s)
+def test_gemm16_variants_bit_identical_and_tune(dev, shape):
+    """All f16 variants accumulate each output over k in the same order, so their results are
+    bit-identical; the tuner picks one of them, caches it, and variant-0 launches reproduce it."""
+    ta, tb, M, N, K = shape
+    A, B = q16(RNG.standard_normal((M, K))), q16(RNG.standard_normal((N, K)))
+    As, Bs = store_operand(A, ta), store_operand(B, tb)
+    dA, dB = dev.buffer(As.astype(np.float16), L.AH_F16), dev.buffer(Bs.astype(np.float16), L.AH_F16)
+    dC = dev.buffer(M * N, L.AH_F32)
+    dW = dev.buffer(np.zeros(M * N, np.float32))
+    common = dict(dtype=L.AH_F16, ta=ta, tb=tb, M=M, N=N, K=K, A=dA, B=dB, lda=As.shape[1], ldb=Bs.shape[1], ldc=N)
+    outs = []
+    for v in F16_VARIANTS:
+        dW.write(np.zeros(M * N, np.float32))
+        dev.gemm(epi=L.EPI_SGD, scale=1.0, W32=dW, lr=-1.0, variant=v, **common)   # W = 0 + acc, exact f32
+        outs.append(dW.read())
+    for v, o in zip(F16_VARIANTS, outs):
+        np.testing.assert_array_equal(o.view(np.uint32), outs[0].view(np.uint32), err_msg=f"variant {v}")
+    best, us = dev.gemm_tune(iterations=2, epi=L.EPI_SGD, scale=1.0, W32=dW, lr=-1.0, **common)
+    assert best in F16_VARIANTS and us > 0
+    dW.write(np.zeros(M * N, np.float32))
+    dev.gemm(epi=L.EPI_SGD, scale=1.0, W32=dW, lr=-1.0, **common)
+    np.testing.assert_array_equal(dW.read().view(np.uint32), outs[0].view(np.uint32))
+    for b in (dA, dB, dC, dW):
+        b.free()
