@@ -149,15 +149,21 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
 // 3: like 2, but the DMAs are issued from inline asm (no compiler-inserted waits) and every thread
 // also prefetches one line of stage kt+NS into L2, so the DMA of that stage one iteration later hits
 // L2 instead of waiting on the Infinity Cache or HBM. Needs k=64 stages and 2*BM threads.
-template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH>
-__global__ __launch_bounds__(64 * WVM * WVN) void gemm16_kernel(GemmDesc d) {
+// KG: k-groups. With KG = 2 the workgroup holds two sets of WVM x WVN waves on the same tile; group g
+// contracts the g-th half of K through its own LDS stages, and at the end group 1 hands its
+// accumulators to group 0 through LDS, which adds them and runs the epilogue. Two waves then share
+// each SIMD on tiles whose accumulators leave room for only one wave set (the 128x128 tile).
+template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, int KG = 1>
+__global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d) {
     constexpr int NW = WVM * WVN;
     constexpr int WM = BM / WVM, WN = BN / WVN, FM = WM / 32, FN = WN / 32;
     constexpr int ABYTES = BM * BK * 2, BBYTES = BN * BK * 2, STAGE = ABYTES + BBYTES;
     constexpr int KS = BK / 16;                                           // MFMA k-steps per stage
     constexpr int PERSTAGE = Fetch<BM, TA, BK, NW>::PER + Fetch<BN, TB, BK, NW>::PER;
     constexpr int SMEM0 = (NS * STAGE > NW * WM * 256) ? NS * STAGE : NW * WM * 256;
-    constexpr int SMEM = FETCH == 3 ? SMEM0 + NW * 256 : SMEM0;       // + per-wave prefetch junk slots
+    constexpr int SMEMG = FETCH == 3 ? SMEM0 + NW * 256 : SMEM0;      // + per-wave prefetch junk slots
+    constexpr int SMEMR = KG > 1 ? BM * BN * 4 : 0;                   // k-group reduction buffer
+    constexpr int SMEM = KG * SMEMG > SMEMR ? KG * SMEMG : SMEMR;
     static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
     __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
@@ -173,14 +179,23 @@ __global__ __launch_bounds__(64 * WVM * WVN) void gemm16_kernel(GemmDesc d) {
     const int rem = L - group * G * tiles_n;
     const int m0 = (gm0 + rem % gsz) * BM, n0 = (rem / gsz) * BN;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int kg = KG > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) / NW : 0;   // k-group
+    const int tid = threadIdx.x - kg * 64 * NW, wave = tid >> 6;                             // within the group
     const int wm0 = (wave / WVN) * WM, wn0 = (wave % WVN) * WN;
+    char *gsm = smem + kg * SMEMG;                                                          // the group's LDS
 
     Fetch<BM, TA, BK, NW> fa;
     Fetch<BN, TB, BK, NW> fb;
     fa.init(d.lda, m0, d.M, wave, lane);
     fb.init(d.ldb, n0, d.N, wave, lane);
     const char *Ab = (const char *)d.A, *Bb = (const char *)d.B;
+    const int nk = d.K / BK / KG;
+    if constexpr (KG > 1) {   // this group's half of K starts at kg * nk * BK
+        const long k0 = (long)kg * nk * BK;
+        Ab += TA == 0 ? k0 * 2 : k0 * d.lda * 2;
+        Bb += TB == 0 ? k0 * 2 : k0 * d.ldb * 2;
+    }
 
     floatx16 acc[FM][FN];
 #pragma unroll
@@ -188,9 +203,8 @@ __global__ __launch_bounds__(64 * WVM * WVN) void gemm16_kernel(GemmDesc d) {
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
 
-    const int nk = d.K / BK;
     static_assert(FETCH != 3 || (BK == 64 && 64 * NW == 2 * BM && BM == BN), "prefetch mapping: one line per thread");
-    const char *junk = smem + SMEM0 + wave * 256;
+    const char *junk = gsm + SMEM0 + wave * 256;
     // prefetch: the first half of the waves covers A's stage lines, the second half B's. The branch
     // is on a scalar (wave-uniform) value, so each wave issues exactly one prefetch load per stage,
     // which the vmcnt accounting of the loop relies on.
@@ -203,11 +217,11 @@ __global__ __launch_bounds__(64 * WVM * WVN) void gemm16_kernel(GemmDesc d) {
     for (int p = 0; p < NS - 1; p++) {
         const int kp = min(p, nk - 1) * BK;
         if constexpr (FETCH == 3) {
-            fa.issue_asm(Ab, d.lda, kp, smem + p * STAGE, wave);
-            fb.issue_asm(Bb, d.ldb, kp, smem + p * STAGE + ABYTES, wave);
+            fa.issue_asm(Ab, d.lda, kp, gsm + p * STAGE, wave);
+            fb.issue_asm(Bb, d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
         } else {
-            fa.issue(Ab, d.lda, kp, smem + p * STAGE, wave);
-            fb.issue(Bb, d.ldb, kp, smem + p * STAGE + ABYTES, wave);
+            fa.issue(Ab, d.lda, kp, gsm + p * STAGE, wave);
+            fb.issue(Bb, d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
         }
     }
     if constexpr (FETCH == 3) prefetch(min(NS - 1, nk - 1) * BK);
@@ -219,10 +233,10 @@ __global__ __launch_bounds__(64 * WVM * WVN) void gemm16_kernel(GemmDesc d) {
         else asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE) : "memory");
         __syncthreads();
 #endif
-        const char *sa = smem + (kt % NS) * STAGE, *sb = sa + ABYTES;
+        const char *sa = gsm + (kt % NS) * STAGE, *sb = sa + ABYTES;
         // Refill the buffer consumed in the previous iteration with stage kt+NS-1 (clamped: the
         // tail re-fetches the last stage into idle buffers, keeping the loop one basic block).
-        char *nxt = smem + ((kt + NS - 1) % NS) * STAGE;
+        char *nxt = gsm + ((kt + NS - 1) % NS) * STAGE;
         const int kn = min(kt + NS - 1, nk - 1) * BK;
         if constexpr (FETCH == 2) {
 #ifndef AH_EXP_NOFETCH
@@ -282,10 +296,36 @@ __global__ __launch_bounds__(64 * WVM * WVN) void gemm16_kernel(GemmDesc d) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // drain the tail re-fetches before LDS reuse
 
+    if constexpr (KG > 1) {
+        // group 1 -> LDS -> group 0: element e of lane l of wave w at [w][e][l] (conflict-free)
+        constexpr int NE = FM * FN * 16;
+        float *red = (float *)smem + wave * NE * 64 + lane;
+        __syncthreads();
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) red[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * FN + j) * 16 + r) * 64];
+        }
+        __syncthreads();   // the epilogue below reuses this LDS
+        if (kg == 1) return;
+    }
+
     const int mb = m0 + wm0, nb = n0 + wn0;
     if constexpr (VEPI) {
         // Epilogue through the (now idle) operand LDS: each wave owns FM*32 rows x 64 f32 columns.
-        __syncthreads();
+        if constexpr (KG == 1) __syncthreads();
         epilogue_lds<EPI, half_t, FM, FN>(d, acc, mb, nb, lane, smem + wave * (WM * 256));
     } else {
         epilogue_tile<EPI, half_t, FM, FN>(d, acc, mb, nb, lane);
@@ -298,15 +338,15 @@ static bool operand_ok(const void *p, long ld, int rows) {
     return T == 0 || (rows % 8) == 0;
 }
 
-template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, int TA, int TB, int EPI>
+template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, int TA, int TB, int EPI, int KG = 1>
 static hipError_t launch(const GemmDesc &d, hipStream_t s) {
     int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
     const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
                         (uintptr_t)d.W16 | (uintptr_t)d.gout;
     const bool vepi = d.M % BM == 0 && d.N % BM == 0 && d.ldc % 4 == 0 && d.ldaux % 4 == 0 && (a & 15) == 0;
-    constexpr int NT = 64 * WVM * WVN;
-    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH>), dim3(tiles), dim3(NT), 0, s, d);
-    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS, WVM, WVN, FETCH>), dim3(tiles), dim3(NT), 0, s, d);
+    constexpr int NT = 64 * WVM * WVN * KG;
+    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH, KG>), dim3(tiles), dim3(NT), 0, s, d);
+    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS, WVM, WVN, FETCH, KG>), dim3(tiles), dim3(NT), 0, s, d);
     return hipGetLastError();
 }
 
@@ -317,8 +357,9 @@ static hipError_t launch(const GemmDesc &d, hipStream_t s) {
 //   7 = 256x256, 8 waves, k=32 stages, 5 in flight (160 KiB), fetch mode 2
 //   8 = 256x256, 8 waves, fetch mode 3 (asm DMA + L2 prefetch)
 //   9 = 128x128, 4 waves, fetch mode 3
+//  10 = 128x128, 2 k-groups of 4 waves, fetch mode 3   11 = the same with fetch mode 2
 // 0 picks by shape.
-constexpr int kMaxVariant = 9;
+constexpr int kMaxVariant = 11;
 template <int TA, int TB, int EPI>
 static hipError_t launch_tile(const GemmDesc &d, hipStream_t s) {
     int v = d.variant;
@@ -339,6 +380,8 @@ static hipError_t launch_tile(const GemmDesc &d, hipStream_t s) {
         case 7: return launch<256, 4, 2, 32, 5, 2, TA, TB, EPI>(d, s);
         case 8: return launch<256, 4, 2, 64, 2, 3, TA, TB, EPI>(d, s);
         case 9: return launch<128, 2, 2, 64, 2, 3, TA, TB, EPI>(d, s);
+        case 10: return launch<128, 2, 2, 64, 2, 3, TA, TB, EPI, 2>(d, s);
+        case 11: return launch<128, 2, 2, 64, 2, 2, TA, TB, EPI, 2>(d, s);
         default: return launch<256, 4, 2, 64, 2, 1, TA, TB, EPI>(d, s);
     }
 }
@@ -361,7 +404,8 @@ static hipError_t launch_epi(const GemmDesc &d, hipStream_t s) {
 // Returns true (and launches) when the shape/alignment admits the direct-to-LDS f16 kernel.
 bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
     using namespace g16;
-    if (d.dtype != GEMM_F16 || d.K <= 0 || d.K % 64) return false;   // every variant's stage divides 64
+    if (d.dtype != GEMM_F16 || d.K <= 0 || d.K % 64) return false;
+    if ((d.variant == 10 || d.variant == 11) && d.K % 128) return false;   // two k-groups of whole stages   // every variant's stage divides 64
     if (d.tile != 0 && d.tile != 128 && d.tile != 256) return false;
     if (d.variant < 0 || d.variant > kMaxVariant) return false;
     bool ok = (d.ta ? operand_ok<1>(d.A, d.lda, d.M) : operand_ok<0>(d.A, d.lda, d.M)) &&

@@ -103,7 +103,7 @@ static int copy_in_f16(ah_device *d, half_t *dst, const float *src, size_t n) {
 
 // ── GEMM variant tuning ─────────────────────────────────────────────────────
 
-constexpr int kGemm16Variants = 9;
+constexpr int kGemm16Variants = 11;
 
 static std::string tune_key(const GemmDesc &g) {
     char b[96];
@@ -592,7 +592,7 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d) {
     if ((d->epi == AH_EPI_MASK || d->epi == AH_EPI_MSE) && !d->aux) return set_error(AH_ERR_INVALID, "ah_gemm: epilogue needs aux");
     if (d->epi == AH_EPI_MSE && (d->dtype != AH_F16 || !d->lossacc)) return set_error(AH_ERR_INVALID, "ah_gemm: MSE epilogue is f16 with lossacc");
     if (d->tile != 0 && d->tile != 64 && d->tile != 128 && d->tile != 256) return set_error(AH_ERR_INVALID, "ah_gemm: tile %d", d->tile);
-    if (d->variant < 0 || d->variant > 9) return set_error(AH_ERR_INVALID, "ah_gemm: variant %d", d->variant);
+    if (d->variant < 0 || d->variant > kGemm16Variants) return set_error(AH_ERR_INVALID, "ah_gemm: variant %d", d->variant);
     GemmDesc g;
     memset(&g, 0, sizeof g);
     g.dtype = d->dtype == AH_F16 ? GEMM_F16 : GEMM_F32;
