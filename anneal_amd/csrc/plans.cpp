@@ -518,7 +518,9 @@ int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags) {
     if (batch <= 0 || batch > t->max_batch())
         return set_error(AH_ERR_INVALID, "ah_trainer_step: batch %lld outside [1, %d]", (long long)batch, t->max_batch());
     if (flags & AH_STEP_GRAPH) {
-        auto it = t->graphs.find(batch);
+        // one graph per (batch, gradient-output choice): the two capture different kernels' arguments
+        const int64_t key = batch * 2 + ((flags & AH_STEP_STORE_GRADS) ? 1 : 0);
+        auto it = t->graphs.find(key);
         if (it == t->graphs.end()) {
             int saved = t->probe_index;
             t->probe_index = -1;
@@ -531,7 +533,7 @@ int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags) {
             t->probe_index = saved;
             if (rc2) { ah_graph_destroy(g); return rc2; }
             if (rc) return rc;
-            it = t->graphs.emplace(batch, g).first;
+            it = t->graphs.emplace(key, g).first;
         }
         return ah_graph_replay(t->dev, it->second);
     }

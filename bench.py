@@ -25,6 +25,11 @@ PEAK_F16 = 2.5e15     # MI355X dense f16/bf16 MFMA, FLOP/s
 PEAK_F32 = 157.3e12   # MI355X f32 matrix/vector, FLOP/s
 PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
 
+# HBM bytes per launch of the dominant kernels, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
+# scaled by a plain copy of known size (read factor 2.0, write factor 1.0): profiles/hbm_traffic_pmc.md.
+TRAFFIC_BYTES = {(3, "dW2"): 269.7e6 + 100.9e6, (5, "chain_grad"): 134.4e6 + 134.3e6,
+                 (5, "chain_stats"): 134.3e6 + 4.2e6}
+
 
 def config_workload(cfg: int):
     """Returns (trainer kind, dims, lr, batch, inputs dict, kernels [(name, kind, amount)], meta)."""
@@ -80,6 +85,62 @@ def cpu_baseline(cfg: int, inputs: dict):
     return None
 
 
+def other_configs(dev, skip: int) -> dict:
+    """Steps/s of the other BASELINE configs at their own shapes (graph replay of the device-resident
+    step, the tensor.JIT pattern; config 4 per bound batch N). Parity for each is in tests/."""
+    from anneal_amd import _lib as L
+    from anneal_amd import data
+    from anneal_amd.backend import Trainer
+
+    def rate(t, batch, steps=50):
+        for _ in range(3):
+            t.step(batch, graph=True)
+        dev.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            t.step(batch, graph=True)
+        dev.sync()
+        return steps / (time.perf_counter() - t0)
+
+    out = {}
+    if skip != 1:
+        p = data.mlp_ce_inputs(64, 784, 128, 10)
+        t = Trainer(dev, L.TRAIN_MLP_CE, [64, 784, 128, 10], 0.01)
+        for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+            t.set(k, p[k])
+        out["config1_mlp_784-128-10_b64_f32"] = {"steps_per_s": rate(t, 64)}
+        t.close()
+    if skip != 2:
+        p = data.convnet_inputs()
+        t = Trainer(dev, L.TRAIN_CONVNET, [32, 28, 8, 16, 10], 0.01)
+        for k in ("x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+            t.set(k, p[k])
+        out["config2_convnet_b32_f32"] = {"steps_per_s": rate(t, 32)}
+        t.close()
+    if skip != 4:
+        p = data.mlp_ce_inputs(4096, 512, 2048, 512, x_lo=-1.0, x_hi=1.0)
+        t = Trainer(dev, L.TRAIN_MLP_CE, [4096, 512, 2048, 512], 0.01)
+        for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+            t.set(k, p[k])
+        out["config4_dynmlp_512-2048-512_f32"] = {f"N={n}_steps_per_s": rate(t, n, 100) for n in (1, 7, 256, 4096)}
+        t.close()
+    if skip != 5:
+        kind, dims, lr, batch, p, _, _ = config_workload(5)
+        t = Trainer(dev, kind, dims, lr)
+        for k, v in p.items():
+            t.set(k, v)
+        out["config5_chain_8192x4096_f32"] = {"steps_per_s": rate(t, batch)}
+        t.close()
+    if skip != 3:
+        kind, dims, lr, batch, p, _, _ = config_workload(3)
+        t = Trainer(dev, kind, dims, lr)
+        for k, v in p.items():
+            t.set(k, v)
+        out["config3_f16_mlp_b4096"] = {"steps_per_s": rate(t, batch, 20)}
+        t.close()
+    return out
+
+
 def copy_probe(mib: int):
     """Plain copy of a known size: FETCH_SIZE / WRITE_SIZE of this kernel calibrate the HBM counters."""
     import torch
@@ -99,6 +160,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-others", action="store_true", help="skip the steps/s of the other configs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 5 times (HBM counter calibration)")
     args = ap.parse_args()
@@ -151,7 +213,7 @@ def main():
     else:
         roof = {"bound": "hbm", "achieved": amount / dom_avg_s / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s"}
     roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["traffic"] = None
+    roof["traffic"] = TRAFFIC_BYTES.get((args.config, name))
     roof["kernel"] = name
     roof["avg_us"] = dom_avg_s * 1e6
 
@@ -179,6 +241,8 @@ def main():
         out["step_tflops"] = meta["flop_per_step"] * sps / 1e12
     out["cpu_baseline"] = None if args.no_cpu else cpu_baseline(args.config, p)
     t.close()
+    if not args.no_others:
+        out["other_configs"] = other_configs(dev, args.config)
     dev.close()
     print(json.dumps(out))
 

@@ -182,3 +182,17 @@ def test_config5_full_size_trainer_vs_oracle(dev):
         assert np.max(np.abs(got - exact)[mask]) / den <= ora_err + 1e-4
         assert O.relerr(t.get("dg", Cc), wdg) < 1e-5
     t.close()
+
+
+def test_graph_replay_keyed_by_gradient_outputs(dev):
+    """A graph captured without gradient outputs must not be replayed for a step that asks for them."""
+    B = 64
+    p = data.mlp_ce_inputs(B, 784, 128, 10)
+    t = Trainer(dev, L.TRAIN_MLP_CE, [B, 784, 128, 10], 0.0)
+    for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+        t.set(k, p[k])
+    t.step(B, store_grads=False, graph=True)
+    t.step(B, store_grads=True, graph=True)
+    _, g, _ = O.mlp_ce_step(p, 0.0)
+    assert O.relerr(t.get("dW1", 128 * 784), g["dW1"].ravel()) < 1e-4
+    t.close()
