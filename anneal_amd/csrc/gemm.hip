@@ -74,8 +74,7 @@ struct LoadK {
     static constexpr int VEC = 16 / sizeof(T);
     static constexpr int PER = R * 8 / kThreads;
     u32x4 v[PER];
-    __device__ __forceinline__ void load(const T *p, long ld, int r0, int rmax, int k0, int K, bool vec_ok) {
-        const int tid = threadIdx.x;
+    __device__ __forceinline__ void load(const T *p, long ld, int r0, int rmax, int k0, int K, bool vec_ok, int tid) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             int id = tid + kThreads * i;
@@ -90,8 +89,7 @@ struct LoadK {
             }
         }
     }
-    __device__ __forceinline__ void store(char *lds) const {
-        const int tid = threadIdx.x;
+    __device__ __forceinline__ void store(char *lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             int id = tid + kThreads * i;
@@ -108,8 +106,7 @@ struct LoadMN {
     static constexpr int NSUB = 8 * RB;
     static constexpr int PER = (NSUB + kThreads - 1) / kThreads;
     u32x4 v[PER][VEC];
-    __device__ __forceinline__ void load(const T *p, long ld, int r0, int rmax, int k0, int K, bool vec_ok) {
-        const int tid = threadIdx.x;
+    __device__ __forceinline__ void load(const T *p, long ld, int r0, int rmax, int k0, int K, bool vec_ok, int tid) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             int id = tid + kThreads * i;
@@ -128,8 +125,7 @@ struct LoadMN {
             }
         }
     }
-    __device__ __forceinline__ void store(char *lds) const {
-        const int tid = threadIdx.x;
+    __device__ __forceinline__ void store(char *lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             int id = tid + kThreads * i;
@@ -158,15 +154,22 @@ struct Loader<T, R, 0> : LoadK<T, R> {};
 template <typename T, int R>
 struct Loader<T, R, 1> : LoadMN<T, R> {};
 
-template <typename T, int BM, int BN, int TA, int TB, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmDesc d) {
+// KG: k-groups. The workgroup holds KG sets of 4 waves on the same tile; group g contracts the K
+// chunks [g*nkg, (g+1)*nkg) (chunks past K load as zeros, so every group runs the same number of
+// iterations and barriers), and groups 1..KG-1 hand their accumulators to group 0 through LDS, which
+// adds them in group order (deterministic) and runs the epilogue. Small-output, long-K contractions
+// (config 1's 64x128x784, config 4's small batches) get KG times the waves per tile.
+template <typename T, int BM, int BN, int TA, int TB, int EPI, int KG>
+__global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
     using MF = Mfma<T>;
     using vec_t = typename MF::vec_t;
     constexpr int VEC = MF::VEC;
     constexpr int BK = 8 * VEC;
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
     constexpr int STAGE = (BM + BN) * 128;
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    constexpr int SMEM_K = KG * 2 * STAGE;
+    constexpr int SMEM_R = (KG - 1) * BM * BN * 4;
+    __shared__ __attribute__((aligned(16))) char smem[SMEM_K > SMEM_R ? SMEM_K : SMEM_R];
 
     const int tiles_n = (d.N + BN - 1) / BN;
     const int tiles_m = (d.M + BM - 1) / BM;
@@ -184,8 +187,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmDesc d) {
     int tm = gm0 + rem % gsz, tn = rem / gsz;
     const int m0 = tm * BM, n0 = tn * BN;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kg = KG > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) : 0;
+    const int tid = threadIdx.x & (kThreads - 1), lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    char *gsm = smem + kg * 2 * STAGE;
 
     const T *A = (const T *)d.A;
     const T *B = (const T *)d.B;
@@ -201,19 +206,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmDesc d) {
         for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
 
     const int nk = (d.K + BK - 1) / BK;
-    la.load(A, d.lda, m0, d.M, 0, d.K, avec);
-    lb.load(B, d.ldb, n0, d.N, 0, d.K, bvec);
-    la.store(smem);
-    lb.store(smem + BM * 128);
+    const int nkg = (nk + KG - 1) / KG;       // chunks per group
+    const int kbeg = kg * nkg * BK;           // this group's first k (may lie past K: zeros)
+    la.load(A, d.lda, m0, d.M, kbeg, d.K, avec, tid);
+    lb.load(B, d.ldb, n0, d.N, kbeg, d.K, bvec, tid);
+    la.store(gsm, tid);
+    lb.store(gsm + BM * 128, tid);
     __syncthreads();
 
-    for (int kt = 0; kt < nk; kt++) {
-        char *cur = smem + (kt & 1) * STAGE;
-        char *nxt = smem + ((kt + 1) & 1) * STAGE;
-        const bool more = kt + 1 < nk;
+    for (int kt = 0; kt < nkg; kt++) {
+        char *cur = gsm + (kt & 1) * STAGE;
+        char *nxt = gsm + ((kt + 1) & 1) * STAGE;
+        const bool more = kt + 1 < nkg;
         if (more) {
-            la.load(A, d.lda, m0, d.M, (kt + 1) * BK, d.K, avec);
-            lb.load(B, d.ldb, n0, d.N, (kt + 1) * BK, d.K, bvec);
+            la.load(A, d.lda, m0, d.M, kbeg + (kt + 1) * BK, d.K, avec, tid);
+            lb.load(B, d.ldb, n0, d.N, kbeg + (kt + 1) * BK, d.K, bvec, tid);
         }
         const char *sa = cur, *sb = cur + BM * 128;
 #pragma unroll
@@ -230,19 +237,58 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmDesc d) {
                 for (int j = 0; j < FN; j++) MF::mma(a[i], b[j], acc[i][j]);
         }
         if (more) {
-            la.store(nxt);
-            lb.store(nxt + BM * 128);
+            la.store(nxt, tid);
+            lb.store(nxt + BM * 128, tid);
         }
         __syncthreads();
     }
 
+    if constexpr (KG > 1) {
+        // groups 1..KG-1 -> LDS -> group 0, element e of lane l of wave w at [g-1][w][e][l]
+        constexpr int NE = FM * FN * 16;
+        if (kg > 0) {
+            float *red = (float *)smem + ((kg - 1) * 4 + wave) * NE * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) red[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kg > 0) return;
+        for (int g = 1; g < KG; g++) {
+            const float *red = (const float *)smem + ((g - 1) * 4 + wave) * NE * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * FN + j) * 16 + r) * 64];
+        }
+    }
     epilogue_tile<EPI, T, FM, FN>(d, acc, m0 + wm0, n0 + wn0, lane);
 }
 
 template <typename T, int BM, int TA, int TB, int EPI>
 static hipError_t launch_t(const GemmDesc &d, hipStream_t s) {
-    int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI>), dim3(tiles), dim3(kThreads), 0, s, d);
+    const int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
+    constexpr int VEC = 16 / sizeof(T), BK = 8 * VEC;
+    const int nk = (d.K + BK - 1) / BK;
+    // k-groups while the tiles alone leave the 256 CUs short of 2 workgroups' worth of waves and
+    // every group still gets at least 4 chunks of K (LDS: 64-tile 4 groups 128 KiB, 128-tile 2)
+    int kg = 1;
+    if (BM <= 128) {
+        const int maxkg = BM == 64 ? 4 : 2;
+        while (kg < maxkg && tiles * kg < 512 && nk >= 8 * kg) kg *= 2;
+    }
+    if constexpr (BM == 64) {
+        if (kg == 4) { hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 4>), dim3(tiles), dim3(kThreads * 4), 0, s, d); return hipGetLastError(); }
+    }
+    if constexpr (BM <= 128) {
+        if (kg == 2) { hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 2>), dim3(tiles), dim3(kThreads * 2), 0, s, d); return hipGetLastError(); }
+    }
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 1>), dim3(tiles), dim3(kThreads), 0, s, d);
     return hipGetLastError();
 }
 
