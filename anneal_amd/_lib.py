@@ -91,6 +91,7 @@ SIGNATURES = {
     "ah_benchmark": (C.c_int, [_P, C.POINTER(ah_exec_item), C.c_int32, C.c_int32, C.POINTER(ah_bench_result)]),
     "ah_outputs_free": (None, [C.POINTER(ah_output), C.c_int32]),
     "ah_gemm": (C.c_int, [_P, C.POINTER(ah_gemm_desc)]),
+    "ah_translate_wgsl": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
     "ah_gemm_tune": (C.c_int, [_P, C.POINTER(ah_gemm_desc), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
     "ah_softmax_ce": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P]),
     "ah_chain_step": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P]),
@@ -125,6 +126,16 @@ def load() -> C.CDLL:
 
 class AnnealHipError(RuntimeError):
     pass
+
+
+def translate_wgsl(src: str) -> str:
+    """HIP C++ rendering of a WGSL kernel in the subset anneal's codegen emits (host only, no device)."""
+    lib = load()
+    need = C.c_int64()
+    check(lib.ah_translate_wgsl(src.encode(), None, 0, C.byref(need)))
+    buf = C.create_string_buffer(need.value)
+    check(lib.ah_translate_wgsl(src.encode(), buf, need.value, C.byref(need)))
+    return buf.value.decode()
 
 
 def check(rc: int) -> None:

@@ -57,4 +57,5 @@ struct ah_graph {
 
 namespace ah {
 int template_create(const std::string &source, TemplateKernel **out);
+std::string wgsl_to_hip(const std::string &src, std::string *err);
 }

@@ -228,16 +228,30 @@ int ah_module_get(ah_device *d, const char *source, const char *entry, ah_kernel
         int rc = template_create(source, &k->tmpl);
         if (rc != AH_OK) { delete k; return rc; }
     } else {
+        // The reference's schedule cache delivers kernels as rendered WGSL (schedule/cache.go:69-100):
+        // such a source is first rendered as HIP by the WGSL-subset translator (wgsl.cpp).
+        std::string hip_src = source;
+        const bool from_wgsl = strstr(source, "@compute") != nullptr;
+        if (from_wgsl) {
+            std::string err;
+            hip_src = wgsl_to_hip(source, &err);
+            if (hip_src.empty()) {
+                delete k;
+                return set_error(AH_ERR_COMPILE, "wgsl: %s", err.c_str());
+            }
+        }
         hiprtcProgram prog;
-        if (hiprtcCreateProgram(&prog, source, "anneal_kernel.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
+        if (hiprtcCreateProgram(&prog, hip_src.c_str(), "anneal_kernel.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
             delete k;
             return set_error(AH_ERR_COMPILE, "hiprtcCreateProgram failed");
         }
         std::string arch = "--offload-arch=" + d->arch.substr(0, d->arch.find(':'));
-        // No packed FP32 VALU ops in generated code either (same flag as the library build).
+        // No packed FP32 VALU ops in generated code either (same flag as the library build); WGSL
+        // kernels are compiled without FMA contraction (each WGSL operation rounds on its own) and
+        // with wrapping signed arithmetic (WGSL i32 overflow wraps).
         const char *opts[] = {arch.c_str(), "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
-                              "-packed-fp32-ops"};
-        hiprtcResult rc = hiprtcCompileProgram(prog, 7, opts);
+                              "-packed-fp32-ops", "-ffp-contract=off", "-fwrapv"};
+        hiprtcResult rc = hiprtcCompileProgram(prog, from_wgsl ? 9 : 7, opts);
         if (rc != HIPRTC_SUCCESS) {
             size_t ls = 0;
             hiprtcGetProgramLogSize(prog, &ls);

@@ -70,6 +70,14 @@ float ah_f16_to_f32(uint16_t h);   /* uop/dtype.go:447 Float16ToFloat32 */
  * Kernel arguments: n_ptrs device pointers (data0 = output, data1.. = inputs, PARAM order as in
  * codegen/wgsl.go:58-76), then n_scalars int32 values (the params_n uniform of symbolic kernels). */
 int ah_module_get(ah_device *dev, const char *source, const char *entry, ah_kernel **out);
+
+/* The WGSL anneal's codegen renders (codegen/wgsl.go:41-238 RenderWGSL, the string the schedule cache
+ * keeps in ExecItem.WGSL, schedule/cache.go:69-100) is also accepted as `source` by ah_module_get / ah_run:
+ * it is rendered as HIP C++ (entry point `kernel`, the storage bindings in binding order, then the four
+ * int32 fields of params_n for symbolic kernels) and compiled by hiprtc. This call exposes that rendering
+ * on its own (no device needed): writes at most cap bytes of NUL-terminated HIP source to out and the
+ * full size to *needed; AH_ERR_COMPILE if the WGSL is outside the subset the reference emits. */
+int ah_translate_wgsl(const char *wgsl, char *out, int64_t cap, int64_t *needed);
 int ah_launch(ah_device *dev, ah_kernel *k, const uint32_t grid[3], const uint32_t block[3],
               void *const *ptrs, int32_t n_ptrs, const int32_t *scalars, int32_t n_scalars);
 
