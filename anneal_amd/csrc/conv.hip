@@ -90,18 +90,20 @@ __global__ __launch_bounds__(256) void conv_bwd_x_kernel(const float *G, const f
     dX[idx] = acc;
 }
 
-// Weight/bias gradient with the SGD update fused: block (co, ci) owns 9 weights (and the bias when
-// ci == 0), reduces over the N*H*H positions with an LDS tree, then updates them in place.
-__global__ __launch_bounds__(256) void conv_bwd_w_sgd_kernel(const float *X, const float *G, int N, int Ci, int H,
-                                                              int Co, float *w, float *b, float lr, float *gw,
-                                                              float *gb) {
+// Weight/bias gradient, stage 1: block (co, ci, split) owns the 9 weights of (co, ci) (and the bias
+// when ci == 0) over one contiguous share of the N*H*H positions, reduced with an LDS tree; the share's
+// 10 partial sums go to part[split][co][ci][10]. Splitting the positions keeps enough blocks in flight
+// when Co*Ci is small (conv1: 8 weight groups over 25088 positions each).
+__global__ __launch_bounds__(256) void conv_bwd_w_partial_kernel(const float *X, const float *G, int N, int Ci, int H,
+                                                                  int Co, int S, float *part) {
     __shared__ float red[10][256];
-    const int co = blockIdx.x, ci = blockIdx.y, tid = threadIdx.x;
+    const int co = blockIdx.x, ci = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
     float acc[10];
 #pragma unroll
     for (int q = 0; q < 10; q++) acc[q] = 0.0f;
-    const long HH = (long)H * H;
-    for (long i = tid; i < (long)N * HH; i += 256) {
+    const long HH = (long)H * H, total = (long)N * HH;
+    const long chunk = (total + S - 1) / S, i0 = (long)sp * chunk, i1 = min(total, i0 + chunk);
+    for (long i = i0 + tid; i < i1; i += 256) {
         int n = i / HH, p = i % HH, h = p / H, wv = p % H;
         float g = G[((long)n * Co + co) * HH + p];
         const float *xp = X + ((long)n * Ci + ci) * HH;
@@ -124,22 +126,41 @@ __global__ __launch_bounds__(256) void conv_bwd_w_sgd_kernel(const float *X, con
             for (int q = 0; q < 10; q++) red[q][tid] += red[q][tid + o];
         __syncthreads();
     }
-    if (tid < 9) {
-        long wi = ((long)co * Ci + ci) * 9 + tid;
-        float g = red[tid][0];
+    if (tid < 10) part[(((long)sp * Co + co) * Ci + ci) * 10 + tid] = red[tid][0];
+}
+
+// Stage 2: one thread per (co, ci, q) adds the S partials in split order (deterministic) and applies
+// SGD to the weight (q < 9) or the bias (q == 9, ci == 0).
+__global__ __launch_bounds__(256) void conv_bwd_w_finalize_kernel(const float *part, int S, int Co, int Ci, float *w,
+                                                                   float *b, float lr, float *gw, float *gb) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= Co * Ci * 10) return;
+    const int q = idx % 10, ci = (idx / 10) % Ci, co = idx / (10 * Ci);
+    float g = 0.0f;
+    for (int sp = 0; sp < S; sp++) g += part[(((long)sp * Co + co) * Ci + ci) * 10 + q];
+    if (q < 9) {
+        long wi = ((long)co * Ci + ci) * 9 + q;
         if (gw) gw[wi] = g;
         w[wi] = w[wi] - lr * g;
-    } else if (tid == 9 && ci == 0) {
-        float g = red[9][0];
+    } else if (ci == 0) {
         if (gb) gb[co] = g;
         b[co] = b[co] - lr * g;
     }
 }
 
+int conv_bwd_w_splits(int N, int Ci, int H, int Co) {
+    long groups = (long)Co * Ci, total = (long)N * H * H;
+    long s = 512 / groups;                 // about 512 blocks in flight
+    if (s > total / 1024) s = total / 1024;   // and at least ~4 positions per thread
+    return (int)(s < 1 ? 1 : s > 64 ? 64 : s);
+}
+
 hipError_t conv_fwd_relu_pool(const float *X, int N, int Ci, int H, const float *w, const float *b, int Co, float *Hout,
                               float *Pout, hipStream_t s) {
+    // 64-thread blocks: config 2's conv2 has 25088 pooled outputs, so 256-thread blocks would leave
+    // most of the 256 CUs idle
     long total = (long)N * Co * (H / 2) * (H / 2);
-    hipLaunchKernelGGL(conv_fwd_relu_pool_kernel, dim3((total + 255) / 256), dim3(256), 0, s, X, N, Ci, H, w, b, Co,
+    hipLaunchKernelGGL(conv_fwd_relu_pool_kernel, dim3((total + 63) / 64), dim3(64), 0, s, X, N, Ci, H, w, b, Co,
                        Hout, Pout);
     return hipGetLastError();
 }
@@ -150,12 +171,19 @@ hipError_t pool_relu_bwd(const float *dP, const float *Hact, const float *Pv, in
 }
 hipError_t conv_bwd_x(const float *G, const float *w, int N, int Ci, int H, int Co, float *dX, hipStream_t s) {
     long total = (long)N * Ci * H * H;
-    hipLaunchKernelGGL(conv_bwd_x_kernel, dim3((total + 255) / 256), dim3(256), 0, s, G, w, N, Ci, H, Co, dX);
+    hipLaunchKernelGGL(conv_bwd_x_kernel, dim3((total + 63) / 64), dim3(64), 0, s, G, w, N, Ci, H, Co, dX);
     return hipGetLastError();
 }
-hipError_t conv_bwd_w_sgd(const float *X, const float *G, int N, int Ci, int H, int Co, float *w, float *b, float lr,
-                          float *gw, float *gb, hipStream_t s) {
-    hipLaunchKernelGGL(conv_bwd_w_sgd_kernel, dim3(Co, Ci), dim3(256), 0, s, X, G, N, Ci, H, Co, w, b, lr, gw, gb);
+hipError_t conv_bwd_w_partial(const float *X, const float *G, int N, int Ci, int H, int Co, float *part, hipStream_t s) {
+    const int S = conv_bwd_w_splits(N, Ci, H, Co);
+    hipLaunchKernelGGL(conv_bwd_w_partial_kernel, dim3(Co, Ci, S), dim3(256), 0, s, X, G, N, Ci, H, Co, S, part);
+    return hipGetLastError();
+}
+hipError_t conv_bwd_w_finalize(const float *part, int N, int Ci, int H, int Co, float *w, float *b, float lr, float *gw,
+                               float *gb, hipStream_t s) {
+    const int S = conv_bwd_w_splits(N, Ci, H, Co);
+    const int n = Co * Ci * 10;
+    hipLaunchKernelGGL(conv_bwd_w_finalize_kernel, dim3((n + 255) / 256), dim3(256), 0, s, part, S, Co, Ci, w, b, lr, gw, gb);
     return hipGetLastError();
 }
 

@@ -322,8 +322,71 @@ static hipError_t launch_epi(const GemmDesc &d, hipStream_t s) {
     }
 }
 
+// ── few outputs, long K: one wave per output element ────────────────────────
+// Contractions whose M*N outputs are too few to occupy the CUs as tiles (config 1's 64x10 logits,
+// config 2's 32x10 fc, config 4's single-row batches) reduce each dot product across the 64 lanes of
+// a wave instead: lanes stride K in 16-byte chunks (A and B both K-contiguous), a shuffle tree sums
+// them, and lane 0 applies the same scalar epilogue as the tiled kernels.
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void gemm_dot_kernel(GemmDesc d) {
+    constexpr int VEC = 16 / sizeof(T);
+    const int lane = threadIdx.x & 63;
+    const long o = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (o >= (long)d.M * d.N) return;
+    const int m = (int)(o / d.N), n = (int)(o % d.N);
+    const T *a = (const T *)d.A + (long)m * d.lda, *b = (const T *)d.B + (long)n * d.ldb;
+    const bool vec = ((d.lda | d.ldb) % VEC) == 0 && (((uintptr_t)d.A | (uintptr_t)d.B) & 15) == 0;
+    float acc = 0.0f;
+    int k = lane * VEC;
+    if (vec) {
+        for (; k + VEC <= d.K; k += 64 * VEC) {
+            typedef T vt __attribute__((ext_vector_type(VEC)));
+            const vt x = *(const vt *)(a + k), y = *(const vt *)(b + k);
+#pragma unroll
+            for (int e = 0; e < VEC; e++) acc += (float)x[e] * (float)y[e];
+        }
+    }
+    for (; k < d.K; k += 64 * VEC)
+        for (int e = 0; e < VEC && k + e < d.K; e++) acc += (float)a[k + e] * (float)b[k + e];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane != 0) return;
+    float in = 0.0f, bias = 0.0f, lossp = 0.0f;
+    if constexpr (EPI == EPI_SGD) in = d.W32[(long)m * d.ldc + n];
+    if constexpr (EPI == EPI_MASK || EPI == EPI_MSE) in = (float)((const T *)d.aux)[(long)m * d.ldaux + n];
+    if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RELU || EPI == EPI_MSE) bias = (float)((const T *)d.bias)[n];
+    const float cs = epi_apply<EPI, T>(d, m, n, acc, in, bias, lossp);
+    if (d.colsum) atomicAdd(d.colsum + n, cs);
+    if constexpr (EPI == EPI_MSE) atomicAdd(d.lossacc, lossp);
+}
+
+template <typename T>
+static hipError_t launch_dot(const GemmDesc &d, hipStream_t s) {
+    const long outs = (long)d.M * d.N;
+    const dim3 grid((unsigned)((outs + 3) / 4));
+    switch (d.epi) {
+        case EPI_STORE: hipLaunchKernelGGL((gemm_dot_kernel<T, EPI_STORE>), grid, dim3(256), 0, s, d); break;
+        case EPI_BIAS: hipLaunchKernelGGL((gemm_dot_kernel<T, EPI_BIAS>), grid, dim3(256), 0, s, d); break;
+        case EPI_BIAS_RELU: hipLaunchKernelGGL((gemm_dot_kernel<T, EPI_BIAS_RELU>), grid, dim3(256), 0, s, d); break;
+        case EPI_MSE:
+            if constexpr (sizeof(T) == 2) { hipLaunchKernelGGL((gemm_dot_kernel<T, EPI_MSE>), grid, dim3(256), 0, s, d); break; }
+            else return hipErrorInvalidValue;
+        case EPI_MASK: hipLaunchKernelGGL((gemm_dot_kernel<T, EPI_MASK>), grid, dim3(256), 0, s, d); break;
+        case EPI_SGD: hipLaunchKernelGGL((gemm_dot_kernel<T, EPI_SGD>), grid, dim3(256), 0, s, d); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// The dot path takes A and B K-contiguous, at most 16384 outputs and K of at least 256 (where a tile
+// would run a long serial K loop on a handful of workgroups).
+static bool use_dot(const GemmDesc &d) {
+    return d.ta == 0 && d.tb == 0 && d.tile == 0 && (long)d.M * d.N <= 16384 && d.K >= 256;
+}
+
 template <typename T>
 static hipError_t launch_layout(const GemmDesc &d, hipStream_t s) {
+    if (use_dot(d)) return launch_dot<T>(d, s);
     int code = d.ta * 2 + d.tb;
     switch (code) {
         case 0: return launch_epi<T, 0, 0>(d, s);

@@ -406,7 +406,7 @@ struct ChainTrainer : ah_trainer {
 struct ConvNetTrainer : ah_trainer {
     int N, Hin, C1, C2, NC, P1, P2, F;
     float *x, *cw1, *cb1, *cw2, *cb2, *fw, *fb, *H1, *Pl1, *H2, *Pl2, *lg, *dlg, *dP2, *dZ2, *dP1, *dZ1;
-    float *rowloss, *acc, *loss, *gcw1, *gcb1, *gcw2, *gcb2, *gfw, *gfb;
+    float *rowloss, *acc, *loss, *gcw1, *gcb1, *gcw2, *gcb2, *gfw, *gfb, *wpart1, *wpart2;
     int32_t *lab;
     int init() {
         N = (int)dims[0]; Hin = (int)dims[1]; C1 = (int)dims[2]; C2 = (int)dims[3]; NC = (int)dims[4];
@@ -422,6 +422,8 @@ struct ConvNetTrainer : ah_trainer {
         rc |= alloc(&dZ2, (size_t)N * C2 * P1 * P1); rc |= alloc(&dP1, (size_t)N * C1 * P1 * P1);
         rc |= alloc(&dZ1, (size_t)N * C1 * Hin * Hin); rc |= alloc(&rowloss, N); rc |= alloc(&acc, NC);
         rc |= alloc(&loss, 1); rc |= alloc(&gcw1, (size_t)C1 * 9); rc |= alloc(&gcb1, C1);
+        rc |= alloc(&wpart1, (size_t)conv_bwd_w_splits(N, 1, Hin, C1) * C1 * 10);
+        rc |= alloc(&wpart2, (size_t)conv_bwd_w_splits(N, C1, P1, C2) * C2 * C1 * 10);
         rc |= alloc(&gcw2, (size_t)C2 * C1 * 9); rc |= alloc(&gcb2, C2); rc |= alloc(&gfw, (size_t)NC * F); rc |= alloc(&gfb, NC);
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * NC));
@@ -464,9 +466,11 @@ struct ConvNetTrainer : ah_trainer {
         LAUNCH("dfw", gemm_run(dev, g, s));
         LAUNCH("pool2_bwd", pool_relu_bwd(dP2, H2, Pl2, B * C2, P1, dZ2, s));
         LAUNCH("conv2_dx", conv_bwd_x(dZ2, cw2, B, C1, P1, C2, dP1, s));
-        LAUNCH("conv2_dw", conv_bwd_w_sgd(Pl1, dZ2, B, C1, P1, C2, cw2, cb2, lr, sg ? gcw2 : nullptr, sg ? gcb2 : nullptr, s));
+        LAUNCH("conv2_dw", conv_bwd_w_partial(Pl1, dZ2, B, C1, P1, C2, wpart2, s));
+        LAUNCH("conv2_dw_sgd", conv_bwd_w_finalize(wpart2, B, C1, P1, C2, cw2, cb2, lr, sg ? gcw2 : nullptr, sg ? gcb2 : nullptr, s));
         LAUNCH("pool1_bwd", pool_relu_bwd(dP1, H1, Pl1, B * C1, Hin, dZ1, s));
-        LAUNCH("conv1_dw", conv_bwd_w_sgd(x, dZ1, B, 1, Hin, C1, cw1, cb1, lr, sg ? gcw1 : nullptr, sg ? gcb1 : nullptr, s));
+        LAUNCH("conv1_dw", conv_bwd_w_partial(x, dZ1, B, 1, Hin, C1, wpart1, s));
+        LAUNCH("conv1_dw_sgd", conv_bwd_w_finalize(wpart1, B, 1, Hin, C1, cw1, cb1, lr, sg ? gcw1 : nullptr, sg ? gcb1 : nullptr, s));
         TailArgs ta{};
         ta.seg[0] = {fb, nullptr, acc, sg ? gfb : nullptr, NC, 1.0f};
         ta.nseg = 1; ta.lr = lr; ta.loss_mode = 2; ta.loss_scale = a; ta.rowloss = rowloss; ta.nrow = B; ta.loss_out = loss;

@@ -226,3 +226,38 @@ def test_gemm16_variants_bit_identical_and_tune(dev, shape):
     np.testing.assert_array_equal(dW.read().view(np.uint32), outs[best - 1].view(np.uint32))
     for b in (dA, dB, dC, dW):
         b.free()
+
+
+@pytest.mark.parametrize("dt", [L.AH_F32, L.AH_F16])
+def test_gemm_dot_path_epilogues(dev, dt):
+    """Few outputs with a long K (M*N <= 16384, K >= 256, A and B K-contiguous) take the
+    wave-per-output path: bias+ReLU, mask+colsum and SGD epilogues against f64."""
+    M, N, K = 24, 40, 300
+    npdt = np.float16 if dt == L.AH_F16 else np.float32
+    A, B = RNG.standard_normal((M, K)).astype(np.float32), RNG.standard_normal((N, K)).astype(np.float32)
+    bias = RNG.standard_normal(N).astype(np.float32)
+    if dt == L.AH_F16:
+        A, B, bias = q16(A), q16(B), q16(bias)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    dA, dB, db = dev.buffer(A.astype(npdt), dt), dev.buffer(B.astype(npdt), dt), dev.buffer(bias.astype(npdt), dt)
+    dC = dev.buffer(M * N, dt)
+    common = dict(dtype=dt, ta=0, tb=0, M=M, N=N, K=K, A=dA, B=dB, lda=K, ldb=K, ldc=N)
+    dev.gemm(epi=L.EPI_BIAS_RELU, bias=db, C_out=dC, **common)
+    H = dC.read().astype(np.float32).reshape(M, N)
+    z = ref + bias if dt == L.AH_F32 else q16(q16(ref) + bias)
+    tol = 1e-5 if dt == L.AH_F32 else 2e-3
+    assert O.relerr(H, np.maximum(z, 0)) < tol
+    assert np.array_equal(np.signbit(H) & (H == 0), z < 0)
+    Hact = np.where(RNG.standard_normal((M, N)) < 0, np.float32(-0.0), np.float32(1.0)).astype(npdt)
+    dH, cs = dev.buffer(Hact, dt), dev.buffer(np.zeros(N, np.float32))
+    dev.gemm(epi=L.EPI_MASK, scale=0.5, aux=dH, ldaux=N, colsum=cs, C_out=dC, **common)
+    masked = np.where(np.signbit(Hact.astype(np.float32)), 0.0, 0.5 * ref)
+    assert O.relerr(dC.read().astype(np.float32).reshape(M, N), masked) < tol
+    assert O.relerr(cs.read(), masked.sum(0)) < 1e-4
+    W = RNG.standard_normal((M, N)).astype(np.float32)
+    dW, dg = dev.buffer(W), dev.buffer(M * N)
+    dev.gemm(epi=L.EPI_SGD, scale=0.25, W32=dW, lr=0.1, gout=dg, **common)
+    assert O.relerr(dg.read().reshape(M, N), 0.25 * ref) < 1e-5
+    assert O.relerr(dW.read().reshape(M, N) - W, -0.025 * ref) < 1e-4
+    for b in (dA, dB, db, dC, dH, cs, dW, dg):
+        b.free()
