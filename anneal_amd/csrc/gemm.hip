@@ -54,6 +54,14 @@ struct Mfma<float> {
         c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[2], b[2], c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[3], b[3], c, 0, 0, 0);
     }
+    // Two independent chains (elements 0,2 into c and 1,3 into c2): a wave holding a single 32x32
+    // accumulator would otherwise issue four dependent 16-pass MFMAs back to back.
+    __device__ static __forceinline__ void mma2(const vec_t &a, const vec_t &b, floatx16 &c, floatx16 &c2) {
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[1], b[1], c2, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[2], b[2], c, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[3], b[3], c2, 0, 0, 0);
+    }
 };
 
 // Guarded element-wise fill of one 16-byte chunk (slow path for unaligned / ragged shapes).
@@ -199,11 +207,12 @@ __global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
 
     Loader<T, BM, TA> la;
     Loader<T, BN, TB> lb;
-    floatx16 acc[FM][FN];
+    constexpr bool ILP2 = sizeof(T) == 4 && FM * FN == 1;   // second accumulator bank, see Mfma::mma2
+    floatx16 acc[FM][FN], acc2[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
+        for (int j = 0; j < FN; j++) acc[i][j] = acc2[i][j] = (floatx16){};
 
     const int nk = (d.K + BK - 1) / BK;
     const int nkg = (nk + KG - 1) / KG;       // chunks per group
@@ -223,18 +232,32 @@ __global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
             lb.load(B, d.ldb, n0, d.N, kbeg + (kt + 1) * BK, d.K, bvec, tid);
         }
         const char *sa = cur, *sb = cur + BM * 128;
+        // Fragments are double-buffered: the LDS reads of chunk s+1 are issued before the MFMAs of
+        // chunk s, so their latency hides behind those MFMAs.
+        vec_t a[2][FM], b[2][FN];
+#pragma unroll
+        for (int i = 0; i < FM; i++) a[0][i] = *(const vec_t *)(sa + lds_off(wm0 + i * 32 + (lane & 31), lane >> 5));
+#pragma unroll
+        for (int j = 0; j < FN; j++) b[0][j] = *(const vec_t *)(sb + lds_off(wn0 + j * 32 + (lane & 31), lane >> 5));
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            const int c = 2 * s + (lane >> 5);
-            vec_t a[FM], b[FN];
+            const int cb = s & 1, nb = cb ^ 1;
+            if (s + 1 < 4) {
+                const int c = 2 * (s + 1) + (lane >> 5);
 #pragma unroll
-            for (int i = 0; i < FM; i++) a[i] = *(const vec_t *)(sa + lds_off(wm0 + i * 32 + (lane & 31), c));
+                for (int i = 0; i < FM; i++) a[nb][i] = *(const vec_t *)(sa + lds_off(wm0 + i * 32 + (lane & 31), c));
 #pragma unroll
-            for (int j = 0; j < FN; j++) b[j] = *(const vec_t *)(sb + lds_off(wn0 + j * 32 + (lane & 31), c));
+                for (int j = 0; j < FN; j++) b[nb][j] = *(const vec_t *)(sb + lds_off(wn0 + j * 32 + (lane & 31), c));
+            }
+            __builtin_amdgcn_sched_barrier(0);   // keep the next reads ahead of this chunk's MFMAs
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++) MF::mma(a[i], b[j], acc[i][j]);
+                for (int j = 0; j < FN; j++) {
+                    if constexpr (ILP2) MF::mma2(a[cb][i], b[cb][j], acc[i][j], acc2[i][j]);
+                    else MF::mma(a[cb][i], b[cb][j], acc[i][j]);
+                }
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (more) {
             la.store(nxt, tid);
@@ -243,6 +266,12 @@ __global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
         __syncthreads();
     }
 
+    if constexpr (ILP2) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) acc[i][j] += acc2[i][j];
+    }
     if constexpr (KG > 1) {
         // groups 1..KG-1 -> LDS -> group 0, element e of lane l of wave w at [g-1][w][e][l]
         constexpr int NE = FM * FN * 16;
@@ -275,12 +304,14 @@ static hipError_t launch_t(const GemmDesc &d, hipStream_t s) {
     const int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
     constexpr int VEC = 16 / sizeof(T), BK = 8 * VEC;
     const int nk = (d.K + BK - 1) / BK;
-    // k-groups while the tiles alone leave the 256 CUs short of 2 workgroups' worth of waves and
-    // every group still gets at least 4 chunks of K (LDS: 64-tile 4 groups 128 KiB, 128-tile 2)
+    // k-groups: each of a tile's register-staged K iterations waits on its global loads, so long K
+    // loops over few waves are latency bound. Add wave sets (each taking a share of K) while there
+    // are at most 4 workgroups' worth per CU and every group keeps at least 8 chunks
+    // (LDS: 64-tile 4 groups 128 KiB, 128-tile 2 groups 128 KiB).
     int kg = 1;
     if (BM <= 128) {
         const int maxkg = BM == 64 ? 4 : 2;
-        while (kg < maxkg && tiles * kg < 512 && nk >= 8 * kg) kg *= 2;
+        while (kg < maxkg && tiles * kg <= 1024 && nk >= 16 * kg) kg *= 2;
     }
     if constexpr (BM == 64) {
         if (kg == 4) { hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 4>), dim3(tiles), dim3(kThreads * 4), 0, s, d); return hipGetLastError(); }
