@@ -92,6 +92,14 @@ SIGNATURES = {
     "ah_outputs_free": (None, [C.POINTER(ah_output), C.c_int32]),
     "ah_gemm": (C.c_int, [_P, C.POINTER(ah_gemm_desc)]),
     "ah_translate_wgsl": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
+    "ah_ckpt_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "ah_ckpt_count": (C.c_int32, [_P]),
+    "ah_ckpt_entry": (C.c_int, [_P, C.c_int32, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.POINTER(C.c_int32),
+                                C.POINTER(C.POINTER(C.c_int64)), C.POINTER(C.c_int64)]),
+    "ah_ckpt_read": (C.c_int, [_P, C.c_int32, C.POINTER(C.c_float), C.c_int64]),
+    "ah_ckpt_close": (None, [_P]),
+    "ah_safetensors_save": (C.c_int, [C.c_char_p, C.c_int32, C.POINTER(C.c_char_p), C.POINTER(C.POINTER(C.c_float)),
+                                      C.POINTER(C.POINTER(C.c_int64)), C.POINTER(C.c_int32)]),
     "ah_gemm_tune": (C.c_int, [_P, C.POINTER(ah_gemm_desc), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
     "ah_softmax_ce": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P]),
     "ah_chain_step": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P]),

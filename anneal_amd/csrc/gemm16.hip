@@ -43,7 +43,9 @@ __device__ __forceinline__ int mnoff(int k, int m) {
 // One 16-byte-per-lane global->LDS DMA issued from inline asm: the compiler's wait-count model does
 // not see it, so it adds no conservative waits (an LDS-DMA the compiler knows about makes it wait
 // for every outstanding LDS read at the next use of any of them). The kernel orders these loads
-// with its own explicit s_waitcnt vmcnt.
+// with its own explicit s_waitcnt vmcnt. M0 (the DMA's LDS base) is written here; the compiler
+// reserves M0 and warns about the clobber, but no instruction it emits in these kernels reads M0 (no
+// builtin LDS-DMA, no dynamic register indexing on the fetch-mode-3 path), so nothing is disturbed.
 __device__ __forceinline__ void dma16(const char *g, const char *lds) {
     const uint32_t l = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),

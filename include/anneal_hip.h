@@ -229,6 +229,25 @@ int ah_trainer_probe(ah_trainer *t, int32_t kernel_index);
 int ah_trainer_probe_read(ah_trainer *t, double *total_ms, int64_t *count);
 int ah_trainer_kernel_count(ah_trainer *t, int64_t batch, int32_t *count);
 
+/* ── Checkpoint formats (host side; no device needed) ─────────────────────────
+ * Readers for safetensors (tensor/safetensors/safetensors.go:150-434 Load / LoadTensors), NumPy .npy and
+ * stored .npz (tensor/npy/npy.go:41-466 Load / LoadNPZ), decoding every tensor to f32 with the reference's
+ * dtype policy (safetensors.go:21-35, npy.go:3-16): F32 exact, F64 -> f32, F16 / BF16 widened (safetensors),
+ * integers by value with an error past 2^24, BOOL -> 0/1, any other dtype an error naming it; Fortran-order
+ * arrays come back in C order. The decoded values are what a trainer uploads with ah_trainer_set. */
+typedef struct ah_ckpt ah_ckpt;
+int ah_ckpt_open(const char *path, ah_ckpt **out);   /* format from the file's magic bytes */
+int32_t ah_ckpt_count(const ah_ckpt *c);
+int ah_ckpt_entry(const ah_ckpt *c, int32_t i, const char **name, const char **dtype, int32_t *rank,
+                  const int64_t **shape, int64_t *n_elems);
+int ah_ckpt_read(const ah_ckpt *c, int32_t i, float *out, int64_t n);
+void ah_ckpt_close(ah_ckpt *c);
+/* Writer for F32 safetensors checkpoints as safetensors.Save writes them (safetensors.go:75-146): names
+ * sorted, header JSON {"name":{"dtype":"F32","shape":[..],"data_offsets":[a,b]},..} padded with spaces to
+ * a multiple of 8 bytes, data little-endian in name order. */
+int ah_safetensors_save(const char *path, int32_t n, const char *const *names, const float *const *data,
+                        const int64_t *const *shapes, const int32_t *ranks);
+
 #ifdef __cplusplus
 }
 #endif

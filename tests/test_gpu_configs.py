@@ -196,3 +196,31 @@ def test_graph_replay_keyed_by_gradient_outputs(dev):
     _, g, _ = O.mlp_ce_step(p, 0.0)
     assert O.relerr(t.get("dW1", 128 * 784), g["dW1"].ravel()) < 1e-4
     t.close()
+
+
+def test_checkpoint_save_load_resumes_training(dev, tmp_path):
+    """Train -> save (safetensors) -> load into a fresh trainer -> the next step is bit-identical to
+    continuing the original trainer (tensor/safetensors/safetensors_test.go:260-390 pattern)."""
+    from anneal_amd import checkpoint as ck
+    B, D, H, Cn = 64, 784, 128, 10
+    p = data.mlp_ce_inputs(B, D, H, Cn)
+    names = {"fc1.weight": ("W1", (H, D)), "fc1.bias": ("b1", (H,)), "fc2.weight": ("W2", (Cn, H)),
+             "fc2.bias": ("b2", (Cn,))}
+    a = Trainer(dev, L.TRAIN_MLP_CE, [B, D, H, Cn], 0.01)
+    for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+        a.set(k, p[k])
+    a.step(B)
+    path = str(tmp_path / "mlp.safetensors")
+    ck.save_params(path, a, names)
+    b = Trainer(dev, L.TRAIN_MLP_CE, [B, D, H, Cn], 0.01)
+    b.set("x", p["x"])
+    b.set("labels", p["labels"])
+    ck.load_params(path, b, names)
+    a.step(B, store_grads=True)
+    b.step(B, store_grads=True)
+    for k, n in (("loss", 1), ("dW1", H * D), ("W1", H * D), ("W2", Cn * H), ("b2", Cn)):
+        np.testing.assert_array_equal(a.get(k, n).view(np.uint32), b.get(k, n).view(np.uint32), err_msg=k)
+    with pytest.raises(L.AnnealHipError, match="shape"):
+        ck.load_params(path, b, {"fc1.weight": ("W1", (D, H))})
+    a.close()
+    b.close()
