@@ -100,6 +100,7 @@ SIGNATURES = {
     "ah_ckpt_close": (None, [_P]),
     "ah_safetensors_save": (C.c_int, [C.c_char_p, C.c_int32, C.POINTER(C.c_char_p), C.POINTER(C.POINTER(C.c_float)),
                                       C.POINTER(C.POINTER(C.c_int64)), C.POINTER(C.c_int32)]),
+    "ah_gemm_tune_cache": (C.c_int, [_P, C.c_char_p, C.c_int32]),
     "ah_gemm_tune": (C.c_int, [_P, C.POINTER(ah_gemm_desc), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
     "ah_softmax_ce": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P]),
     "ah_chain_step": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P]),

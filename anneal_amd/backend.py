@@ -99,6 +99,10 @@ class Device:
         L.check(self.lib.ah_gemm_tune(self.h, C.byref(d), iterations, C.byref(v), C.byref(us)))
         return v.value, us.value
 
+    def gemm_tune_cache(self, path: str, save: bool) -> None:
+        """Saves the tuned f16 variant choices to path, or merges a saved file into this device's cache."""
+        L.check(self.lib.ah_gemm_tune_cache(self.h, str(path).encode(), 1 if save else 0))
+
     def softmax_ce(self, z: DeviceBuffer, labels: DeviceBuffer, B: int, Cn: int, dz: DeviceBuffer,
                    loss: DeviceBuffer) -> None:
         L.check(self.lib.ah_softmax_ce(self.h, z.ptr, labels.ptr, B, Cn, dz.ptr, loss.ptr))

@@ -7,6 +7,7 @@
 // device stream: the forward once, every gradient once, and SGD fused into the weight-gradient GEMM
 // epilogues, with parameters resident in HBM across steps.
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -330,6 +331,13 @@ struct Mlp3Trainer : ah_trainer {
     // Variant selection for the step's contractions (BEAM over the f16 kernels): each is timed with
     // a store epilogue into scratch, so tuning touches no parameter, accumulator or activation.
     int tune() {
+        // BEAM's disk cache (codegen/beam.go:118-169): with AH_GEMM_TUNE_CACHE naming a file, earlier
+        // choices are loaded first and the file is rewritten after tuning.
+        const char *cache = getenv("AH_GEMM_TUNE_CACHE");
+        if (cache && *cache) {
+            FILE *f = fopen(cache, "r");
+            if (f) { fclose(f); int rc0 = ah_gemm_tune_cache(dev, cache, 0); if (rc0) return rc0; }
+        }
         size_t most = 0;
         for (int i = 0; i < kGemms; i++) {
             GemmDesc g = gemm(i, false);
@@ -345,6 +353,7 @@ struct Mlp3Trainer : ah_trainer {
             rc = tune_gemm(dev, g, 3, nullptr, nullptr);
         }
         hipFree(scratch);
+        if (rc == AH_OK && cache && *cache) rc = ah_gemm_tune_cache(dev, cache, 1);
         return rc;
     }
     int enqueue(int64_t batch, int flags) override {
@@ -608,6 +617,44 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d) {
     g.lr = d->lr; g.gout = d->gout; g.lossacc = d->lossacc; g.tile = d->tile; g.variant = d->variant;
     AH_HIP(gemm_run(dev, g, dev->stream));
     return AH_OK;
+}
+
+int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save) {
+    if (!dev || !path) return set_error(AH_ERR_INVALID, "ah_gemm_tune_cache: null argument");
+    if (save) {
+        FILE *f = fopen(path, "w");
+        if (!f) return set_error(AH_ERR_INVALID, "gemm tune cache: cannot write %s", path);
+        std::vector<std::pair<std::string, int>> rows(dev->gemm_variant.begin(), dev->gemm_variant.end());
+        std::sort(rows.begin(), rows.end());
+        fprintf(f, "# anneal_hip gemm variants v1 %s\n", dev->arch.c_str());
+        for (auto &r : rows) fprintf(f, "%s %d\n", r.first.c_str(), r.second);
+        if (fclose(f) != 0) return set_error(AH_ERR_INVALID, "gemm tune cache: write to %s failed", path);
+        return AH_OK;
+    }
+    FILE *f = fopen(path, "r");
+    if (!f) return set_error(AH_ERR_INVALID, "gemm tune cache: cannot read %s", path);
+    char line[256];
+    int rc = AH_OK, lineno = 0;
+    std::unordered_map<std::string, int> got;
+    while (fgets(line, sizeof line, f)) {
+        lineno++;
+        if (line[0] == '#' || line[0] == '\n') {
+            // the header names the device the choices were timed on; another arch starts afresh
+            if (lineno == 1 && !strstr(line, dev->arch.c_str())) { fclose(f); return AH_OK; }
+            continue;
+        }
+        char key[128];
+        int v = 0;
+        if (sscanf(line, "%127s %d", key, &v) != 2 || v < 1 || v > kGemm16Variants) {
+            rc = set_error(AH_ERR_INVALID, "gemm tune cache %s: bad line %d", path, lineno);
+            break;
+        }
+        got[key] = v;
+    }
+    fclose(f);
+    if (rc == AH_OK)
+        for (auto &kv : got) dev->gemm_variant[kv.first] = kv.second;
+    return rc;
 }
 
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us) {

@@ -186,6 +186,11 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * scheduling and accumulate each output over k in the same order (bit-identical results); variants
  * 10-11 add two k-halves, which rounds differently in f32 (relative 1e-6 level). */
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us);
+/* BEAM's disk cache (codegen/beam.go:118-169): save (save != 0) the device's tuned choices to path, one
+ * "dtype/ta/tb/M/N/K variant" line each under a header naming the gfx arch, or merge a saved file into
+ * the device's cache (a file timed on another arch is ignored). The config-3 trainer loads and rewrites
+ * the file named by the environment variable AH_GEMM_TUNE_CACHE around its tuning. */
+int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save);
 
 /* Softmax cross-entropy forward+backward composed from reference ops (one wave64 per row):
  * m=Max, zs=z-m, e=Exp(zs), s=Sum e, logp=zs-Log(s), loss=Sum(onehot*logp)*(-1/B); dz includes the

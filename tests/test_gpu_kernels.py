@@ -261,3 +261,25 @@ def test_gemm_dot_path_epilogues(dev, dt):
     assert O.relerr(dW.read().reshape(M, N) - W, -0.025 * ref) < 1e-4
     for b in (dA, dB, db, dC, dH, cs, dW, dg):
         b.free()
+
+
+def test_gemm_tune_disk_cache(dev, tmp_path):
+    """Tuned choices survive a save/load through the disk cache, and a malformed file is rejected."""
+    M, N, K = 256, 256, 128
+    A, B = q16(RNG.standard_normal((M, K))), q16(RNG.standard_normal((N, K)))
+    dA, dB = dev.buffer(A.astype(np.float16), L.AH_F16), dev.buffer(B.astype(np.float16), L.AH_F16)
+    dC = dev.buffer(M * N, L.AH_F16)
+    best, _ = dev.gemm_tune(iterations=1, dtype=L.AH_F16, epi=L.EPI_STORE, ta=0, tb=0, M=M, N=N, K=K, A=dA, B=dB,
+                            lda=K, ldb=K, C_out=dC, ldc=N)
+    path = tmp_path / "tune.txt"
+    dev.gemm_tune_cache(str(path), True)
+    lines = path.read_text().splitlines()
+    assert lines[0].startswith("# anneal_hip gemm variants v1")
+    assert f"1/0/0/{M}/{N}/{K} {best}" in lines
+    dev.gemm_tune_cache(str(path), False)
+    bad = tmp_path / "bad.txt"
+    bad.write_text(lines[0] + "\n1/0/0/8/8/8 99\n")
+    with pytest.raises(L.AnnealHipError, match="bad line"):
+        dev.gemm_tune_cache(str(bad), False)
+    for b in (dA, dB, dC):
+        b.free()
