@@ -37,15 +37,17 @@ struct GemmDesc {
     const void *bias; // [N], type = dtype
     const void *aux;  // [M,N] with ldaux, type = dtype (MSE targets / ReLU activations)
     long ldaux;
-    float scale;
     float *colsum;    // [N] f32 accumulator (atomic), optional
     float *W32;       // EPI_SGD master weights [M,N] (row stride ldc)
     void *W16;        // EPI_SGD f16 copy, optional
-    float lr;
     float *gout;      // EPI_SGD gradient output [M,N] (row stride ldc), optional
     float *lossacc;   // EPI_MSE scalar accumulator
     int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
-    int variant;      // f16 kernel variant (0 = auto; see gemm16.hip launch_tile), the tuning hook
+    int variant;      // f16 kernel variant (0 = auto; table Var<V> in gemm16_kernel.h), the tuning hook
+    // The float scalars sit beside the ints, away from the pointers: the compiler may merge loads of
+    // neighbouring fields into one vector, and a vector mixing pointers and floats is kept in memory.
+    float scale;
+    float lr;
 };
 
 hipError_t gemm_launch(const GemmDesc &d, hipStream_t s);

@@ -1,371 +1,47 @@
-// gemm16.hip — f16 MFMA contraction for gfx950 with direct global->LDS loads (no register staging).
-//
-// Block tile BM x BN (256x256 or 128x128), 4 wave64s in a 2x2 arrangement, K in LDS stages of 32 or 64
-// with 4 stages in flight.
-// Every operand tile is fetched with global_load_lds_dwordx4 (each lane's 16 bytes land at
-// LDS base + 16*lane), so loads for stage k+1 are in flight while stage k is contracted, and no VGPRs
-// or ds_write instructions are spent on staging. The layouts are chosen so that the fetch order
-// produces a bank-conflict-free LDS image (the LDS of gfx950 has 64 four-byte banks):
-//   K-contiguous operand ([rows][K]): rows of 64 or 128 bytes are packed into 256-byte super-rows
-//     whose 16-byte slots are XOR-swizzled by the super-row index; fragments are ds_read_b128.
-//   MN-contiguous operand ([K][rows]): k-rows stay in the stored orientation, 32-byte segments
-//     XOR-swizzled by 2*(k & 3); fragments are read with two ds_read_b64_tr_b16, the CDNA4 LDS
-//     transpose read (within 16 lanes, lane j addressing T[kb + j/4][mb + 4*(j%4)] receives
-//     T[kb..kb+3][mb + j]), so transposed operands cost no extra pass and no register shuffles.
-// Fragments of k-step s+1 are read while the MFMAs of k-step s run. Accumulation is f32
-// (codegen/lower.go:667-716 accumulates f16 reduces in f32); f16 products are exact in f32.
-#include "ah_common.h"
-#include "gemm.h"
-#include "gemm_epi.h"
+// gemm16.hip — host dispatch of the f16 MFMA contraction (kernel template: gemm16_kernel.h; each
+// variant is compiled in its own translation unit from gemm16_var.hip).
+#include "gemm16_kernel.h"
 
 namespace ah {
-namespace g16 {
 
-typedef half_t h8 __attribute__((ext_vector_type(8)));
-typedef short s4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s4 lds_s4;
+#define AH_G16_DECL(n) hipError_t gemm16_variant_##n(const GemmDesc &d, hipStream_t s);
+AH_G16_DECL(1) AH_G16_DECL(2) AH_G16_DECL(3) AH_G16_DECL(4) AH_G16_DECL(5) AH_G16_DECL(6) AH_G16_DECL(7)
+AH_G16_DECL(8) AH_G16_DECL(9) AH_G16_DECL(10) AH_G16_DECL(11) AH_G16_DECL(12) AH_G16_DECL(13)
+AH_G16_DECL(14) AH_G16_DECL(15) AH_G16_DECL(16) AH_G16_DECL(17) AH_G16_DECL(18) AH_G16_DECL(19)
+AH_G16_DECL(20) AH_G16_DECL(21) AH_G16_DECL(22) AH_G16_DECL(23) AH_G16_DECL(24) AH_G16_DECL(25)
+#undef AH_G16_DECL
 
-// Byte offset of (row r, 16-byte chunk c) in a K-contiguous tile whose rows hold BK halves:
-// 256-byte super-rows of 256/(2*BK) rows, 16-byte slots XOR-swizzled by the super-row index.
-template <int BK>
-__device__ __forceinline__ int koff(int r, int c) {
-    constexpr int CH = BK / 8, SR = 16 / CH;        // chunks per row, rows per super-row
-    const int q = r / SR;
-    return q * 256 + ((((r % SR) * CH + c) ^ (q & 15)) << 4);
-}
+namespace {
+typedef hipError_t (*VariantFn)(const GemmDesc &, hipStream_t);
+const VariantFn kVariants[g16::kMaxVariant + 1] = {
+    nullptr, gemm16_variant_1, gemm16_variant_2, gemm16_variant_3, gemm16_variant_4, gemm16_variant_5,
+    gemm16_variant_6, gemm16_variant_7, gemm16_variant_8, gemm16_variant_9, gemm16_variant_10,
+    gemm16_variant_11, gemm16_variant_12, gemm16_variant_13, gemm16_variant_14, gemm16_variant_15,
+    gemm16_variant_16, gemm16_variant_17, gemm16_variant_18, gemm16_variant_19, gemm16_variant_20,
+    gemm16_variant_21, gemm16_variant_22, gemm16_variant_23, gemm16_variant_24, gemm16_variant_25};
 
-// Byte offset of element (k-row k, column m) in an MN-contiguous tile of R columns.
-template <int R>
-__device__ __forceinline__ int mnoff(int k, int m) {
-    return k * (R * 2) + (((m >> 4) ^ ((k & 3) << 1)) << 5) + ((m & 15) << 1);
-}
-
-// One 16-byte-per-lane global->LDS DMA issued from inline asm: the compiler's wait-count model does
-// not see it, so it adds no conservative waits (an LDS-DMA the compiler knows about makes it wait
-// for every outstanding LDS read at the next use of any of them). The kernel orders these loads
-// with its own explicit s_waitcnt vmcnt. M0 (the DMA's LDS base) is written here; the compiler
-// reserves M0 and warns about the clobber, but no instruction it emits in these kernels reads M0 (no
-// builtin LDS-DMA, no dynamic register indexing on the fetch-mode-3 path), so nothing is disturbed.
-__device__ __forceinline__ void dma16(const char *g, const char *lds) {
-    const uint32_t l = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
-                 "s"(__builtin_amdgcn_readfirstlane(l))
-                 : "memory", "m0");
-}
-
-// L2 prefetch of one 128-byte line: a 4-byte-per-lane LDS-DMA into a junk LDS slot that nothing
-// reads (a load into a VGPR would need that register reserved against the load's late write-back).
-__device__ __forceinline__ void prefetch_line(const char *g, const char *junk) {
-    const uint32_t l = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)junk;
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
-                 "s"(__builtin_amdgcn_readfirstlane(l))
-                 : "memory", "m0");
-}
-
-// Per-lane global byte offsets for the 1 KiB blocks this wave fetches (stage-independent part).
-template <int R, int T, int BK, int NW>
-struct Fetch {
-    static constexpr int NB = R * BK * 2 / 1024;   // 1 KiB blocks per tile
-    static constexpr int PER = NB / NW;            // blocks per wave
-    static_assert(PER * NW == NB, "tile blocks must split evenly over the waves");
-    uint32_t off[PER];
-    __device__ __forceinline__ void init(long ld, int r0, int rmax, int wave, int lane) {
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int b = wave * PER + j;
-            if constexpr (T == 0) {
-                constexpr int CH = BK / 8, SR = 16 / CH;
-                const int q = 4 * b + (lane >> 4);
-                const int x = (lane & 15) ^ (q & 15);
-                const int row = min(r0 + q * SR + x / CH, rmax - 1);
-                off[j] = (uint32_t)(((long)row * ld + (x % CH) * 8) * 2);
-            } else {
-                constexpr int ROWS = 512 / R;                 // k-rows per block
-                const int kk = b * ROWS + (16 * lane) / (2 * R);
-                const int pos16 = ((16 * lane) % (2 * R)) / 16;
-                const int seg = (pos16 >> 1) ^ ((kk & 3) << 1);
-                const int m = min(r0 + seg * 16 + (pos16 & 1) * 8, rmax - 8);
-                off[j] = (uint32_t)(((long)kk * ld + m) * 2);
-            }
-        }
-    }
-    // Issue this wave's loads of the stage starting at k0 into `tile` (a 1 KiB-aligned LDS region).
-    __device__ __forceinline__ void issue(const char *base, long ld, int k0, char *tile, int wave) const {
-#pragma unroll
-        for (int j = 0; j < PER; j++) issue_one(j, base, ld, k0, tile, wave);
-    }
-    __device__ __forceinline__ void issue_one(int j, const char *base, long ld, int k0, char *tile, int wave) const {
-        const long adv = T == 0 ? (long)k0 * 2 : (long)k0 * ld * 2;
-        __builtin_amdgcn_global_load_lds((const void *)(base + adv + off[j]), (void *)(tile + (wave * PER + j) * 1024),
-                                         16, 0, 0);
-    }
-    __device__ __forceinline__ void issue_asm(const char *base, long ld, int k0, char *tile, int wave) const {
-        const long adv = T == 0 ? (long)k0 * 2 : (long)k0 * ld * 2;
-#pragma unroll
-        for (int j = 0; j < PER; j++) dma16(base + adv + off[j], tile + (wave * PER + j) * 1024);
-    }
-};
-
-// L2 prefetch of one operand's stage (k = k0 .. k0+63): the stage is R lines of 128 bytes (a
-// K-contiguous row holds 64 halves = one line; an MN-contiguous k-row of R halves holds R/64 lines).
-// Line i of the stage is touched by thread i (callers pass i < R, ragged rows clamped).
-template <int R, int T>
-__device__ __forceinline__ void prefetch_stage(const char *base, long ld, int r0, int rmax, int k0, int i,
-                                               const char *junk) {
-    if constexpr (T == 0) {
-        const int row = min(r0 + i, rmax - 1);
-        prefetch_line(base + ((long)row * ld + k0) * 2, junk);
-    } else {
-        constexpr int LPR = R / 64;
-        const int col = min(r0 + (i % LPR) * 64, rmax - 1);
-        prefetch_line(base + ((long)(k0 + i / LPR) * ld + col) * 2, junk);
+// k-groups of the variant (the K split must give each group whole 64-wide stages)
+int variant_kgroups(int v) {
+    switch (v) {
+#define AH_G16_KG(n) case n: return g16::Var<n>::KG;
+        AH_G16_KG(1) AH_G16_KG(2) AH_G16_KG(3) AH_G16_KG(4) AH_G16_KG(5) AH_G16_KG(6) AH_G16_KG(7)
+        AH_G16_KG(8) AH_G16_KG(9) AH_G16_KG(10) AH_G16_KG(11) AH_G16_KG(12) AH_G16_KG(13)
+        AH_G16_KG(14) AH_G16_KG(15) AH_G16_KG(16) AH_G16_KG(17) AH_G16_KG(18) AH_G16_KG(19)
+        AH_G16_KG(20) AH_G16_KG(21) AH_G16_KG(22) AH_G16_KG(23) AH_G16_KG(24) AH_G16_KG(25)
+#undef AH_G16_KG
+        default: return 1;
     }
 }
+}  // namespace
 
-template <int R, int T, int BK>
-__device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
-    if constexpr (T == 0) {
-        return *(const h8 *)(tile + koff<BK>(r + (lane & 31), 2 * s + (lane >> 5)));
-    } else {
-        const int g = lane >> 4, j = lane & 15;
-        const int m = r + 16 * (g & 1) + 4 * (j & 3);
-        const int k = 16 * s + 8 * (g >> 1) + (j >> 2);
-        s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(tile + mnoff<R>(k, m)));
-        s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(tile + mnoff<R>(k + 4, m)));
-        typedef short s8 __attribute__((ext_vector_type(8)));
-        s8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        return __builtin_bit_cast(h8, v);
-    }
-}
-
-// VEPI: every wave tile is in bounds and the epilogue arrays admit vector access, so the LDS-staged
-// vector epilogue is used (chosen on the host; a kernel holding both epilogues spills registers).
-// BK: k per LDS stage (32 or 64); NS: LDS stages in flight (the fetch of stage k+NS-1 is issued
-// while stage k is contracted). WVM x WVN waves share the tile: with 2x2 each wave holds a 128x128
-// accumulator (one wave per SIMD); with 4x2 on a 256x256 tile each wave holds 64x128 and two waves
-// share a SIMD, so one wave's MFMAs cover the other's LDS reads and barrier waits.
-// FETCH: where a stage's global->LDS fetches are issued. 0: as one group after the first k-step's
-// fragment reads; 1: spread between the MFMAs; 2: as one group right after the stage barrier, before
-// any fragment read. (An LDS-DMA issue makes the compiler wait for every outstanding LDS read at the
-// next MFMA, so with 0 and 1 the fragment reads of k-step s+1 are waited on before the MFMAs of s.)
-// 3: like 2, but the DMAs are issued from inline asm (no compiler-inserted waits) and every thread
-// also prefetches one line of stage kt+NS into L2, so the DMA of that stage one iteration later hits
-// L2 instead of waiting on the Infinity Cache or HBM. Needs k=64 stages and 2*BM threads.
-// KG: k-groups. With KG = 2 the workgroup holds two sets of WVM x WVN waves on the same tile; group g
-// contracts the g-th half of K through its own LDS stages, and at the end group 1 hands its
-// accumulators to group 0 through LDS, which adds them and runs the epilogue. Two waves then share
-// each SIMD on tiles whose accumulators leave room for only one wave set (the 128x128 tile).
-template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, int KG = 1>
-__global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d) {
-    constexpr int NW = WVM * WVN;
-    constexpr int WM = BM / WVM, WN = BN / WVN, FM = WM / 32, FN = WN / 32;
-    constexpr int ABYTES = BM * BK * 2, BBYTES = BN * BK * 2, STAGE = ABYTES + BBYTES;
-    constexpr int KS = BK / 16;                                           // MFMA k-steps per stage
-    constexpr int PERSTAGE = Fetch<BM, TA, BK, NW>::PER + Fetch<BN, TB, BK, NW>::PER;
-    constexpr int SMEM0 = (NS * STAGE > NW * WM * 256) ? NS * STAGE : NW * WM * 256;
-    constexpr int SMEMG = FETCH == 3 ? SMEM0 + NW * 256 : SMEM0;      // + per-wave prefetch junk slots
-    constexpr int SMEMR = KG > 1 ? BM * BN * 4 : 0;                   // k-group reduction buffer
-    constexpr int SMEM = KG * SMEMG > SMEMR ? KG * SMEMG : SMEMR;
-    static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
-    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
-
-    const int tiles_n = (d.N + BN - 1) / BN;
-    const int tiles_m = (d.M + BM - 1) / BM;
-    const int ntiles = tiles_m * tiles_n;
-    int L = blockIdx.x;
-    if ((ntiles & 7) == 0) L = (L & 7) * (ntiles >> 3) + (L >> 3);   // contiguous tile runs per XCD
-    constexpr int G = 4;
-    const int group = L / (G * tiles_n);
-    const int gm0 = group * G;
-    const int gsz = min(G, tiles_m - gm0);
-    const int rem = L - group * G * tiles_n;
-    const int m0 = (gm0 + rem % gsz) * BM, n0 = (rem / gsz) * BN;
-
-    const int lane = threadIdx.x & 63;
-    const int kg = KG > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) / NW : 0;   // k-group
-    const int tid = threadIdx.x - kg * 64 * NW, wave = tid >> 6;                             // within the group
-    const int wm0 = (wave / WVN) * WM, wn0 = (wave % WVN) * WN;
-    char *gsm = smem + kg * SMEMG;                                                          // the group's LDS
-
-    Fetch<BM, TA, BK, NW> fa;
-    Fetch<BN, TB, BK, NW> fb;
-    fa.init(d.lda, m0, d.M, wave, lane);
-    fb.init(d.ldb, n0, d.N, wave, lane);
-    const char *Ab = (const char *)d.A, *Bb = (const char *)d.B;
-    const int nk = d.K / BK / KG;
-    if constexpr (KG > 1) {   // this group's half of K starts at kg * nk * BK
-        const long k0 = (long)kg * nk * BK;
-        Ab += TA == 0 ? k0 * 2 : k0 * d.lda * 2;
-        Bb += TB == 0 ? k0 * 2 : k0 * d.ldb * 2;
-    }
-
-    floatx16 acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
-
-    static_assert(FETCH != 3 || (BK == 64 && 64 * NW == 2 * BM && BM == BN), "prefetch mapping: one line per thread");
-    const char *junk = gsm + SMEM0 + wave * 256;
-    // prefetch: the first half of the waves covers A's stage lines, the second half B's. The branch
-    // is on a scalar (wave-uniform) value, so each wave issues exactly one prefetch load per stage,
-    // which the vmcnt accounting of the loop relies on.
-    const bool pf_a = __builtin_amdgcn_readfirstlane(wave) < NW / 2;
-    auto prefetch = [&](int k0) {
-        if (pf_a) prefetch_stage<BM, TA>(Ab, d.lda, m0, d.M, k0, tid, junk);
-        else prefetch_stage<BN, TB>(Bb, d.ldb, n0, d.N, k0, tid - BM, junk);
-    };
-#pragma unroll
-    for (int p = 0; p < NS - 1; p++) {
-        const int kp = min(p, nk - 1) * BK;
-        if constexpr (FETCH == 3) {
-            fa.issue_asm(Ab, d.lda, kp, gsm + p * STAGE, wave);
-            fb.issue_asm(Bb, d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
-        } else {
-            fa.issue(Ab, d.lda, kp, gsm + p * STAGE, wave);
-            fb.issue(Bb, d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
-        }
-    }
-    if constexpr (FETCH == 3) prefetch(min(NS - 1, nk - 1) * BK);
-    for (int kt = 0; kt < nk; kt++) {
-        // stage kt has landed once at most the NS-2 younger stages (and, with prefetching, the one
-        // younger prefetch line) are still in flight
-#ifndef AH_EXP_NOBARRIER
-        if constexpr (FETCH == 3) asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE + 1) : "memory");
-        else asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE) : "memory");
-        __syncthreads();
-#endif
-        const char *sa = gsm + (kt % NS) * STAGE, *sb = sa + ABYTES;
-        // Refill the buffer consumed in the previous iteration with stage kt+NS-1 (clamped: the
-        // tail re-fetches the last stage into idle buffers, keeping the loop one basic block).
-        char *nxt = gsm + ((kt + NS - 1) % NS) * STAGE;
-        const int kn = min(kt + NS - 1, nk - 1) * BK;
-        if constexpr (FETCH == 2) {
-#ifndef AH_EXP_NOFETCH
-            fa.issue(Ab, d.lda, kn, nxt, wave);
-            fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
-#endif
-            __builtin_amdgcn_sched_barrier(0);
-        } else if constexpr (FETCH == 3) {
-            fa.issue_asm(Ab, d.lda, kn, nxt, wave);
-            fb.issue_asm(Bb, d.ldb, kn, nxt + ABYTES, wave);
-            prefetch(min(kt + NS, nk - 1) * BK);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        h8 a[2][FM], b[2][FN];
-#pragma unroll
-        for (int i = 0; i < FM; i++) a[0][i] = frag<BM, TA, BK>(sa, wm0 + i * 32, 0, lane);
-#pragma unroll
-        for (int j = 0; j < FN; j++) b[0][j] = frag<BN, TB, BK>(sb, wn0 + j * 32, 0, lane);
-        // Scheduling fences fix the issue order: the LDS reads of k-step s+1 go out as a group ahead
-        // of the MFMAs of k-step s (their latency hides behind the MFMAs); the stage fetches are
-        // spread evenly between the MFMAs (issued back to back they fill the vector-memory queue
-        // and stall MFMA issue); MFMAs of different k-steps, which share accumulators, never mix.
-        __builtin_amdgcn_sched_barrier(0);
-        constexpr int NM = FM * FN;
-        constexpr int PA = Fetch<BM, TA, BK, NW>::PER;
-        constexpr int FPS = (PERSTAGE + KS - 1) / KS;                      // fetches per k-step
-        constexpr bool SPREAD = FETCH == 1;
-        if constexpr (FETCH == 0) {
-#ifndef AH_EXP_NOFETCH
-            fa.issue(Ab, d.lda, kn, nxt, wave);
-            fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
-#endif
-        }
-#pragma unroll
-        for (int s = 0; s < KS; s++) {
-            const int c = s & 1, n = c ^ 1;
-            if (s + 1 < KS) {
-#pragma unroll
-                for (int i = 0; i < FM; i++) a[n][i] = frag<BM, TA, BK>(sa, wm0 + i * 32, s + 1, lane);
-#pragma unroll
-                for (int j = 0; j < FN; j++) b[n][j] = frag<BN, TB, BK>(sb, wn0 + j * 32, s + 1, lane);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-#pragma unroll
-            for (int t = 0; t < NM; t++) {
-                acc[t / FN][t % FN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][t / FN], b[c][t % FN], acc[t / FN][t % FN], 0, 0, 0);
-                if (SPREAD && t % (NM / FPS) == NM / FPS - 1) {
-                    const int f = s * FPS + t / (NM / FPS);
-#ifndef AH_EXP_NOFETCH
-                    if (f < PA) fa.issue_one(f, Ab, d.lda, kn, nxt, wave);
-                    else if (f < PERSTAGE) fb.issue_one(f - PA, Bb, d.ldb, kn, nxt + ABYTES, wave);
-#endif
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-        }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // drain the tail re-fetches before LDS reuse
-
-    if constexpr (KG > 1) {
-        // group 1 -> LDS -> group 0: element e of lane l of wave w at [w][e][l] (conflict-free)
-        constexpr int NE = FM * FN * 16;
-        float *red = (float *)smem + wave * NE * 64 + lane;
-        __syncthreads();
-        if (kg == 1) {
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) red[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
-        }
-        __syncthreads();
-        if (kg == 0) {
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * FN + j) * 16 + r) * 64];
-        }
-        __syncthreads();   // the epilogue below reuses this LDS
-        if (kg == 1) return;
-    }
-
-    const int mb = m0 + wm0, nb = n0 + wn0;
-    if constexpr (VEPI) {
-        // Epilogue through the (now idle) operand LDS: each wave owns FM*32 rows x 64 f32 columns.
-        if constexpr (KG == 1) __syncthreads();
-        epilogue_lds<EPI, half_t, FM, FN>(d, acc, mb, nb, lane, smem + wave * (WM * 256));
-    } else {
-        epilogue_tile<EPI, half_t, FM, FN>(d, acc, mb, nb, lane);
-    }
-}
-
-template <int T>
-static bool operand_ok(const void *p, long ld, int rows) {
-    if (((uintptr_t)p & 15) || (ld % 8) || rows < 8) return false;
-    return T == 0 || (rows % 8) == 0;
-}
-
-template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, int TA, int TB, int EPI, int KG = 1>
-static hipError_t launch(const GemmDesc &d, hipStream_t s) {
-    int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
-    const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
-                        (uintptr_t)d.W16 | (uintptr_t)d.gout;
-    const bool vepi = d.M % BM == 0 && d.N % BM == 0 && d.ldc % 4 == 0 && d.ldaux % 4 == 0 && (a & 15) == 0;
-    constexpr int NT = 64 * WVM * WVN * KG;
-    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH, KG>), dim3(tiles), dim3(NT), 0, s, d);
-    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS, WVM, WVN, FETCH, KG>), dim3(tiles), dim3(NT), 0, s, d);
-    return hipGetLastError();
-}
-
-// Variants (GemmDesc::variant), k=64 LDS stages, 2 in flight:
-//   1 = 128x128 tile, 4 waves, fetch mode 0          2 = 256x256, 4 waves (2x2), fetch mode 1
-//   3 = 256x256, 8 waves (4x2), fetch mode 1         4 = 256x256, 8 waves, fetch mode 2
-//   5 = 128x128, 4 waves, fetch mode 2               6 = 256x256, 4 waves, fetch mode 2
-//   7 = 256x256, 8 waves, k=32 stages, 5 in flight (160 KiB), fetch mode 2
-//   8 = 256x256, 8 waves, fetch mode 3 (asm DMA + L2 prefetch)
-//   9 = 128x128, 4 waves, fetch mode 3
-//  10 = 128x128, 2 k-groups of 4 waves, fetch mode 3   11 = the same with fetch mode 2
-// 0 picks by shape.
-constexpr int kMaxVariant = 11;
-template <int TA, int TB, int EPI>
-static hipError_t launch_tile(const GemmDesc &d, hipStream_t s) {
+// Returns true (and launches) when the shape/alignment admits the direct-to-LDS f16 kernel.
+bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
+    using namespace g16;
+    if (d.dtype != GEMM_F16 || d.K <= 0 || d.K % 64) return false;   // every variant's stage divides 64
+    if (d.tile != 0 && d.tile != 128 && d.tile != 256) return false;
+    if (d.variant < 0 || d.variant > kMaxVariant) return false;
     int v = d.variant;
-    if (v == 0) {
+    if (v == 0) {   // by shape: 256x256 tiles when they fill the chip, else 128x128
         int tile = d.tile;
         if (tile == 0) {
             long t256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
@@ -373,52 +49,11 @@ static hipError_t launch_tile(const GemmDesc &d, hipStream_t s) {
         }
         v = tile == 256 ? 3 : 1;
     }
-    switch (v) {
-        case 1: return launch<128, 2, 2, 64, 2, 0, TA, TB, EPI>(d, s);
-        case 2: return launch<256, 2, 2, 64, 2, 1, TA, TB, EPI>(d, s);
-        case 4: return launch<256, 4, 2, 64, 2, 2, TA, TB, EPI>(d, s);
-        case 5: return launch<128, 2, 2, 64, 2, 2, TA, TB, EPI>(d, s);
-        case 6: return launch<256, 2, 2, 64, 2, 2, TA, TB, EPI>(d, s);
-        case 7: return launch<256, 4, 2, 32, 5, 2, TA, TB, EPI>(d, s);
-        case 8: return launch<256, 4, 2, 64, 2, 3, TA, TB, EPI>(d, s);
-        case 9: return launch<128, 2, 2, 64, 2, 3, TA, TB, EPI>(d, s);
-        case 10: return launch<128, 2, 2, 64, 2, 3, TA, TB, EPI, 2>(d, s);
-        case 11: return launch<128, 2, 2, 64, 2, 2, TA, TB, EPI, 2>(d, s);
-        default: return launch<256, 4, 2, 64, 2, 1, TA, TB, EPI>(d, s);
-    }
-}
-
-template <int TA, int TB>
-static hipError_t launch_epi(const GemmDesc &d, hipStream_t s) {
-    switch (d.epi) {
-        case EPI_STORE: return launch_tile<TA, TB, EPI_STORE>(d, s);
-        case EPI_BIAS: return launch_tile<TA, TB, EPI_BIAS>(d, s);
-        case EPI_BIAS_RELU: return launch_tile<TA, TB, EPI_BIAS_RELU>(d, s);
-        case EPI_MSE: return launch_tile<TA, TB, EPI_MSE>(d, s);
-        case EPI_MASK: return launch_tile<TA, TB, EPI_MASK>(d, s);
-        case EPI_SGD: return launch_tile<TA, TB, EPI_SGD>(d, s);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-}  // namespace g16
-
-// Returns true (and launches) when the shape/alignment admits the direct-to-LDS f16 kernel.
-bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
-    using namespace g16;
-    if (d.dtype != GEMM_F16 || d.K <= 0 || d.K % 64) return false;
-    if ((d.variant == 10 || d.variant == 11) && d.K % 128) return false;   // two k-groups of whole stages   // every variant's stage divides 64
-    if (d.tile != 0 && d.tile != 128 && d.tile != 256) return false;
-    if (d.variant < 0 || d.variant > kMaxVariant) return false;
+    if (d.K % (64 * variant_kgroups(v))) return false;   // k-groups contract whole stages
     bool ok = (d.ta ? operand_ok<1>(d.A, d.lda, d.M) : operand_ok<0>(d.A, d.lda, d.M)) &&
               (d.tb ? operand_ok<1>(d.B, d.ldb, d.N) : operand_ok<0>(d.B, d.ldb, d.N));
     if (!ok) return false;
-    switch (d.ta * 2 + d.tb) {
-        case 0: *err = launch_epi<0, 0>(d, s); break;
-        case 1: *err = launch_epi<0, 1>(d, s); break;
-        case 2: *err = launch_epi<1, 0>(d, s); break;
-        default: *err = launch_epi<1, 1>(d, s); break;
-    }
+    *err = kVariants[v](d, s);
     return true;
 }
 

@@ -137,6 +137,10 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
     constexpr int G = EPI == EPI_MSE ? 4 : 8;   // row groups whose inputs are loaded together
     typedef typename Vec4<T>::type T4;
     float lossp = 0.0f;
+    // Scalars are read into locals: a struct field multiplied into a vector is lowered as a 16-byte
+    // vector load at the field's address, which pins that part of the argument struct in memory.
+    const float sc = d.scale, lr = d.lr;
+    float *const colsum = d.colsum;
     const int c4 = (lane & 15) * 4;
 #pragma unroll
     for (int jp = 0; jp < FN / 2; jp++) {
@@ -174,7 +178,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
                 const floatx4 a = *(const floatx4 *)(wlds + epi_lds_off(row, jp * 0 + c4));
                 floatx4 v;
                 if constexpr (EPI == EPI_STORE) {
-                    v = d.scale * a;
+                    v = sc * a;
                     T4 o = {(T)v[0], (T)v[1], (T)v[2], (T)v[3]};
                     *(T4 *)((T *)d.C + m * d.ldc + n) = o;
                 } else if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RELU) {
@@ -201,14 +205,14 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
                     T4 o;
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        v[e] = relu_dead(in[u][e]) ? 0.0f : d.scale * a[e];
+                        v[e] = relu_dead(in[u][e]) ? 0.0f : sc * a[e];
                         o[e] = (T)v[e];
                     }
                     *(T4 *)((T *)d.C + m * d.ldc + n) = o;
                 } else {  // EPI_SGD
-                    const floatx4 g = d.scale * a;
+                    const floatx4 g = sc * a;
                     if (d.gout) *(floatx4 *)(d.gout + m * d.ldc + n) = g;
-                    const floatx4 w = in[u] - d.lr * g;
+                    const floatx4 w = in[u] - lr * g;
                     *(floatx4 *)(d.W32 + m * d.ldc + n) = w;
                     if (d.W16) {
                         typedef half_t h4 __attribute__((ext_vector_type(4)));
@@ -220,13 +224,13 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
                 cs += v;
             }
         }
-        if (d.colsum) {
+        if (colsum) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 float x = cs[e];
                 x += __shfl_xor(x, 16, 64);
                 x += __shfl_xor(x, 32, 64);
-                if (lane < 16) atomicAdd(d.colsum + n + e, x);
+                if (lane < 16) atomicAdd(colsum + n + e, x);
             }
         }
         __builtin_amdgcn_wave_barrier();

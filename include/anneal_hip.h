@@ -171,8 +171,8 @@ typedef struct {
     float *gout;
     float *lossacc;
     int32_t tile;           /* 0 = auto, 64, 128, 256 */
-    int32_t variant;        /* f16 kernel variant: 0 = auto (the tuned choice if any), 1..11 = fixed tile /
-                               wave / fetch / k-group choices (gemm16.hip);
+    int32_t variant;        /* f16 kernel variant: 0 = auto (the tuned choice if any), 1..25 = fixed tile /
+                               wave / fetch / k-group choices (table Var<V>, gemm16_kernel.h);
                                the knob a BEAM-style search times (codegen/beam.go:41-541) */
 } ah_gemm_desc;
 int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
@@ -182,9 +182,10 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * describes (iterations launches each, after one warm-up, on the device stream with hipEvents), returns
  * the fastest and its mean time, and caches the choice on the device: later launches of the same
  * (ta, tb, M, N, K) with variant 0 use it. d is launched as given, so its outputs must be scratch
- * (the epilogue runs (iterations + 1) times per variant). Variants 1-9 differ only in tiling and
- * scheduling and accumulate each output over k in the same order (bit-identical results); variants
- * 10-11 add two k-halves, which rounds differently in f32 (relative 1e-6 level). */
+ * (the epilogue runs (iterations + 1) times per variant). Variants without k-groups differ only in
+ * tiling and scheduling and accumulate each output over k in the same order (bit-identical results);
+ * the k-group variants 10, 11, 15 and 25 add two k-halves, which rounds differently in f32 (relative
+ * 1e-6 level). */
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us);
 /* BEAM's disk cache (codegen/beam.go:118-169): save (save != 0) the device's tuned choices to path, one
  * "dtype/ta/tb/M/N/K variant" line each under a header naming the gfx arch, or merge a saved file into
