@@ -184,11 +184,11 @@ def main():
     for _ in range(args.warmup):
         t.step(batch)
     dev.sync()
-    # Calibration (outside the timed region): each kernel's average duration over 3 steps.
+    # Calibration (outside the timed region): each kernel's average duration over 10 steps.
     per = []
     for i in range(nk):
         t.probe(i)
-        for _ in range(3):
+        for _ in range(10):
             t.step(batch)
         ms, n = t.probe_read()
         per.append(ms / max(n, 1))
