@@ -168,6 +168,9 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
 // 5: asm DMAs as in 4, but interleaved one per MFMA (or per few MFMAs) through the k-step that follows
 //    the stage barrier, so that a wave never stalls its MFMA issue behind a burst of vector-memory
 //    instructions (needs XB; the k-step after the barrier is the last one of the previous stage).
+// 6: like 5, and in the other k-steps the fragment reads of k-step s+1 are placed one (or a few)
+//    per MFMA at the start of k-step s (scheduling-group barriers), leaving the last MFMAs of the
+//    k-step to cover the read latency instead of letting reads cluster at its end.
 // XB: cross-barrier fragment prefetch (fetch modes 2-4). The wait and barrier for stage k+1 move in
 // front of the last k-step of stage k, so the first fragment reads of stage k+1 are in flight during
 // the last MFMAs of stage k instead of being exposed after the barrier.
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     constexpr int SMEM = KG * SMEMG > SMEMR ? KG * SMEMG : SMEMR;
     static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
     static_assert(!XB || FETCH >= 2, "cross-barrier prefetch needs the fetches grouped at the barrier");
-    static_assert(FETCH != 5 || XB, "fetch mode 5 interleaves the fetches with the k-step after the barrier (XB)");
+    static_assert(FETCH < 5 || XB, "fetch modes 5 and 6 interleave the fetches with the k-step after the barrier (XB)");
     __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
     const int tiles_n = (d.N + BN - 1) / BN;
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     auto issue_grouped = [&](int kt, bool all_modes = false) {
         char *nxt = gsm + ((kt + NS - 1) % NS) * STAGE;
         const int kn = min(kt + NS - 1, nk - 1) * BK;
-        if (FETCH == 5 && !all_modes) {
+        if (FETCH >= 5 && !all_modes) {
             // mode 5 issues these between the MFMAs that follow
         } else if constexpr (FETCH == 2) {
 #ifndef AH_EXP_NOFETCH
@@ -322,11 +325,12 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
         for (int s = 0; s < KS; s++) {
             const int c = s & 1, n = c ^ 1;
             if (s + 1 < KS) {
+                if constexpr (FETCH == 6) __builtin_amdgcn_sched_barrier(0);   // one region per k-step
 #pragma unroll
                 for (int i = 0; i < FM; i++) a[n][i] = frag<BM, TA, BK>(sa, wm0 + i * 32, s + 1, lane);
 #pragma unroll
                 for (int j = 0; j < FN; j++) b[n][j] = frag<BN, TB, BK>(sb, wn0 + j * 32, s + 1, lane);
-                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (FETCH != 6) __builtin_amdgcn_sched_barrier(0);
             } else if constexpr (XB) {
                 // Open stage kt+1 now (KS is even, so its first fragments go to slot n = 0). In the
                 // last iteration this reads a re-fetched copy of the last stage, which is unused. The
@@ -344,13 +348,13 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
             // mode 5: the refill of stage kt's buffer with stage kt+NS, one DMA after every MPD MFMAs
             constexpr int MPD = NM >= PERSTAGE ? NM / PERSTAGE : 1;
             constexpr int DPM = NM >= PERSTAGE ? 1 : PERSTAGE / NM;
-            static_assert(FETCH != 5 || MPD * PERSTAGE == NM || DPM * NM == PERSTAGE, "DMAs must spread evenly");
+            static_assert(FETCH < 5 || MPD * PERSTAGE == NM || DPM * NM == PERSTAGE, "DMAs must spread evenly");
             char *refill = gsm + (kt % NS) * STAGE;
             const int kr = min(kt + NS, nk - 1) * BK;
 #pragma unroll
             for (int t = 0; t < NM; t++) {
                 acc[t / FN][t % FN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][t / FN], b[c][t % FN], acc[t / FN][t % FN], 0, 0, 0);
-                if constexpr (FETCH == 5) {
+                if constexpr (FETCH >= 5) {
                     if (s == KS - 1 && t % MPD == MPD - 1) {
 #pragma unroll
                         for (int q = 0; q < DPM; q++) {
@@ -370,6 +374,21 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
                     else if (f < PERSTAGE) fb.issue_one(f - PA, Bb, d.ldb, kn, nxt + ABYTES, wave);
 #endif
                     __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if constexpr (FETCH == 6) {
+                if (s + 1 < KS) {
+                    // ds reads of k-step s+1 (two per fragment for the transposing read): RPM after
+                    // each of the first MFMAs, then the rest of the MFMAs
+                    constexpr int NR = (TA ? 2 : 1) * FM + (TB ? 2 : 1) * FN;
+                    constexpr int RPM = (NR + NM - 1) / NM;
+                    constexpr int NMR = (NR + RPM - 1) / RPM;
+#pragma unroll
+                    for (int q = 0; q < NMR; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // one MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);   // then RPM LDS reads
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, NM - NMR, 0);
                 }
             }
         }
@@ -463,8 +482,11 @@ AH_G16_VAR(22, 256, 2, 2, 64, 2, 5, true, 1)
 AH_G16_VAR(23, 256, 4, 2, 64, 2, 5, true, 1)
 AH_G16_VAR(24, 128, 2, 2, 64, 3, 5, true, 1)
 AH_G16_VAR(25, 128, 2, 2, 64, 2, 5, true, 2)
+AH_G16_VAR(26, 256, 2, 2, 64, 2, 6, true, 1)
+AH_G16_VAR(27, 256, 4, 2, 64, 2, 6, true, 1)
+AH_G16_VAR(28, 128, 2, 2, 64, 2, 6, true, 2)
 #undef AH_G16_VAR
-constexpr int kMaxVariant = 25;
+constexpr int kMaxVariant = 28;
 
 template <int V, int TA, int TB>
 static hipError_t run_epi(const GemmDesc &d, hipStream_t s) {

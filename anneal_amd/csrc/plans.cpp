@@ -104,7 +104,7 @@ static int copy_in_f16(ah_device *d, half_t *dst, const float *src, size_t n) {
 
 // ── GEMM variant tuning ─────────────────────────────────────────────────────
 
-constexpr int kGemm16Variants = 25;
+constexpr int kGemm16Variants = 28;
 
 static std::string tune_key(const GemmDesc &g) {
     char b[96];
