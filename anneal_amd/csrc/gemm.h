@@ -44,6 +44,13 @@ struct GemmDesc {
     float *lossacc;   // EPI_MSE scalar accumulator
     int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
     int variant;      // f16 kernel variant (0 = auto; table Var<V> in gemm16_kernel.h), the tuning hook
+    // Deterministic partial sums instead of atomics (0 = atomic accumulation into colsum[N] / lossacc[0]):
+    // with colsum_ld > 0 each wave stores the column sums of its rows, which start at a multiple of 32,
+    // to colsum[(row / 32) * colsum_ld + n]; with loss_ld > 0 each wave stores its MSE partial to
+    // lossacc[(row / 32) * loss_ld + col / 32] (row, col: the wave tile's first element). Entries no
+    // wave writes are left as they are, so the reader sums every entry and re-zeroes it.
+    int colsum_ld;
+    int loss_ld;
     // The float scalars sit beside the ints, away from the pointers: the compiler may merge loads of
     // neighbouring fields into one vector, and a vector mixing pointers and floats is kept in memory.
     float scale;

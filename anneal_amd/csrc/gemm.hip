@@ -387,8 +387,10 @@ __global__ __launch_bounds__(256) void gemm_dot_kernel(GemmDesc d) {
     if constexpr (EPI == EPI_MASK || EPI == EPI_MSE) in = (float)((const T *)d.aux)[(long)m * d.ldaux + n];
     if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RELU || EPI == EPI_MSE) bias = (float)((const T *)d.bias)[n];
     const float cs = epi_apply<EPI, T>(d, m, n, acc, in, bias, lossp);
-    if (d.colsum) atomicAdd(d.colsum + n, cs);
-    if constexpr (EPI == EPI_MSE) atomicAdd(d.lossacc, lossp);
+    // One wave per output: the partial-sum layouts (GemmDesc::colsum_ld / loss_ld) are filled with
+    // atomics here, as 32 waves share each row-block cell (this path serves only small outputs).
+    if (d.colsum) atomicAdd(d.colsum + (d.colsum_ld ? (long)(m / 32) * d.colsum_ld : 0) + n, cs);
+    if constexpr (EPI == EPI_MSE) atomicAdd(d.lossacc + (d.loss_ld ? (long)(m / 32) * d.loss_ld + n / 32 : 0), lossp);
 }
 
 template <typename T>

@@ -93,12 +93,18 @@ __device__ __forceinline__ void epilogue_impl(const GemmDesc &d, const floatx16 
             }
         if (d.colsum) {
             cs += __shfl_xor(cs, 32, 64);
-            if (lane < 32 && nv) atomicAdd(d.colsum + n, cs);
+            if (lane < 32 && nv) {
+                if (d.colsum_ld) d.colsum[(long)(mb / 32) * d.colsum_ld + n] = cs;
+                else atomicAdd(d.colsum + n, cs);
+            }
         }
     }
     if constexpr (EPI == EPI_MSE) {
         lossp = wave_sum(lossp);
-        if (lane == 0) atomicAdd(d.lossacc, lossp);
+        if (lane == 0) {
+            if (d.loss_ld) d.lossacc[(long)(mb / 32) * d.loss_ld + nb / 32] = lossp;
+            else atomicAdd(d.lossacc, lossp);
+        }
     }
 }
 
@@ -141,6 +147,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
     // vector load at the field's address, which pins that part of the argument struct in memory.
     const float sc = d.scale, lr = d.lr;
     float *const colsum = d.colsum;
+    const int colsum_ld = d.colsum_ld;
     const int c4 = (lane & 15) * 4;
 #pragma unroll
     for (int jp = 0; jp < FN / 2; jp++) {
@@ -230,14 +237,25 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
                 float x = cs[e];
                 x += __shfl_xor(x, 16, 64);
                 x += __shfl_xor(x, 32, 64);
-                if (lane < 16) atomicAdd(colsum + n + e, x);
+                cs[e] = x;
+            }
+            if (lane < 16) {
+                float *const row = colsum + (long)(mb / 32) * colsum_ld;   // colsum itself when atomic
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (colsum_ld) row[n + e] = cs[e];
+                    else atomicAdd(colsum + n + e, cs[e]);
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();
     }
     if constexpr (EPI == EPI_MSE) {
         lossp = wave_sum(lossp);
-        if (lane == 0) atomicAdd(d.lossacc, lossp);
+        if (lane == 0) {
+            if (d.loss_ld) d.lossacc[(long)(mb / 32) * d.loss_ld + nb / 32] = lossp;
+            else atomicAdd(d.lossacc, lossp);
+        }
     }
 }
 

@@ -249,13 +249,23 @@ struct Mlp3Trainer : ah_trainer {
         rc |= alloc(&b3, D3); rc |= alloc(&b3h, D3);
         rc |= alloc(&H1, (size_t)B * D1); rc |= alloc(&H2, (size_t)B * D2); rc |= alloc(&Dd, (size_t)B * D3);
         rc |= alloc(&dZ2, (size_t)B * D2); rc |= alloc(&dZ1, (size_t)B * D1);
-        rc |= alloc(&acc, D1 + D2 + D3 + 1); rc |= alloc(&loss, 1);
+        rc |= alloc(&acc, acc_floats()); rc |= alloc(&loss, 1);
         rc |= alloc(&gW1, (size_t)D1 * D0); rc |= alloc(&gW2, (size_t)D2 * D1); rc |= alloc(&gW3, (size_t)D3 * D2);
         rc |= alloc(&gb1, D1); rc |= alloc(&gb2, D2); rc |= alloc(&gb3, D3);
         if (rc) return AH_ERR_HIP;
-        AH_HIP(hipMemset(acc, 0, sizeof(float) * (D1 + D2 + D3 + 1)));
+        AH_HIP(hipMemset(acc, 0, sizeof(float) * acc_floats()));
         return tune();
     }
+    // Bias-gradient and loss accumulators as deterministic per-wave partials (GemmDesc::colsum_ld,
+    // loss_ld): R = ceil(B/32) row blocks of db1 [D1], db2 [D2], db3 [D3], then R x L loss partials
+    // (L = ceil(D3/32)); the step tail sums them in row order and re-zeroes them.
+    int rblocks() const { return (B + 31) / 32; }
+    int lblocks() const { return (D3 + 31) / 32; }
+    size_t acc_floats() const { return (size_t)rblocks() * (D1 + D2 + D3 + lblocks()); }
+    float *db1p() const { return acc; }
+    float *db2p() const { return acc + (size_t)rblocks() * D1; }
+    float *db3p() const { return acc + (size_t)rblocks() * (D1 + D2); }
+    float *lossp() const { return acc + (size_t)rblocks() * (D1 + D2 + D3); }
     int max_batch() const override { return B; }
     int set(int slot, const void *h, int64_t n) override {
         const float *f = (const float *)h;
@@ -296,7 +306,7 @@ struct Mlp3Trainer : ah_trainer {
     GemmDesc gemm(int i, bool sg) const {
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
-        float *db1 = acc, *db2 = acc + D1, *db3 = acc + D1 + D2, *lacc = acc + D1 + D2 + D3;
+        float *db1 = db1p(), *db2 = db2p(), *db3 = db3p(), *lacc = lossp();
         GemmDesc g;
         switch (i) {
             case 0: g = gdesc(GEMM_F16, EPI_BIAS_RELU, 0, 0, B, D1, D0, X, D0, W1h, D0, H1, D1); g.bias = b1h; break;
@@ -304,10 +314,11 @@ struct Mlp3Trainer : ah_trainer {
             case 2:
                 g = gdesc(GEMM_F16, EPI_MSE, 0, 0, B, D3, D2, H2, D2, W3h, D2, Dd, D3);
                 g.bias = b3h; g.aux = T; g.ldaux = D3; g.colsum = db3; g.lossacc = lacc;
+                g.colsum_ld = D3; g.loss_ld = lblocks();
                 break;
             case 3:
                 g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D2, D3, Dd, D3, W3h, D2, dZ2, D2);
-                g.aux = H2; g.ldaux = D2; g.colsum = db2;
+                g.aux = H2; g.ldaux = D2; g.colsum = db2; g.colsum_ld = D2;
                 break;
             case 4:
                 g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D3, D2, B, Dd, D3, H2, D2, nullptr, D2);
@@ -315,7 +326,7 @@ struct Mlp3Trainer : ah_trainer {
                 break;
             case 5:
                 g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D1, D2, dZ2, D2, W2h, D1, dZ1, D1);
-                g.aux = H1; g.ldaux = D1; g.colsum = db1;
+                g.aux = H1; g.ldaux = D1; g.colsum = db1; g.colsum_ld = D1;
                 break;
             case 6:
                 g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D2, D1, B, dZ2, D2, H1, D1, nullptr, D1);
@@ -329,7 +340,9 @@ struct Mlp3Trainer : ah_trainer {
         return g;
     }
     // Variant selection for the step's contractions (BEAM over the f16 kernels): each is timed with
-    // a store epilogue into scratch, so tuning touches no parameter, accumulator or activation.
+    // its own epilogue (register pressure and epilogue traffic differ between epilogues), reading the
+    // real operands, bias and activations but writing only to scratch, so tuning changes no
+    // parameter, accumulator or activation.
     int tune() {
         // BEAM's disk cache (codegen/beam.go:118-169): with AH_GEMM_TUNE_CACHE naming a file, earlier
         // choices are loaded first and the file is rewritten after tuning.
@@ -343,16 +356,27 @@ struct Mlp3Trainer : ah_trainer {
             GemmDesc g = gemm(i, false);
             most = std::max(most, (size_t)g.M * g.N);
         }
-        half_t *scratch = nullptr;
-        AH_HIP(hipMalloc(&scratch, most * sizeof(half_t)));
+        half_t *s16 = nullptr;
+        float *s32 = nullptr;
         int rc = AH_OK;
+        if (hipMalloc(&s16, most * sizeof(half_t)) != hipSuccess || hipMalloc(&s32, most * sizeof(float)) != hipSuccess ||
+            hipMemset(s32, 0, most * sizeof(float)) != hipSuccess)
+            rc = set_error(AH_ERR_HIP, "MLP3: tuning scratch");
         for (int i = 0; i < kGemms && rc == AH_OK; i++) {
             GemmDesc g = gemm(i, false);
             if (dev->gemm_variant.count(tune_key(g))) continue;
-            g.epi = EPI_STORE; g.C = scratch; g.ldc = g.N; g.colsum = nullptr; g.lossacc = nullptr;
-            rc = tune_gemm(dev, g, 3, nullptr, nullptr);
+            if (g.epi == EPI_SGD) {
+                g.W32 = s32; g.W16 = s16; g.gout = nullptr;
+            } else {
+                // the partial sums (at most ceil(M/32) x N values) go to s32, which no other output uses
+                g.C = s16;
+                if (g.colsum) g.colsum = s32;
+                if (g.lossacc) g.lossacc = s32;
+            }
+            rc = tune_gemm(dev, g, 4, nullptr, nullptr);
         }
-        hipFree(scratch);
+        hipFree(s16);
+        hipFree(s32);
         if (rc == AH_OK && cache && *cache) rc = ah_gemm_tune_cache(dev, cache, 1);
         return rc;
     }
@@ -362,14 +386,15 @@ struct Mlp3Trainer : ah_trainer {
         const bool sg = flags & AH_STEP_STORE_GRADS;
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
-        float *db1 = acc, *db2 = acc + D1, *db3 = acc + D1 + D2, *lacc = acc + D1 + D2 + D3;
         static const char *names[kGemms] = {"fc1", "fc2", "fc3_mse", "dH2", "dW3", "dH1", "dW2", "dW1"};
         for (int i = 0; i < kGemms; i++) LAUNCH(names[i], gemm_run(dev, gemm(i, sg), s));
         TailArgs ta{};
-        ta.seg[0] = {b3, b3h, db3, sg ? gb3 : nullptr, D3, bs};
-        ta.seg[1] = {b2, b2h, db2, sg ? gb2 : nullptr, D2, bs};
-        ta.seg[2] = {b1, b1h, db1, sg ? gb1 : nullptr, D1, bs};
-        ta.nseg = 3; ta.lr = lr; ta.loss_mode = 1; ta.lossacc = lacc; ta.loss_scale = sc; ta.loss_out = loss;
+        const int R = rblocks();
+        ta.seg[0] = {b3, b3h, db3p(), sg ? gb3 : nullptr, D3, bs, R, D3};
+        ta.seg[1] = {b2, b2h, db2p(), sg ? gb2 : nullptr, D2, bs, R, D2};
+        ta.seg[2] = {b1, b1h, db1p(), sg ? gb1 : nullptr, D1, bs, R, D1};
+        ta.nseg = 3; ta.lr = lr; ta.loss_mode = 1; ta.lossacc = lossp(); ta.loss_parts = R * lblocks();
+        ta.loss_scale = sc; ta.loss_out = loss;
         LAUNCH("tail", step_tail(ta, s));
         return AH_OK;
     }

@@ -24,6 +24,8 @@ struct TailSeg {
     float *gout;     // optional gradient output
     long n;
     float scale;     // gradient = scale * acc
+    int acc_rows;    // > 0: acc holds acc_rows partial rows (row stride acc_ld), summed in row order
+    long acc_ld;
 };
 struct TailArgs {
     TailSeg seg[4];
@@ -31,6 +33,7 @@ struct TailArgs {
     float lr;
     int loss_mode;   // 0 none, 1 f16-narrowed accumulator * loss_scale, 2 sum(rowloss) * loss_scale
     float *lossacc;
+    int loss_parts;  // loss_mode 1: > 0 sums lossacc[0 .. loss_parts) in a fixed order (and re-zeroes)
     float loss_scale;
     const float *rowloss;
     int nrow;

@@ -323,11 +323,37 @@ __global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, 
 }
 
 // ── step tail: bias SGD for several parameters + loss finalize, in one launch ─────
-// Each accumulator element is read and re-zeroed by the same thread, leaving the accumulators
-// ready for the next step's atomics (no separate zero-fill launch).
+// Each accumulator element (or partial-row entry) is read and re-zeroed by the thread that sums it,
+// leaving the accumulators ready for the next step's atomics or partial stores (no zero-fill launch).
 __global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
     if (blockIdx.x == 0) {
-        if (t.loss_mode == 1) {
+        if (t.loss_mode == 1 && t.loss_parts > 0) {
+            // per-wave partials, summed in a fixed order, then the f16(acc) narrowing (lower.go:712)
+            __shared__ float red[256];
+            float acc = 0.0f;
+            int i = threadIdx.x;
+            for (; i + 7 * 256 < t.loss_parts; i += 8 * 256) {   // 8 loads in flight, then the zeroing
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = t.lossacc[i + j * 256];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    acc += v[j];
+                    t.lossacc[i + j * 256] = 0.0f;
+                }
+            }
+            for (; i < t.loss_parts; i += 256) {
+                acc += t.lossacc[i];
+                t.lossacc[i] = 0.0f;
+            }
+            red[threadIdx.x] = acc;
+            __syncthreads();
+            for (int o = 128; o > 0; o >>= 1) {
+                if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+                __syncthreads();
+            }
+            if (threadIdx.x == 0) t.loss_out[0] = q16(red[0]) * t.loss_scale;
+        } else if (t.loss_mode == 1) {
             if (threadIdx.x == 0) {
                 t.loss_out[0] = q16(t.lossacc[0]) * t.loss_scale;   // f16(acc) narrowing, lower.go:712
                 t.lossacc[0] = 0.0f;
@@ -345,26 +371,62 @@ __global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
             if (threadIdx.x == 0) t.loss_out[0] = red[0] * t.loss_scale;
         }
     }
+    // 16 elements per block pass; the rows of a partial-row accumulator are split into 16 chunks
+    // summed by 16 threads (8 loads in flight each) and combined in a fixed order, so the result is
+    // deterministic.
     long total = 0;
     for (int s = 0; s < t.nseg; s++) total += t.seg[s].n;
-    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    __shared__ float part[16][16];
+    const int e = threadIdx.x & 15, q = threadIdx.x >> 4;
+    for (long base = (long)blockIdx.x * 16; base < total; base += (long)gridDim.x * 16) {
+        const long i = base + e;
         long k = i;
         int s = 0;
-        while (k >= t.seg[s].n) { k -= t.seg[s].n; s++; }
+        if (i < total)
+            while (k >= t.seg[s].n) { k -= t.seg[s].n; s++; }
         const TailSeg &g = t.seg[s];
-        const float gv = g.scale * g.acc[k];
-        g.acc[k] = 0.0f;
-        if (g.gout) g.gout[k] = gv;
-        const float w = g.p[k] - t.lr * gv;
-        g.p[k] = w;
-        if (g.p16) g.p16[k] = (half_t)w;
+        float a = 0.0f;
+        if (i < total) {
+            if (g.acc_rows > 0) {
+                const int rq = (g.acc_rows + 15) / 16, r0 = q * rq, r1 = min(r0 + rq, g.acc_rows);
+                float p[8] = {};
+                int r = r0;
+                for (; r + 8 <= r1; r += 8) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) p[j] += g.acc[(r + j) * g.acc_ld + k];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) g.acc[(r + j) * g.acc_ld + k] = 0.0f;
+                }
+                for (int j = 0; r < r1; r++, j++) {
+                    p[j] += g.acc[r * g.acc_ld + k];
+                    g.acc[r * g.acc_ld + k] = 0.0f;
+                }
+                a = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            } else if (q == 0) {
+                a = g.acc[k];
+                g.acc[k] = 0.0f;
+            }
+        }
+        part[q][e] = a;
+        __syncthreads();
+        if (q == 0 && i < total) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 16; c++) sum += part[c][e];
+            const float gv = g.scale * sum;
+            if (g.gout) g.gout[k] = gv;
+            const float w = g.p[k] - t.lr * gv;
+            g.p[k] = w;
+            if (g.p16) g.p16[k] = (half_t)w;
+        }
+        __syncthreads();
     }
 }
 
 hipError_t step_tail(const TailArgs &t, hipStream_t s) {
     long total = 0;
     for (int i = 0; i < t.nseg; i++) total += t.seg[i].n;
-    int blocks = (int)std::min<long>(std::max<long>((total + 255) / 256, 1), 1024);
+    int blocks = (int)std::min<long>(std::max<long>((total + 15) / 16, 1), 2048);
     hipLaunchKernelGGL(tail_kernel, dim3(blocks), dim3(256), 0, s, t);
     return hipGetLastError();
 }

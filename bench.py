@@ -1,6 +1,7 @@
 """Benchmark of anneal's training hot path on one MI355X.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+  python bench.py --library-probe     (config-3 GEMM shapes here vs hipBLASLt, store epilogue)
 
 One "step" is one full training step of a BASELINE config (forward, backward, SGD) with inputs and
 parameters resident in HBM. Prints ONE JSON line: steps/s for the config, the roofline of its dominant
@@ -27,7 +28,7 @@ PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
 
 # HBM bytes per launch of the dominant kernels, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
 # scaled by a plain copy of known size (read factor 2.0, write factor 1.0): profiles/hbm_traffic_pmc.md.
-TRAFFIC_BYTES = {(3, "dW2"): 272.2e6 + 100.7e6, (5, "chain_grad"): 134.4e6 + 134.4e6,
+TRAFFIC_BYTES = {(3, "dW2"): 268.6e6 + 100.7e6, (5, "chain_grad"): 134.4e6 + 134.4e6,
                  (5, "chain_stats"): 134.3e6 + 4.2e6}
 
 
@@ -153,6 +154,53 @@ def copy_probe(mib: int):
     print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}))
 
 
+def library_probe():
+    """The eight config-3 contractions with a plain f16 store epilogue: this library (each shape tuned,
+    then timed) next to hipBLASLt (torch.matmul on the same layouts), 20 launches each, hipEvents."""
+    import torch
+    from anneal_amd import _lib as L
+    from anneal_amd.backend import Device
+    dev = Device(0)
+    B, D0, D1, D2, D3 = 4096, 1024, 4096, 4096, 1024
+    shapes = [("fc1", 0, 0, B, D1, D0), ("fc2", 0, 0, B, D2, D1), ("fc3", 0, 0, B, D3, D2), ("dH2", 0, 1, B, D2, D3),
+              ("dW3", 1, 1, D3, D2, B), ("dH1", 0, 1, B, D1, D2), ("dW2", 1, 1, D2, D1, B), ("dW1", 1, 1, D1, D0, B)]
+    rng = np.random.default_rng(0)
+    big = 4096 * 4096
+    A = dev.buffer((rng.standard_normal(big) * 0.1).astype(np.float16), L.AH_F16)
+    Bb = dev.buffer((rng.standard_normal(big) * 0.1).astype(np.float16), L.AH_F16)
+    Cc = dev.buffer(big, L.AH_F16)
+    rows = []
+    for name, ta, tb, M, N, K in shapes:
+        kw = dict(dtype=L.AH_F16, epi=L.EPI_STORE, ta=ta, tb=tb, M=M, N=N, K=K, A=A, B=Bb, lda=M if ta else K,
+                  ldb=N if tb else K, C_out=Cc, ldc=N, scale=1.0)
+        variant, _ = dev.gemm_tune(iterations=3, **kw)
+        for _ in range(3):
+            dev.gemm(**kw)
+        dev.sync()
+        dev.timer_start()
+        for _ in range(20):
+            dev.gemm(**kw)
+        ours = dev.timer_stop() / 20 * 1e3
+        a = torch.randn((K, M) if ta else (M, K), device="cuda", dtype=torch.float16)
+        b = torch.randn((K, N) if tb else (N, K), device="cuda", dtype=torch.float16)
+        a2, b2 = (a.t() if ta else a), (b if tb else b.t())
+        for _ in range(3):
+            c = a2 @ b2
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            c = a2 @ b2
+        e1.record()
+        torch.cuda.synchronize()
+        blas = e0.elapsed_time(e1) / 20 * 1e3
+        fl = 2.0 * M * N * K
+        rows.append({"gemm": name, "M": M, "N": N, "K": K, "ta": ta, "tb": tb, "variant": variant,
+                     "us": round(ours, 1), "tflops": round(fl / ours / 1e6), "hipblaslt_us": round(blas, 1),
+                     "hipblaslt_tflops": round(fl / blas / 1e6)})
+    print(json.dumps({"library_probe": rows}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -163,7 +211,12 @@ def main():
     ap.add_argument("--no-others", action="store_true", help="skip the steps/s of the other configs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 5 times (HBM counter calibration)")
+    ap.add_argument("--library-probe", action="store_true",
+                    help="only time the config-3 contraction shapes here and in hipBLASLt (store epilogue)")
     args = ap.parse_args()
+    if args.library_probe:
+        library_probe()
+        return
     if args.copy_probe:
         copy_probe(args.copy_probe)
         return
