@@ -138,6 +138,27 @@ def test_config3_f16_mlp_step_vs_oracle(dev, shape):
         assert check_update(out[k], p[k], new[k], 2e-2), k
 
 
+def test_config3_steps_bit_repeatable(dev):
+    """The config-3 step has no float atomics (bias gradients and the loss are per-wave partials summed
+    in a fixed order by the step tail), so re-running the same steps from the same state reproduces
+    every gradient, parameter and the loss bit for bit."""
+    B, D0, D1, D2, D3 = 512, 256, 512, 384, 256
+    p = data.mlp3_inputs(B, D0, D1, D2, D3)
+    t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], 1e-3)
+    runs = []
+    for _ in range(2):
+        for k in ("x", "t", "W1", "b1", "W2", "b2", "W3", "b3"):
+            t.set(k, p[k])
+        t.step(B)
+        t.step(B, store_grads=True)
+        runs.append({k: t.get(k, p[k.lstrip("d")].size if k.startswith("d") else p[k].size).view(np.uint32)
+                     for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3", "W1", "b1", "W2", "b2", "W3", "b3")})
+        runs[-1]["loss"] = t.get("loss", 1).view(np.uint32)
+    t.close()
+    for k in runs[0]:
+        np.testing.assert_array_equal(runs[0][k], runs[1][k], err_msg=k)
+
+
 def test_config3_full_size_vs_numpy_restatement(dev):
     """Full config-3 shape (4096x1024 -> 4096 -> 4096 -> 1024): one step vs the blocked numpy
     restatement of the oracle (pinned to the C oracle on CPU). The f16 loss accumulator overflows at
