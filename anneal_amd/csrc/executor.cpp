@@ -285,8 +285,8 @@ int ah_benchmark(ah_device *d, const ah_exec_item *item, int32_t warmup, int32_t
         block[a] = (uint32_t)std::max(1, item->local_size[a]);
     }
     hipEvent_t e0, e1;
-    hipEventCreate(&e0);
-    hipEventCreate(&e1);
+    hipEventCreateWithFlags(&e0, hipEventDisableSystemFence);   // timing only
+    hipEventCreateWithFlags(&e1, hipEventDisableSystemFence);
     std::vector<double> us;
     for (int i = 0; i < warmup + iterations && rc == AH_OK; i++) {
         hipEventRecord(e0, d->stream);

@@ -61,8 +61,10 @@ struct ah_trainer {
         if (probe) {
             if (n_probe >= ev_a.size()) {
                 hipEvent_t a, b;
-                AH_HIP(hipEventCreate(&a));
-                AH_HIP(hipEventCreate(&b));
+                // timing-only events: no system-scope fence (cache writeback and invalidate) at
+                // record time, which would add to the bracketed kernel's measured duration
+                AH_HIP(hipEventCreateWithFlags(&a, hipEventDisableSystemFence));
+                AH_HIP(hipEventCreateWithFlags(&b, hipEventDisableSystemFence));
                 ev_a.push_back(a);
                 ev_b.push_back(b);
             }
@@ -127,8 +129,8 @@ static int tune_gemm(ah_device *dev, GemmDesc g, int iters, int *best, double *b
     if (g.dtype != GEMM_F16) return set_error(AH_ERR_UNSUPPORTED, "gemm tuning covers the f16 kernels");
     if (iters <= 0) return set_error(AH_ERR_INVALID, "gemm tuning: iterations must be > 0");
     hipEvent_t e0, e1;
-    AH_HIP(hipEventCreate(&e0));
-    AH_HIP(hipEventCreate(&e1));
+    AH_HIP(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence));   // timing only
+    AH_HIP(hipEventCreateWithFlags(&e1, hipEventDisableSystemFence));
     int bv = 0;
     float bt = 0.0f;
     hipError_t err = hipSuccess;

@@ -299,8 +299,8 @@ int ah_launch(ah_device *d, ah_kernel *k, const uint32_t grid[3], const uint32_t
 int ah_timer_start(ah_device *d) {
     if (!d) return set_error(AH_ERR_INVALID, "ah_timer_start: null device");
     if (!d->t0) {
-        AH_HIP(hipEventCreate(&d->t0));
-        AH_HIP(hipEventCreate(&d->t1));
+        AH_HIP(hipEventCreateWithFlags(&d->t0, hipEventDisableSystemFence));   // timing only
+        AH_HIP(hipEventCreateWithFlags(&d->t1, hipEventDisableSystemFence));
     }
     AH_HIP(hipEventRecord(d->t0, d->stream));
     return AH_OK;
