@@ -175,9 +175,9 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
 // front of the last k-step of stage k, so the first fragment reads of stage k+1 are in flight during
 // the last MFMAs of stage k instead of being exposed after the barrier.
 // KG: k-groups. With KG = 2 the workgroup holds two sets of WVM x WVN waves on the same tile; group g
-// contracts the g-th half of K through its own LDS stages, and at the end group 1 hands its
-// accumulators to group 0 through LDS, which adds them and runs the epilogue. Two waves then share
-// each SIMD on tiles whose accumulators leave room for only one wave set (the 128x128 tile).
+// contracts the g-th half of K through its own LDS stages; at the end the groups exchange halves of
+// their accumulators through LDS, and each adds and finishes one half of the tile. Two waves then
+// share each SIMD on tiles whose accumulators leave room for only one wave set (the 128x128 tile).
 template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG>
 __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d) {
     constexpr int NW = WVM * WVN;
@@ -395,36 +395,44 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // drain the tail re-fetches before LDS reuse
 
+    const int mb = m0 + wm0, nb = n0 + wn0;
     if constexpr (KG > 1) {
-        // group 1 -> LDS -> group 0: element e of lane l of wave w at [w][e][l] (conflict-free)
+        // The two k-groups split the finish: group g owns 32-row block g of each wave tile (which has
+        // two). Each group hands the other group's block over through LDS (element e of lane l of
+        // wave w at [w][e][l], conflict-free), adds the block it receives, and runs the epilogue on
+        // its own block, so all waves of the workgroup take part in the epilogue traffic.
+        static_assert(KG == 2 && FM == 2, "k-groups split the wave tile's two row blocks");
         constexpr int NE = FM * FN * 16;
         float *red = (float *)smem + wave * NE * 64 + lane;
         __syncthreads();
-        if (kg == 1) {
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+        for (int j = 0; j < FN; j++)
 #pragma unroll
-                for (int j = 0; j < FN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) red[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
-        }
+            for (int r = 0; r < 16; r++) {   // hand over the block the other group owns
+                const float v = kg == 0 ? acc[1][j][r] : acc[0][j][r];
+                red[(((1 - kg) * FN + j) * 16 + r) * 64] = v;
+            }
         __syncthreads();
-        if (kg == 0) {
+        // own block + the other group's partial of it (f32 addition is commutative, so the sum is the
+        // same whichever group adds it)
+        floatx16 mine[1][FN];
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+        for (int j = 0; j < FN; j++)
 #pragma unroll
-                for (int j = 0; j < FN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * FN + j) * 16 + r) * 64];
-        }
+            for (int r = 0; r < 16; r++) {
+                const float own = kg == 0 ? acc[0][j][r] : acc[1][j][r];
+                mine[0][j][r] = own + red[((kg * FN + j) * 16 + r) * 64];
+            }
         __syncthreads();   // the epilogue below reuses this LDS
-        if (kg == 1) return;
+        if constexpr (VEPI)
+            epilogue_lds<EPI, half_t, 1, FN>(d, mine, mb + kg * 32, nb, lane, smem + (kg * NW + wave) * (32 * 256));
+        else
+            epilogue_tile<EPI, half_t, 1, FN>(d, mine, mb + kg * 32, nb, lane);
+        return;
     }
-
-    const int mb = m0 + wm0, nb = n0 + wn0;
     if constexpr (VEPI) {
         // Epilogue through the (now idle) operand LDS: each wave owns FM*32 rows x 64 f32 columns.
-        if constexpr (KG == 1) __syncthreads();
+        __syncthreads();
         epilogue_lds<EPI, half_t, FM, FN>(d, acc, mb, nb, lane, smem + wave * (WM * 256));
     } else {
         epilogue_tile<EPI, half_t, FM, FN>(d, acc, mb, nb, lane);
