@@ -179,10 +179,11 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
 
 /* BEAM over the f16 kernel variants (replaces BeamSearch timing candidate Opt sequences per kernel and
  * caching the winner, codegen/beam.go:41-541, :118-169). Times every variant of the contraction d
- * describes (iterations launches each, after one warm-up, on the device stream with hipEvents), returns
+ * describes (iterations launches each, after one warm-up, on the device stream with hipEvents; two passes,
+ * each variant timed by the lower of its two means), returns
  * the fastest and its mean time, and caches the choice on the device: later launches of the same
  * (ta, tb, M, N, K) with variant 0 use it. d is launched as given, so its outputs must be scratch
- * (the epilogue runs (iterations + 1) times per variant). Variants without k-groups differ only in
+ * (the epilogue runs 2 * (iterations + 1) times per variant). Variants without k-groups differ only in
  * tiling and scheduling and accumulate each output over k in the same order (bit-identical results);
  * the k-group variants 10, 11, 15, 25 and 28 add two k-halves, which rounds differently in f32 (relative
  * 1e-6 level). */
