@@ -49,10 +49,10 @@ __device__ __forceinline__ int mnoff(int k, int m) {
 // with its own explicit s_waitcnt vmcnt. M0 (the DMA's LDS base) is written here; the compiler
 // reserves M0 and warns about the clobber, but no instruction it emits in these kernels reads M0 (no
 // builtin LDS-DMA, no dynamic register indexing on the fetch-mode-3 path), so nothing is disturbed.
-__device__ __forceinline__ void dma16(const char *g, const char *lds) {
-    const uint32_t l = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
-                 "s"(__builtin_amdgcn_readfirstlane(l))
+// The global address is a wave-uniform base in SGPRs plus a 32-bit per-lane offset (the saddr form),
+// and the LDS destination a wave-uniform 32-bit LDS address, so a DMA costs no VALU address work.
+__device__ __forceinline__ void dma16(uint32_t voff, const char *sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                  : "memory", "m0");
 }
 
@@ -108,14 +108,14 @@ struct Fetch {
         __builtin_amdgcn_global_load_lds((const void *)(base + adv + off[j]), (void *)(tile + (wave * PER + j) * 1024),
                                          16, 0, 0);
     }
-    __device__ __forceinline__ void issue_one_asm(int j, const char *base, long ld, int k0, char *tile, int wave) const {
+    // asm DMAs: tile_lds is the tile's 32-bit LDS address and wave is wave-uniform (an SGPR)
+    __device__ __forceinline__ void issue_one_asm(int j, const char *base, long ld, int k0, uint32_t tile_lds, int wave) const {
         const long adv = T == 0 ? (long)k0 * 2 : (long)k0 * ld * 2;
-        dma16(base + adv + off[j], tile + (wave * PER + j) * 1024);
+        dma16(off[j], base + adv, tile_lds + (uint32_t)((wave * PER + j) * 1024));
     }
-    __device__ __forceinline__ void issue_asm(const char *base, long ld, int k0, char *tile, int wave) const {
-        const long adv = T == 0 ? (long)k0 * 2 : (long)k0 * ld * 2;
+    __device__ __forceinline__ void issue_asm(const char *base, long ld, int k0, uint32_t tile_lds, int wave) const {
 #pragma unroll
-        for (int j = 0; j < PER; j++) dma16(base + adv + off[j], tile + (wave * PER + j) * 1024);
+        for (int j = 0; j < PER; j++) issue_one_asm(j, base, ld, k0, tile_lds, wave);
     }
 };
 
@@ -211,6 +211,9 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     const int tid = threadIdx.x - kg * 64 * NW, wave = tid >> 6;                             // within the group
     const int wm0 = (wave / WVN) * WM, wn0 = (wave % WVN) * WN;
     char *gsm = smem + kg * SMEMG;                                                          // the group's LDS
+    // the same region as a 32-bit LDS address, and the wave index as a wave-uniform value, for the asm DMAs
+    const uint32_t gsm_lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)smem + kg * SMEMG;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
     Fetch<BM, TA, BK, NW> fa;
     Fetch<BN, TB, BK, NW> fb;
@@ -244,8 +247,8 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     for (int p = 0; p < NS - 1; p++) {
         const int kp = min(p, nk - 1) * BK;
         if constexpr (FETCH >= 3) {
-            fa.issue_asm(Ab, d.lda, kp, gsm + p * STAGE, wave);
-            fb.issue_asm(Bb, d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
+            fa.issue_asm(Ab, d.lda, kp, gsm_lds + p * STAGE, wave_u);
+            fb.issue_asm(Bb, d.ldb, kp, gsm_lds + p * STAGE + ABYTES, wave_u);
         } else {
             fa.issue(Ab, d.lda, kp, gsm + p * STAGE, wave);
             fb.issue(Bb, d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
@@ -278,8 +281,9 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
 #endif
         } else if constexpr (FETCH >= 3) {
 #ifndef AH_EXP_NOFETCH
-            fa.issue_asm(Ab, d.lda, kn, nxt, wave);
-            fb.issue_asm(Bb, d.ldb, kn, nxt + ABYTES, wave);
+            const uint32_t nxt_lds = gsm_lds + ((kt + NS - 1) % NS) * STAGE;
+            fa.issue_asm(Ab, d.lda, kn, nxt_lds, wave_u);
+            fb.issue_asm(Bb, d.ldb, kn, nxt_lds + ABYTES, wave_u);
             if constexpr (FETCH == 3) prefetch(min(kt + NS, nk - 1) * BK);
 #endif
         }
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
             constexpr int MPD = NM >= PERSTAGE ? NM / PERSTAGE : 1;
             constexpr int DPM = NM >= PERSTAGE ? 1 : PERSTAGE / NM;
             static_assert(FETCH < 5 || MPD * PERSTAGE == NM || DPM * NM == PERSTAGE, "DMAs must spread evenly");
-            char *refill = gsm + (kt % NS) * STAGE;
+            const uint32_t refill_lds = gsm_lds + (kt % NS) * STAGE;
             const int kr = min(kt + NS, nk - 1) * BK;
 #pragma unroll
             for (int t = 0; t < NM; t++) {
@@ -360,8 +364,8 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
                         for (int q = 0; q < DPM; q++) {
                             const int f = (t / MPD) * DPM + q;
 #ifndef AH_EXP_NOFETCH
-                            if (f < PA) fa.issue_one_asm(f, Ab, d.lda, kr, refill, wave);
-                            else fb.issue_one_asm(f - PA, Bb, d.ldb, kr, refill + ABYTES, wave);
+                            if (f < PA) fa.issue_one_asm(f, Ab, d.lda, kr, refill_lds, wave_u);
+                            else fb.issue_one_asm(f - PA, Bb, d.ldb, kr, refill_lds + ABYTES, wave_u);
 #endif
                         }
                         __builtin_amdgcn_sched_barrier(0);
@@ -442,7 +446,9 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
 template <int T>
 static bool operand_ok(const void *p, long ld, int rows) {
     if (((uintptr_t)p & 15) || (ld % 8) || rows < 8) return false;
-    return T == 0 || (rows % 8) == 0;
+    // K-contiguous operands address each lane's row by a 32-bit byte offset from the stage base
+    if (T == 0) return (long)rows * ld * 2 < (1l << 32);
+    return (rows % 8) == 0;
 }
 
 template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, bool XB, int KG, int TA, int TB, int EPI>
