@@ -10,6 +10,7 @@ AH_G16_DECL(8) AH_G16_DECL(9) AH_G16_DECL(10) AH_G16_DECL(11) AH_G16_DECL(12) AH
 AH_G16_DECL(14) AH_G16_DECL(15) AH_G16_DECL(16) AH_G16_DECL(17) AH_G16_DECL(18) AH_G16_DECL(19)
 AH_G16_DECL(20) AH_G16_DECL(21) AH_G16_DECL(22) AH_G16_DECL(23) AH_G16_DECL(24) AH_G16_DECL(25)
 AH_G16_DECL(26) AH_G16_DECL(27) AH_G16_DECL(28)
+AH_G16_DECL(29) AH_G16_DECL(30) AH_G16_DECL(31)
 #undef AH_G16_DECL
 
 namespace {
@@ -20,7 +21,8 @@ const VariantFn kVariants[g16::kMaxVariant + 1] = {
     gemm16_variant_11, gemm16_variant_12, gemm16_variant_13, gemm16_variant_14, gemm16_variant_15,
     gemm16_variant_16, gemm16_variant_17, gemm16_variant_18, gemm16_variant_19, gemm16_variant_20,
     gemm16_variant_21, gemm16_variant_22, gemm16_variant_23, gemm16_variant_24, gemm16_variant_25,
-    gemm16_variant_26, gemm16_variant_27, gemm16_variant_28};
+    gemm16_variant_26, gemm16_variant_27, gemm16_variant_28,
+    gemm16_variant_29, gemm16_variant_30, gemm16_variant_31};
 
 // k-groups of the variant (the K split must give each group whole 64-wide stages)
 int variant_kgroups(int v) {
@@ -31,6 +33,7 @@ int variant_kgroups(int v) {
         AH_G16_KG(14) AH_G16_KG(15) AH_G16_KG(16) AH_G16_KG(17) AH_G16_KG(18) AH_G16_KG(19)
         AH_G16_KG(20) AH_G16_KG(21) AH_G16_KG(22) AH_G16_KG(23) AH_G16_KG(24) AH_G16_KG(25)
         AH_G16_KG(26) AH_G16_KG(27) AH_G16_KG(28)
+        AH_G16_KG(29) AH_G16_KG(30) AH_G16_KG(31)
 #undef AH_G16_KG
         default: return 1;
     }

@@ -171,6 +171,7 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
 // 6: like 5, and in the other k-steps the fragment reads of k-step s+1 are placed one (or a few)
 //    per MFMA at the start of k-step s (scheduling-group barriers), leaving the last MFMAs of the
 //    k-step to cover the read latency instead of letting reads cluster at its end.
+// 7: like 6, with the fragment reads spread evenly over the whole k-step (one every NM/NR MFMAs).
 // XB: cross-barrier fragment prefetch (fetch modes 2-4). The wait and barrier for stage k+1 move in
 // front of the last k-step of stage k, so the first fragment reads of stage k+1 are in flight during
 // the last MFMAs of stage k instead of being exposed after the barrier.
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     constexpr int SMEM = KG * SMEMG > SMEMR ? KG * SMEMG : SMEMR;
     static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
     static_assert(!XB || FETCH >= 2, "cross-barrier prefetch needs the fetches grouped at the barrier");
-    static_assert(FETCH < 5 || XB, "fetch modes 5 and 6 interleave the fetches with the k-step after the barrier (XB)");
+    static_assert(FETCH < 5 || XB, "fetch modes 5-7 interleave the fetches with the k-step after the barrier (XB)");
     __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
     const int tiles_n = (d.N + BN - 1) / BN;
@@ -329,12 +330,12 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
         for (int s = 0; s < KS; s++) {
             const int c = s & 1, n = c ^ 1;
             if (s + 1 < KS) {
-                if constexpr (FETCH == 6) __builtin_amdgcn_sched_barrier(0);   // one region per k-step
+                if constexpr (FETCH >= 6) __builtin_amdgcn_sched_barrier(0);   // one region per k-step
 #pragma unroll
                 for (int i = 0; i < FM; i++) a[n][i] = frag<BM, TA, BK>(sa, wm0 + i * 32, s + 1, lane);
 #pragma unroll
                 for (int j = 0; j < FN; j++) b[n][j] = frag<BN, TB, BK>(sb, wn0 + j * 32, s + 1, lane);
-                if constexpr (FETCH != 6) __builtin_amdgcn_sched_barrier(0);
+                if constexpr (FETCH < 6) __builtin_amdgcn_sched_barrier(0);
             } else if constexpr (XB) {
                 // Open stage kt+1 now (KS is even, so its first fragments go to slot n = 0). In the
                 // last iteration this reads a re-fetched copy of the last stage, which is unused. The
@@ -378,6 +379,22 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
                     else if (f < PERSTAGE) fb.issue_one(f - PA, Bb, d.ldb, kn, nxt + ABYTES, wave);
 #endif
                     __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if constexpr (FETCH == 7) {
+                if (s + 1 < KS) {
+                    // ds reads of k-step s+1 spread evenly: one after every NM/NR MFMAs (or RPM after
+                    // each MFMA when there are more reads than MFMAs)
+                    constexpr int NR = (TA ? 2 : 1) * FM + (TB ? 2 : 1) * FN;
+                    constexpr int RPM = (NR + NM - 1) / NM;
+                    constexpr int MPR = NR >= NM ? 1 : NM / NR;
+                    constexpr int NG = (NR + RPM - 1) / RPM;
+#pragma unroll
+                    for (int q = 0; q < NG; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);
+                    }
+                    if constexpr (NM > NG * MPR) __builtin_amdgcn_sched_group_barrier(0x008, NM - NG * MPR, 0);
                 }
             }
             if constexpr (FETCH == 6) {
@@ -499,8 +516,11 @@ AH_G16_VAR(25, 128, 2, 2, 64, 2, 5, true, 2)
 AH_G16_VAR(26, 256, 2, 2, 64, 2, 6, true, 1)
 AH_G16_VAR(27, 256, 4, 2, 64, 2, 6, true, 1)
 AH_G16_VAR(28, 128, 2, 2, 64, 2, 6, true, 2)
+AH_G16_VAR(29, 256, 2, 2, 64, 2, 7, true, 1)
+AH_G16_VAR(30, 256, 4, 2, 64, 2, 7, true, 1)
+AH_G16_VAR(31, 128, 2, 2, 64, 2, 7, true, 2)
 #undef AH_G16_VAR
-constexpr int kMaxVariant = 28;
+constexpr int kMaxVariant = 31;
 
 template <int V, int TA, int TB>
 static hipError_t run_epi(const GemmDesc &d, hipStream_t s) {

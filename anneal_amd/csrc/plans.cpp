@@ -106,7 +106,7 @@ static int copy_in_f16(ah_device *d, half_t *dst, const float *src, size_t n) {
 
 // ── GEMM variant tuning ─────────────────────────────────────────────────────
 
-constexpr int kGemm16Variants = 28;
+constexpr int kGemm16Variants = 31;
 
 static std::string tune_key(const GemmDesc &g) {
     char b[96];

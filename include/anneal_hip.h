@@ -171,7 +171,7 @@ typedef struct {
     float *gout;
     float *lossacc;
     int32_t tile;           /* 0 = auto, 64, 128, 256 */
-    int32_t variant;        /* f16 kernel variant: 0 = auto (the tuned choice if any), 1..28 = fixed tile /
+    int32_t variant;        /* f16 kernel variant: 0 = auto (the tuned choice if any), 1..31 = fixed tile /
                                wave / fetch / k-group choices (table Var<V>, gemm16_kernel.h);
                                the knob a BEAM-style search times (codegen/beam.go:41-541) */
 } ah_gemm_desc;
@@ -185,7 +185,7 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * (ta, tb, M, N, K) with variant 0 use it. d is launched as given, so its outputs must be scratch
  * (the epilogue runs 2 * (iterations + 1) times per variant). Variants without k-groups differ only in
  * tiling and scheduling and accumulate each output over k in the same order (bit-identical results);
- * the k-group variants 10, 11, 15, 25 and 28 add two k-halves, which rounds differently in f32 (relative
+ * the k-group variants 10, 11, 15, 25, 28 and 31 add two k-halves, which rounds differently in f32 (relative
  * 1e-6 level). */
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us);
 /* BEAM's disk cache (codegen/beam.go:118-169): save (save != 0) the device's tuned choices to path, one
