@@ -45,7 +45,8 @@ __device__ __forceinline__ float epi_apply(const GemmDesc &d, int m, int n, floa
     } else {  // EPI_SGD
         const float g = d.scale * acc;
         if (d.gout) d.gout[ci] = g;
-        const float w = in - d.lr * g;
+        float w = in - d.lr * g;
+        asm volatile("" : "+v"(w));   // W16 is f16 of the stored W32 (no differently rounded fused op)
         d.W32[ci] = w;
         if (d.W16) ((half_t *)d.W16)[ci] = (half_t)w;
         return 0.0f;
@@ -219,7 +220,10 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
                 } else {  // EPI_SGD
                     const floatx4 g = sc * a;
                     if (d.gout) *(floatx4 *)(d.gout + m * d.ldc + n) = g;
-                    const floatx4 w = in[u] - lr * g;
+                    floatx4 w = in[u] - lr * g;
+                    // W16 must be f16 of the stored W32: the empty asm pins w as one f32 value, so the
+                    // compiler cannot fold the f16 conversion into a differently rounded fused op
+                    asm volatile("" : "+v"(w));
                     *(floatx4 *)(d.W32 + m * d.ldc + n) = w;
                     if (d.W16) {
                         typedef half_t h4 __attribute__((ext_vector_type(4)));

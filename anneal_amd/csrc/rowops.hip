@@ -42,6 +42,7 @@ __global__ void sgd_kernel(float *p, const float *g, long n, float lr, float sca
         float gv = scale * g[i];
         if (gout) gout[i] = gv;
         float w = p[i] - lr * gv;
+        asm volatile("" : "+v"(w));   // the f16 copy is f16 of the stored f32 value
         p[i] = w;
         if (p16) p16[i] = (half_t)w;
     }
@@ -415,7 +416,8 @@ __global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
             for (int c = 0; c < 16; c++) sum += part[c][e];
             const float gv = g.scale * sum;
             if (g.gout) g.gout[k] = gv;
-            const float w = g.p[k] - t.lr * gv;
+            float w = g.p[k] - t.lr * gv;
+            asm volatile("" : "+v"(w));   // the f16 copy is f16 of the stored f32 value
             g.p[k] = w;
             if (g.p16) g.p16[k] = (half_t)w;
         }
