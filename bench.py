@@ -221,7 +221,7 @@ def main():
         copy_probe(args.copy_probe)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (see DESIGN.md)",
+        print(json.dumps({"error": "this build runs on one GPU: sharding across GPUs is designed, not built",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
