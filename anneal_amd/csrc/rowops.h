@@ -6,6 +6,8 @@ namespace ah {
 
 constexpr int kChainStatsRows = 128;  // rows per pass-1 block (chunk partials folded per column)
 constexpr int kChainGradRows = 64;    // rows per pass-2 block
+constexpr int kTailCols = 32;         // step tail: elements per block pass (one per thread of a chunk)
+constexpr int kTailChunks = 16;       // step tail: row chunks of a partial-row accumulator
 
 hipError_t fill_f32(float *p, long n, float v, hipStream_t s);
 hipError_t cast_f32_f16(const float *src, half_t *dst, long n, hipStream_t s);

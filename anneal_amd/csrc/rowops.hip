@@ -326,60 +326,58 @@ __global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, 
 // ── step tail: bias SGD for several parameters + loss finalize, in one launch ─────
 // Each accumulator element (or partial-row entry) is read and re-zeroed by the thread that sums it,
 // leaving the accumulators ready for the next step's atomics or partial stores (no zero-fill launch).
-__global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
+__device__ __forceinline__ float block_sum_512(float v, float *red) {   // fixed order: waves, then 8 slots
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+}
+
+__global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
+    static_assert(kTailCols * kTailChunks == 512, "tail block is 512 threads");
     if (blockIdx.x == 0) {
+        __shared__ float red[8];
         if (t.loss_mode == 1 && t.loss_parts > 0) {
             // per-wave partials, summed in a fixed order, then the f16(acc) narrowing (lower.go:712)
-            __shared__ float red[256];
             float acc = 0.0f;
             int i = threadIdx.x;
-            for (; i + 7 * 256 < t.loss_parts; i += 8 * 256) {   // 8 loads in flight, then the zeroing
+            for (; i + 7 * 512 < t.loss_parts; i += 8 * 512) {   // 8 loads in flight, then the zeroing
                 float v[8];
 #pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = t.lossacc[i + j * 256];
+                for (int j = 0; j < 8; j++) v[j] = t.lossacc[i + j * 512];
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     acc += v[j];
-                    t.lossacc[i + j * 256] = 0.0f;
+                    t.lossacc[i + j * 512] = 0.0f;
                 }
             }
-            for (; i < t.loss_parts; i += 256) {
+            for (; i < t.loss_parts; i += 512) {
                 acc += t.lossacc[i];
                 t.lossacc[i] = 0.0f;
             }
-            red[threadIdx.x] = acc;
-            __syncthreads();
-            for (int o = 128; o > 0; o >>= 1) {
-                if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-                __syncthreads();
-            }
-            if (threadIdx.x == 0) t.loss_out[0] = q16(red[0]) * t.loss_scale;
+            acc = block_sum_512(acc, red);
+            if (threadIdx.x == 0) t.loss_out[0] = q16(acc) * t.loss_scale;
         } else if (t.loss_mode == 1) {
             if (threadIdx.x == 0) {
                 t.loss_out[0] = q16(t.lossacc[0]) * t.loss_scale;   // f16(acc) narrowing, lower.go:712
                 t.lossacc[0] = 0.0f;
             }
         } else if (t.loss_mode == 2) {
-            __shared__ float red[256];
             float acc = 0.0f;
-            for (int i = threadIdx.x; i < t.nrow; i += 256) acc += t.rowloss[i];
-            red[threadIdx.x] = acc;
-            __syncthreads();
-            for (int o = 128; o > 0; o >>= 1) {
-                if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-                __syncthreads();
-            }
-            if (threadIdx.x == 0) t.loss_out[0] = red[0] * t.loss_scale;
+            for (int i = threadIdx.x; i < t.nrow; i += 512) acc += t.rowloss[i];
+            acc = block_sum_512(acc, red);
+            if (threadIdx.x == 0) t.loss_out[0] = acc * t.loss_scale;
         }
     }
-    // 16 elements per block pass; the rows of a partial-row accumulator are split into 16 chunks
-    // summed by 16 threads (8 loads in flight each) and combined in a fixed order, so the result is
+    // kTailCols consecutive elements per block pass, so a half-wave reads 128 contiguous bytes of a
+    // partial row; the rows of a partial-row accumulator are split into kTailChunks chunks (up to 16
+    // loads in flight per thread), and the chunk sums are combined in a fixed order, so the result is
     // deterministic.
     long total = 0;
     for (int s = 0; s < t.nseg; s++) total += t.seg[s].n;
-    __shared__ float part[16][16];
-    const int e = threadIdx.x & 15, q = threadIdx.x >> 4;
-    for (long base = (long)blockIdx.x * 16; base < total; base += (long)gridDim.x * 16) {
+    __shared__ float part[kTailChunks][kTailCols];
+    const int e = threadIdx.x % kTailCols, q = threadIdx.x / kTailCols;
+    for (long base = (long)blockIdx.x * kTailCols; base < total; base += (long)gridDim.x * kTailCols) {
         const long i = base + e;
         long k = i;
         int s = 0;
@@ -389,20 +387,25 @@ __global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
         float a = 0.0f;
         if (i < total) {
             if (g.acc_rows > 0) {
-                const int rq = (g.acc_rows + 15) / 16, r0 = q * rq, r1 = min(r0 + rq, g.acc_rows);
-                float p[8] = {};
-                int r = r0;
-                for (; r + 8 <= r1; r += 8) {
+                const int rq = (g.acc_rows + kTailChunks - 1) / kTailChunks, r0 = q * rq;
+                const int r1 = min(r0 + rq, g.acc_rows);
+                float *const col = g.acc + k;
+                float p[16] = {};
+                for (int r = r0; r < r1; r += 16) {   // rows past r1 are predicated off, so p[] stays in registers
+                    float v[16];
 #pragma unroll
-                    for (int j = 0; j < 8; j++) p[j] += g.acc[(r + j) * g.acc_ld + k];
+                    for (int j = 0; j < 16; j++) v[j] = r + j < r1 ? col[(long)(r + j) * g.acc_ld] : 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 8; j++) g.acc[(r + j) * g.acc_ld + k] = 0.0f;
+                    for (int j = 0; j < 16; j++) {
+                        p[j] += v[j];
+                        if (r + j < r1) col[(long)(r + j) * g.acc_ld] = 0.0f;
+                    }
                 }
-                for (int j = 0; r < r1; r++, j++) {
-                    p[j] += g.acc[r * g.acc_ld + k];
-                    g.acc[r * g.acc_ld + k] = 0.0f;
-                }
-                a = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+#pragma unroll
+                for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+                    for (int j = 0; j < w; j++) p[j] += p[j + w];
+                a = p[0];
             } else if (q == 0) {
                 a = g.acc[k];
                 g.acc[k] = 0.0f;
@@ -413,7 +416,7 @@ __global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
         if (q == 0 && i < total) {
             float sum = 0.0f;
 #pragma unroll
-            for (int c = 0; c < 16; c++) sum += part[c][e];
+            for (int c = 0; c < kTailChunks; c++) sum += part[c][e];
             const float gv = g.scale * sum;
             if (g.gout) g.gout[k] = gv;
             float w = g.p[k] - t.lr * gv;
@@ -428,8 +431,8 @@ __global__ __launch_bounds__(256) void tail_kernel(TailArgs t) {
 hipError_t step_tail(const TailArgs &t, hipStream_t s) {
     long total = 0;
     for (int i = 0; i < t.nseg; i++) total += t.seg[i].n;
-    int blocks = (int)std::min<long>(std::max<long>((total + 15) / 16, 1), 2048);
-    hipLaunchKernelGGL(tail_kernel, dim3(blocks), dim3(256), 0, s, t);
+    int blocks = (int)std::min<long>(std::max<long>((total + kTailCols - 1) / kTailCols, 1), 2048);
+    hipLaunchKernelGGL(tail_kernel, dim3(blocks), dim3(kTailCols * kTailChunks), 0, s, t);
     return hipGetLastError();
 }
 
