@@ -10,6 +10,8 @@ constexpr int kTailCols = 32;         // step tail: elements per block pass (one
 constexpr int kTailChunks = 16;       // step tail: row chunks of a partial-row accumulator
 
 hipError_t fill_f32(float *p, long n, float v, hipStream_t s);
+// p[i] and/or p16[i] = amp * (a hash of (seed, i) mapped to [-1, 1)); either pointer may be null.
+hipError_t fill_hash(float *p, half_t *p16, long n, uint32_t seed, float amp, hipStream_t s);
 hipError_t cast_f32_f16(const float *src, half_t *dst, long n, hipStream_t s);
 hipError_t sgd_update(float *p, const float *g, long n, float lr, float scale, half_t *p16, float *gout,
                       hipStream_t s);

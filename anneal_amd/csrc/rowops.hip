@@ -28,6 +28,19 @@ __global__ void fill_f32_kernel(float *p, long n, float v) {
     for (; i < n; i += stride) p[i] = v;
 }
 
+// amp * u, u uniform in [-1, 1) from a 32-bit integer hash of (seed, i); optional f16 copy.
+__global__ void fill_hash_kernel(float *p, half_t *p16, long n, uint32_t seed, float amp) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    long stride = (long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        uint32_t h = (uint32_t)i * 0x9E3779B1u ^ (uint32_t)(i >> 32) ^ seed;
+        h ^= h >> 16; h *= 0x7FEB352Du; h ^= h >> 15; h *= 0x846CA68Bu; h ^= h >> 16;
+        const float v = amp * ((float)(h >> 8) * (1.0f / 8388608.0f) - 1.0f);
+        if (p) p[i] = v;
+        if (p16) p16[i] = (half_t)v;
+    }
+}
+
 __global__ void cast_f32_f16_kernel(const float *src, half_t *dst, long n) {
     long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     long stride = (long)gridDim.x * blockDim.x;
@@ -446,6 +459,11 @@ static int grid_for(long n) {
 hipError_t fill_f32(float *p, long n, float v, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+hipError_t fill_hash(float *p, half_t *p16, long n, uint32_t seed, float amp, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_hash_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, p16, n, seed, amp);
     return hipGetLastError();
 }
 hipError_t cast_f32_f16(const float *src, half_t *dst, long n, hipStream_t s) {

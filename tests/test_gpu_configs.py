@@ -245,3 +245,19 @@ def test_checkpoint_save_load_resumes_training(dev, tmp_path):
         ck.load_params(path, b, {"fc1.weight": ("W1", (D, H))})
     a.close()
     b.close()
+
+
+def test_config3_trainer_starts_zeroed_after_in_step_tuning(dev):
+    """Creating the config-3 trainer for shapes no earlier trainer tuned times the contraction variants
+    inside running steps on hash-filled buffers; afterwards every parameter, the loss and the
+    accumulators are zero again, so one step on all-zero slots keeps the parameters and the loss at
+    zero. (The batch 384 appears in no other test, so every shape key is tuned afresh here.)"""
+    B, D0, D1, D2, D3 = 384, 128, 256, 128, 128
+    t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], 1e-3)
+    for k, n in (("W1", D1 * D0), ("b1", D1), ("W2", D2 * D1), ("b2", D2), ("W3", D3 * D2), ("b3", D3)):
+        assert not np.any(t.get(k, n).view(np.uint32)), k
+    t.step(B, store_grads=True)
+    assert t.get("loss", 1)[0] == 0.0
+    for k, n in (("W1", D1 * D0), ("b3", D3), ("db1", D1), ("db3", D3)):
+        assert not np.any(t.get(k, n)), k
+    t.close()
