@@ -222,7 +222,10 @@ enum {
  *  MLP3   : 0 x, 1 t, 2 W1, 3 b1, 4 W2, 5 b2, 6 W3, 7 b3, 8 loss, 9 dW1, 10 db1, 11 dW2, 12 db2,
  *           13 dW3, 14 db3
  *  CHAIN  : 0 X, 1 g, 2 loss, 3 dX, 4 dg
- * Gradient slots are filled only by steps run with AH_STEP_STORE_GRADS. */
+ * Gradient slots are filled only by steps run with AH_STEP_STORE_GRADS.
+ * Creating an MLP3 trainer tunes its f16 contractions for shapes the device has not tuned yet: each alone
+ * (ah_gemm_tune), then each variant again inside running steps on hash-filled buffers (≈1.5 s at the
+ * config-3 shape); every parameter, data and accumulator buffer is zero when create returns. */
 #define AH_STEP_STORE_GRADS 1
 #define AH_STEP_GRAPH 2      /* capture the step once per batch size as a hipGraph and replay it (tensor.JIT) */
 int ah_trainer_create(ah_device *dev, int32_t kind, const int64_t *dims, int32_t n_dims, float lr,
