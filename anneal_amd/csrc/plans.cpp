@@ -387,6 +387,7 @@ struct Mlp3Trainer : ah_trainer {
         hipFree(s16);
         hipFree(s32);
         if (rc == AH_OK) rc = refine(fresh);
+        if (rc == AH_OK) rc = clear_state();
         if (rc == AH_OK && cache && *cache) rc = ah_gemm_tune_cache(dev, cache, 1);
         return rc;
     }
@@ -395,7 +396,7 @@ struct Mlp3Trainer : ah_trainer {
     // from the previous launch and its epilogue rewriting scratch it just wrote; inside the step the
     // weight-update epilogues read master weights last touched a whole step earlier, which changes the
     // ranking (dW1 of config 3: the alone-fastest variant is 10% slower in place). The refinement runs
-    // on hash-filled parameters and data before any slot is set, and leaves every buffer zeroed.
+    // on hash-filled parameters and data before any slot is set; clear_state() zeroes them afterwards.
     // Contractions whose shape key another contraction of the step shares keep the choice from
     // timing alone (the probe brackets one launch, the key selects the variant for both).
     int refine(const bool *fresh) {
@@ -453,7 +454,12 @@ struct Mlp3Trainer : ah_trainer {
         probe_index = saved;
         n_probe = 0;
         launch_idx = 0;
-        // zero state: parameters, data and accumulators as freshly created
+        return rc;
+    }
+    // Parameters, data, loss and accumulators all zero (the state create returns, tuned or not).
+    int clear_state() {
+        hipStream_t s = dev->stream;
+        int rc = AH_OK;
         float *f32s[] = {W1, W2, W3, b1, b2, b3, loss};
         size_t nf[] = {(size_t)D1 * D0, (size_t)D2 * D1, (size_t)D3 * D2, (size_t)D1, (size_t)D2, (size_t)D3, 1};
         for (int k = 0; k < 7 && rc == AH_OK; k++)
