@@ -224,7 +224,7 @@ enum {
  *  CHAIN  : 0 X, 1 g, 2 loss, 3 dX, 4 dg
  * Gradient slots are filled only by steps run with AH_STEP_STORE_GRADS.
  * Creating an MLP3 trainer tunes its f16 contractions for shapes the device has not tuned yet: each alone
- * (ah_gemm_tune), then each variant again inside running steps on hash-filled buffers (≈1.5 s at the
+ * (ah_gemm_tune), then each variant again inside running steps on hash-filled buffers (≈1.9 s in all at the
  * config-3 shape); every parameter, data and accumulator buffer is zero when create returns. */
 #define AH_STEP_STORE_GRADS 1
 #define AH_STEP_GRAPH 2      /* capture the step once per batch size as a hipGraph and replay it (tensor.JIT) */
