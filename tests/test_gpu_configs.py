@@ -122,7 +122,9 @@ def run_mlp3(dev, p, lr):
     return out
 
 
-@pytest.mark.parametrize("shape", [(256, 128, 256, 256, 128), (512, 256, 512, 384, 256)])
+# (256, 256, 256, 256, 256): all eight contractions fall on three shape keys, so the in-step tuning keeps
+# their alone-timed choices (the shared-key path).
+@pytest.mark.parametrize("shape", [(256, 128, 256, 256, 128), (512, 256, 512, 384, 256), (256, 256, 256, 256, 256)])
 def test_config3_f16_mlp_step_vs_oracle(dev, shape):
     B, D0, D1, D2, D3 = shape
     p = data.mlp3_inputs(B, D0, D1, D2, D3)
