@@ -65,7 +65,7 @@ int template_create(const std::string &source, TemplateKernel **out) {
         base.K = (int)geti("K", -1);
         base.scale = 1.0f;
         base.variant = (int)geti("variant", 0);
-        if (base.variant < 0 || base.variant > 9) return set_error(AH_ERR_INVALID, "tmpl gemm: variant %d", base.variant);
+        if (base.variant < 0 || base.variant > kGemm16Variants) return set_error(AH_ERR_INVALID, "tmpl gemm: variant %d", base.variant);
         if ((!msym && base.M < 0) || base.N <= 0 || base.K < 0) return set_error(AH_ERR_INVALID, "tmpl gemm: M/N/K required");
         auto *t = new TemplateKernel();
         t->key = source;

@@ -13,6 +13,9 @@
 
 namespace ah {
 
+// Number of f16 kernel variants (table Var<V> in gemm16_kernel.h); variant 0 means the tuned choice.
+constexpr int kGemm16Variants = 31;
+
 enum GemmDtype : int { GEMM_F32 = 0, GEMM_F16 = 1 };
 
 enum GemmEpi : int {

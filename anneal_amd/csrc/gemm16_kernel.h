@@ -262,10 +262,8 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     auto stage_wait = [&]() {
         if constexpr (FETCH == 3) asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE + 1) : "memory");
         else asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NS - 2) * PERSTAGE) : "memory");
-#ifndef AH_EXP_NOBARRIER
         if constexpr (FETCH >= 3) lds_barrier();
         else __syncthreads();
-#endif
     };
     // Fetch modes 2-4: right after the barrier that opens stage kt, refill the buffer consumed in
     // stage kt-1 with stage kt+NS-1 (clamped: the tail re-fetches the last stage into idle buffers,
@@ -276,17 +274,13 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
         if (FETCH >= 5 && !all_modes) {
             // mode 5 issues these between the MFMAs that follow
         } else if constexpr (FETCH == 2) {
-#ifndef AH_EXP_NOFETCH
             fa.issue(Ab, d.lda, kn, nxt, wave);
             fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
-#endif
         } else if constexpr (FETCH >= 3) {
-#ifndef AH_EXP_NOFETCH
             const uint32_t nxt_lds = gsm_lds + ((kt + NS - 1) % NS) * STAGE;
             fa.issue_asm(Ab, d.lda, kn, nxt_lds, wave_u);
             fb.issue_asm(Bb, d.ldb, kn, nxt_lds + ABYTES, wave_u);
             if constexpr (FETCH == 3) prefetch(min(kt + NS, nk - 1) * BK);
-#endif
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -321,10 +315,8 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
         constexpr int FPS = (PERSTAGE + KS - 1) / KS;                      // fetches per k-step
         constexpr bool SPREAD = FETCH == 1;
         if constexpr (FETCH == 0) {
-#ifndef AH_EXP_NOFETCH
             fa.issue(Ab, d.lda, kn, nxt, wave);
             fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
-#endif
         }
 #pragma unroll
         for (int s = 0; s < KS; s++) {
@@ -364,20 +356,16 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
 #pragma unroll
                         for (int q = 0; q < DPM; q++) {
                             const int f = (t / MPD) * DPM + q;
-#ifndef AH_EXP_NOFETCH
                             if (f < PA) fa.issue_one_asm(f, Ab, d.lda, kr, refill_lds, wave_u);
                             else fb.issue_one_asm(f - PA, Bb, d.ldb, kr, refill_lds + ABYTES, wave_u);
-#endif
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
                 if (SPREAD && t % (NM / FPS) == NM / FPS - 1) {
                     const int f = s * FPS + t / (NM / FPS);
-#ifndef AH_EXP_NOFETCH
                     if (f < PA) fa.issue_one(f, Ab, d.lda, kn, nxt, wave);
                     else if (f < PERSTAGE) fb.issue_one(f - PA, Bb, d.ldb, kn, nxt + ABYTES, wave);
-#endif
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }

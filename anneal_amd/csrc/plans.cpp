@@ -106,8 +106,6 @@ static int copy_in_f16(ah_device *d, half_t *dst, const float *src, size_t n) {
 
 // ── GEMM variant tuning ─────────────────────────────────────────────────────
 
-constexpr int kGemm16Variants = 31;
-
 static std::string tune_key(const GemmDesc &g) {
     char b[96];
     snprintf(b, sizeof b, "%d/%d/%d/%d/%d/%d", g.dtype, g.ta, g.tb, g.M, g.N, g.K);
