@@ -104,6 +104,7 @@ SIGNATURES = {
     "ah_gemm_tune": (C.c_int, [_P, C.POINTER(ah_gemm_desc), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
     "ah_softmax_ce": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P]),
     "ah_chain_step": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P]),
+    "ah_chain_step_noalloc": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P, _P]),
     "ah_trainer_create": (C.c_int, [_P, C.c_int32, C.POINTER(C.c_int64), C.c_int32, C.c_float, C.POINTER(_P)]),
     "ah_trainer_destroy": (None, [_P]),
     "ah_trainer_set": (C.c_int, [_P, C.c_int32, _P, C.c_int64]),

@@ -110,6 +110,10 @@ class Device:
     def chain_step(self, X, g, R, Cc, dX, dg, loss) -> None:
         L.check(self.lib.ah_chain_step(self.h, X.ptr, g.ptr, R, Cc, dX.ptr, dg.ptr, loss.ptr))
 
+    def chain_step_noalloc(self, X, g, R, Cc, dX, dg, loss) -> None:
+        """chain_step with the workspace in the library's per-GPU static array (enqueues only)."""
+        L.check(self.lib.ah_chain_step_noalloc(self.h, X.ptr, g.ptr, R, Cc, dX.ptr, dg.ptr, loss.ptr))
+
     def close(self) -> None:
         if self.h:
             self.lib.ah_close(self.h)

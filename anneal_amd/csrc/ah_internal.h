@@ -48,6 +48,8 @@ struct ah_device {
     // f16 GEMM variant chosen by ah_gemm_tune per (ta, tb, M, N, K); used when a launch asks for
     // variant 0 (the role of BEAM's cache, codegen/beam.go:118-169).
     std::unordered_map<std::string, int> gemm_variant;
+    // This device's address of the chain's file-scope workspace (ah_chain_step_noalloc), set by ah_open.
+    float *chain_scratch = nullptr;
 };
 
 struct ah_graph {

@@ -817,4 +817,17 @@ int ah_chain_step(ah_device *dev, const float *X, const float *g, int32_t R, int
     return AH_OK;
 }
 
+int ah_chain_step_noalloc(ah_device *dev, const float *X, const float *g, int32_t R, int32_t Cc, float *dX, float *dg,
+                          float *loss) {
+    if (!dev || !X || !g || !dX || !dg || !loss || R <= 0 || Cc <= 0 || Cc % 4)
+        return set_error(AH_ERR_INVALID, "ah_chain_step_noalloc: bad argument (Cc must be a multiple of 4)");
+    const long need = chain_workspace_floats(R, Cc), cap = chain_scratch_floats();
+    if (need > cap)
+        return set_error(AH_ERR_INVALID, "ah_chain_step_noalloc: R=%d x Cc=%d needs %ld workspace floats, the maximum is %ld",
+                         R, Cc, need, cap);
+    if (!dev->chain_scratch) return set_error(AH_ERR_INVALID, "ah_chain_step_noalloc: device has no chain workspace");
+    AH_HIP(chain_step(X, g, R, Cc, dev->chain_scratch, dX, dg, loss, dev->stream));
+    return AH_OK;
+}
+
 }  // extern "C"

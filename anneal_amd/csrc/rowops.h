@@ -46,6 +46,10 @@ struct TailArgs {
 hipError_t step_tail(const TailArgs &t, hipStream_t s);
 
 long chain_workspace_floats(int R, int Cc);
+// Capacity (floats) of the file-scope chain workspace used by ah_chain_step_noalloc, and its address on
+// the device `ordinal` (the current device at the call).
+long chain_scratch_floats();
+hipError_t chain_scratch_init(int ordinal, float **out);
 hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work, float *dX, float *dg, float *loss,
                       hipStream_t s, int phase = -1);
 

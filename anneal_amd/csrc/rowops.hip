@@ -525,3 +525,37 @@ hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work
 }
 
 }  // namespace ah
+
+// ── config-5 chain without allocation ───────────────────────────────────────
+// The chain's workspace (per-chunk column partials, per-column coefficients, loss partials) lives in a
+// file-scope device array instead of a hipMalloc'd buffer, for callers that cannot allocate (graph
+// capture, serving loops). Every GPU the library runs on holds its own copy of `scratch` at its own
+// address until the process ends; host code must use the address hipGetSymbolAddress returned for the
+// current device, never the array's name (which is only a host-side stand-in).
+// The chain writes every workspace entry before reading it (chain_stats fills every chunk partial,
+// chain_finalize every coefficient and loss partial), so nothing needs clearing between calls.
+namespace ah {
+namespace {
+constexpr long kChainScratchFloats = 1L << 21;   // 8 MiB: R x Cc up to 16128 x 4096 (config 5, 8192 x 4096, needs 1.08M floats)
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kChainScratchFloats];
+float *g_scratch_ptr[kMaxDevices];
+}  // namespace
+
+long chain_scratch_floats() { return kChainScratchFloats; }
+
+// Looks up this device's copy of `scratch`, with `ordinal` the current device. Called once per device,
+// from ah_open; later calls return the stored address.
+hipError_t chain_scratch_init(int ordinal, float **out) {
+    if (ordinal < 0 || ordinal >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!g_scratch_ptr[ordinal]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[ordinal] = (float *)p;
+    }
+    *out = g_scratch_ptr[ordinal];
+    return hipSuccess;
+}
+
+}  // namespace ah

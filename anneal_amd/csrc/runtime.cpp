@@ -11,6 +11,7 @@
 #include <mutex>
 
 #include "ah_internal.h"
+#include "rowops.h"
 
 namespace ah {
 
@@ -109,6 +110,12 @@ int ah_open(int ordinal, ah_device **out) {
         hipStreamDestroy(d->stream);
         delete d;
         return set_error(AH_ERR_UNSUPPORTED, "ah_open: device arch %s is not gfx950", d->props.gcnArchName);
+    }
+    e = chain_scratch_init(ordinal, &d->chain_scratch);   // the device is current (hipSetDevice above)
+    if (e != hipSuccess) {
+        hipStreamDestroy(d->stream);
+        delete d;
+        return fail_hip(e, "ah_open: chain workspace address");
     }
     *out = d;
     return AH_OK;

@@ -204,6 +204,15 @@ int ah_softmax_ce(ah_device *dev, const float *z, const int32_t *labels, int32_t
  * out = S * recip(sqrt(mean(S*S,1) + 1e-6)) * g; loss = Sum(out); returns dX [R,Cc], dg [Cc]. */
 int ah_chain_step(ah_device *dev, const float *X, const float *g, int32_t R, int32_t Cc, float *dX, float *dg,
                   float *loss);
+/* ah_chain_step without allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops). The chain's workspace is a
+ * file-scope device array of 2^21 floats (8 MiB per GPU, held until the process ends), so
+ * ceil(R/128)*Cc*4 + Cc*8 + ceil(Cc/32) must not exceed 2^21 (config 5, 8192 x 4096, needs 1.08M);
+ * larger shapes fail with AH_ERR_INVALID. Asynchronous: the three kernels are enqueued on the device
+ * stream and the call returns (ah_sync waits). Every call on one GPU shares that GPU's workspace, so
+ * calls that overlap on one GPU (several device handles or host threads) race. */
+int ah_chain_step_noalloc(ah_device *dev, const float *X, const float *g, int32_t R, int32_t Cc, float *dX,
+                          float *dg, float *loss);
 
 /* ── Device-resident training steps (one BASELINE config each) ───────────────
  * Replaces the reference step pattern: graph build -> tensor.Backward -> one tensor.Realize per gradient
