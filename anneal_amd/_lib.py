@@ -16,6 +16,7 @@ AH_F32, AH_F16, AH_BF16, AH_I32, AH_BOOL, AH_U32 = 0, 1, 2, 3, 4, 5
 EPI_STORE, EPI_BIAS, EPI_BIAS_RELU, EPI_MSE, EPI_MASK, EPI_SGD = range(6)
 TRAIN_MLP_CE, TRAIN_CONVNET, TRAIN_MLP3_F16, TRAIN_CHAIN = 1, 2, 3, 4
 STEP_STORE_GRADS, STEP_GRAPH = 1, 2
+PLAN_GRAPH = 1
 
 
 class ah_caps(C.Structure):
@@ -90,6 +91,11 @@ SIGNATURES = {
                                   C.POINTER(C.POINTER(ah_output)), C.POINTER(C.c_int32)]),
     "ah_benchmark": (C.c_int, [_P, C.POINTER(ah_exec_item), C.c_int32, C.c_int32, C.POINTER(ah_bench_result)]),
     "ah_outputs_free": (None, [C.POINTER(ah_output), C.c_int32]),
+    "ah_plan_create": (C.c_int, [_P, C.POINTER(ah_exec_item), C.c_int32, C.POINTER(_P)]),
+    "ah_plan_run": (C.c_int, [_P, C.POINTER(ah_input), C.c_int32, C.POINTER(C.c_char_p), C.POINTER(C.c_int64),
+                              C.c_int32, C.c_int32, C.POINTER(C.POINTER(ah_output)), C.POINTER(C.c_int32)]),
+    "ah_plan_stats": (C.c_int, [_P, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "ah_plan_destroy": (None, [_P]),
     "ah_gemm": (C.c_int, [_P, C.POINTER(ah_gemm_desc)]),
     "ah_translate_wgsl": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
     "ah_ckpt_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),

@@ -22,13 +22,30 @@ int fail_hip(hipError_t e, const char *what);
 
 int64_t dtype_bytes(int32_t dtype);
 
-// Built-in template kernel, selected by a "tmpl:" source key. run() launches it on the stream with
-// the ExecItem's buffers (PARAM order) and the symbolic scalars.
+// Built-in template kernel, selected by a "tmpl:" source key (templates.cpp). run() launches it on the
+// device stream with the ExecItem's buffers (PARAM order) and the symbolic scalars.
 struct TemplateKernel {
-    std::string key;
-    std::unordered_map<std::string, std::string> params;
-    std::function<int(ah_device *, void *const *ptrs, int32_t n_ptrs, const int32_t *scalars, int32_t n_scalars)> run;
+    std::string key, name;
+    // PARAMs after data0 that the kernel writes (zero: the kernel accumulates into it, so it must start at 0)
+    struct Side {
+        int param;
+        bool zero;
+    };
+    std::vector<Side> side;
+    // bytes of device workspace the kernel needs for a symbolic binding (null: none); the workspace is the
+    // template's own, grown by template_prepare (or on first use) and freed with the template
+    std::function<int64_t(int64_t symval)> workspace;
+    void *ws = nullptr;
+    int64_t ws_bytes = 0;
+    std::function<int(ah_device *, TemplateKernel *self, void *const *ptrs, int32_t n_ptrs, const int32_t *scalars,
+                      int32_t n_scalars)>
+        run;
+    ~TemplateKernel();
 };
+
+struct GemmDesc;
+// A contraction launched with the device's tuned f16 variant when the descriptor leaves the choice open.
+hipError_t gemm_dispatch(ah_device *dev, const GemmDesc &g);
 
 }  // namespace ah
 
@@ -59,5 +76,7 @@ struct ah_graph {
 
 namespace ah {
 int template_create(const std::string &source, TemplateKernel **out);
+// Grows the template's workspace for the binding symval (before a graph capture).
+int template_prepare(TemplateKernel *t, int64_t symval);
 std::string wgsl_to_hip(const std::string &src, std::string *err);
 }

@@ -141,10 +141,10 @@ __global__ __launch_bounds__(256) void conv_bwd_w_finalize_kernel(const float *p
     if (q < 9) {
         long wi = ((long)co * Ci + ci) * 9 + q;
         if (gw) gw[wi] = g;
-        w[wi] = w[wi] - lr * g;
+        if (w) w[wi] = w[wi] - lr * g;   // w == nullptr: gradients only
     } else if (ci == 0) {
         if (gb) gb[co] = g;
-        b[co] = b[co] - lr * g;
+        if (b) b[co] = b[co] - lr * g;
     }
 }
 

@@ -1,13 +1,23 @@
-// executor.cpp — backend.Executor / SymbolicExecutor / Benchmarker mirror over ExecItem-shaped input.
+// executor.cpp — backend.Executor / SymbolicExecutor / Benchmarker mirror over ExecItem-shaped input,
+// and the persistent plans that replay an item list as a HIP graph (tensor.JIT).
 //
 // Follows the reference's Run contract (backend/webgpu/executor.go:26-237, :576-922):
 //   - bufs[0] is the output, bufs[1..] inputs in PARAM order;
-//   - outputs with slot >= 0 share one allocation per slot sized for the largest user;
+//   - outputs with slot >= 0 share one allocation per slot sized for the largest user (4 bytes/element);
 //   - final outputs are outputs no item reads; they are downloaded widened to f32 and keyed by uop_idx;
 //   - inputs whose uop_idx is not in the schedule are ignored;
-//   - every device object made for the call is released before returning.
+//   - every buffer a Run sees starts at zero, as freshly created WebGPU buffers do: a leaf with no input,
+//     or an input shorter than its buffer, leaves zeros behind it;
+//   - ah_run / ah_run_symbolic release every device object made for the call before returning.
 // Differences by design: kernels come from hiprtc-compiled HIP source (cached per source for the device
-// lifetime instead of recompiled each Run) or from "tmpl:" keys naming hand-written kernels.
+// lifetime instead of recompiled each Run) or from "tmpl:" keys naming hand-written kernels, which may
+// also write later PARAMs ("side outputs"); a side output no item reads is returned as a final output too.
+//
+// A plan (ah_plan_*) is the same Run kept alive: its item list is copied, its kernels resolved and its
+// buffers allocated once (re-sized when a larger symbolic binding arrives), and with AH_PLAN_GRAPH each
+// binding's kernel sequence is captured once as a HIP graph and replayed on later runs. This is the device
+// half of tensor.JIT (tensor/jit.go:178-215), which replays one captured item list through Run/RunSymbolic
+// with fresh leaf data on every step.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -17,204 +27,269 @@
 #include <set>
 
 #include "ah_internal.h"
-#include "gemm.h"
-
-namespace ah {
-
-static std::unordered_map<std::string, std::string> parse_params(const std::string &s, std::string *name) {
-    std::unordered_map<std::string, std::string> out;
-    size_t p = s.find(';');
-    *name = s.substr(5, p == std::string::npos ? std::string::npos : p - 5);
-    while (p != std::string::npos) {
-        size_t q = s.find(';', p + 1);
-        std::string kv = s.substr(p + 1, q == std::string::npos ? std::string::npos : q - p - 1);
-        size_t e = kv.find('=');
-        if (e != std::string::npos) out[kv.substr(0, e)] = kv.substr(e + 1);
-        p = q;
-    }
-    return out;
-}
-
-// "tmpl:gemm;dtype=f16;epi=bias_relu;ta=0;tb=0;M=4096;N=4096;K=1024[;variant=3]"
-// PARAM order: data0 = C, data1 = A, data2 = B, data3 = bias (bias epilogues) or aux (mask).
-// M may be "sym": it is then taken from the first symbolic scalar (the bound batch size).
-int template_create(const std::string &source, TemplateKernel **out) {
-    std::string name;
-    auto params = parse_params(source, &name);
-    auto geti = [&](const char *k, long dflt) -> long {
-        auto it = params.find(k);
-        return it == params.end() ? dflt : strtol(it->second.c_str(), nullptr, 10);
-    };
-    if (name == "gemm") {
-        GemmDesc base;
-        memset(&base, 0, sizeof base);
-        std::string dt = params.count("dtype") ? params["dtype"] : "f32";
-        if (dt != "f32" && dt != "f16") return set_error(AH_ERR_UNSUPPORTED, "tmpl gemm: dtype %s", dt.c_str());
-        base.dtype = dt == "f16" ? GEMM_F16 : GEMM_F32;
-        std::string epi = params.count("epi") ? params["epi"] : "store";
-        static const std::map<std::string, int> epis = {{"store", EPI_STORE}, {"bias", EPI_BIAS},
-                                                        {"bias_relu", EPI_BIAS_RELU}, {"mask", EPI_MASK}};
-        auto ei = epis.find(epi);
-        if (ei == epis.end()) return set_error(AH_ERR_UNSUPPORTED, "tmpl gemm: epilogue %s", epi.c_str());
-        base.epi = ei->second;
-        base.ta = (int)geti("ta", 0);
-        base.tb = (int)geti("tb", 0);
-        bool msym = params.count("M") && params["M"] == "sym";
-        base.M = msym ? 0 : (int)geti("M", -1);
-        base.N = (int)geti("N", -1);
-        base.K = (int)geti("K", -1);
-        base.scale = 1.0f;
-        base.variant = (int)geti("variant", 0);
-        if (base.variant < 0 || base.variant > kGemm16Variants) return set_error(AH_ERR_INVALID, "tmpl gemm: variant %d", base.variant);
-        if ((!msym && base.M < 0) || base.N <= 0 || base.K < 0) return set_error(AH_ERR_INVALID, "tmpl gemm: M/N/K required");
-        auto *t = new TemplateKernel();
-        t->key = source;
-        t->params = params;
-        t->run = [base, msym](ah_device *d, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
-            GemmDesc g = base;
-            if (msym) {
-                if (ns < 1) return set_error(AH_ERR_INVALID, "tmpl gemm: symbolic M needs a binding");
-                g.M = sc[0];
-            }
-            int need = (g.epi == EPI_STORE) ? 3 : 4;
-            if (n_ptrs < need) return set_error(AH_ERR_INVALID, "tmpl gemm: needs %d buffers, got %d", need, n_ptrs);
-            g.C = ptrs[0];
-            g.A = ptrs[1];
-            g.B = ptrs[2];
-            if (g.epi == EPI_BIAS || g.epi == EPI_BIAS_RELU) g.bias = ptrs[3];
-            if (g.epi == EPI_MASK) { g.aux = ptrs[3]; g.ldaux = g.N; }
-            g.lda = g.ta ? g.M : g.K;
-            g.ldb = g.tb ? g.N : g.K;
-            g.ldc = g.N;
-            AH_HIP(gemm_launch(g, d->stream));
-            return AH_OK;
-        };
-        *out = t;
-        return AH_OK;
-    }
-    return set_error(AH_ERR_UNSUPPORTED, "unknown template '%s'", name.c_str());
-}
-
-// ── Run ─────────────────────────────────────────────────────────────────────
+#include "itemops.h"
 
 namespace {
 
-struct RunState {
-    ah_device *dev;
-    std::vector<void *> owned;
-    std::map<uint32_t, void *> ptr;
-    std::map<uint32_t, int32_t> dtype;
-    std::map<uint32_t, int64_t> elems;
-    ~RunState() {
-        for (void *p : owned) hipFree(p);
-    }
-};
-
-int64_t bound_size(const ah_buffer_desc &b, int64_t n) {
-    if (b.size > 0) return b.size;
-    if (!b.shape || b.rank <= 0) return b.size;
+int64_t bound_size(int64_t size, const std::vector<int64_t> &shape, int64_t n) {
+    if (size > 0) return size;
+    if (shape.empty()) return size;
     int64_t s = 1;
-    for (int i = 0; i < b.rank; i++) s *= (b.shape[i] == 0 ? n : b.shape[i]);
+    for (int64_t d : shape) s *= (d == 0 ? n : d);
     return s;
 }
 
-int run_impl(ah_device *d, const ah_exec_item *items, int32_t n_items, const ah_input *inputs, int32_t n_inputs,
-             int64_t symval, bool symbolic, ah_output **outputs, int32_t *n_outputs) {
-    if (!d || (!items && n_items) || !outputs || !n_outputs) return set_error(AH_ERR_INVALID, "ah_run: null argument");
-    *outputs = nullptr;
-    *n_outputs = 0;
-    if (n_items == 0) return AH_OK;
-    RunState st;
-    st.dev = d;
-    std::set<uint32_t> written, read_any;
-    for (int i = 0; i < n_items; i++) {
-        if (items[i].n_bufs < 1 || !items[i].bufs || !items[i].source)
-            return set_error(AH_ERR_INVALID, "ah_run: kernel %d has no buffers or source", i);
-        written.insert(items[i].bufs[0].uop_idx);
-        for (int j = 1; j < items[i].n_bufs; j++) read_any.insert(items[i].bufs[j].uop_idx);
-        for (int j = 0; j < items[i].n_bufs; j++) {
-            const ah_buffer_desc &b = items[i].bufs[j];
-            st.dtype[b.uop_idx] = b.dtype;
-            st.elems[b.uop_idx] = bound_size(b, symval);
-        }
-    }
-    // Phase A: slots sized for their largest user (4 bytes per element, executor.go:83-112).
-    std::map<int, int64_t> slot_max;
-    for (int i = 0; i < n_items; i++) {
-        const ah_buffer_desc &o = items[i].bufs[0];
-        if (o.slot >= 0) slot_max[o.slot] = std::max(slot_max[o.slot], bound_size(o, symval));
-    }
-    std::map<int, void *> slot_ptr;
-    for (auto &kv : slot_max) {
-        void *p = nullptr;
-        AH_HIP(hipMalloc(&p, (size_t)std::max<int64_t>(kv.second, 1) * 4));
-        st.owned.push_back(p);
-        slot_ptr[kv.first] = p;
-    }
-    // Phase B/C: dedicated outputs and leaves.
-    for (int i = 0; i < n_items; i++) {
-        for (int j = 0; j < items[i].n_bufs; j++) {
-            const ah_buffer_desc &b = items[i].bufs[j];
-            if (st.ptr.count(b.uop_idx)) continue;
-            if (j == 0 && b.slot >= 0) { st.ptr[b.uop_idx] = slot_ptr[b.slot]; continue; }
-            if (j > 0 && written.count(b.uop_idx)) continue;   // produced by another item; bound when it runs
-            void *p = nullptr;
-            AH_HIP(hipMalloc(&p, (size_t)std::max<int64_t>(st.elems[b.uop_idx], 1) * dtype_bytes(b.dtype)));
-            st.owned.push_back(p);
-            st.ptr[b.uop_idx] = p;
-        }
-    }
-    for (int i = 0; i < n_items; i++) {
-        const ah_buffer_desc &o = items[i].bufs[0];
-        if (!st.ptr.count(o.uop_idx)) return set_error(AH_ERR_INVALID, "ah_run: output %u unallocated", o.uop_idx);
-    }
-    // Upload leaves (inputs for unknown buffers are ignored, executor.go:163-165).
-    for (int i = 0; i < n_inputs; i++) {
-        auto it = st.ptr.find(inputs[i].uop_idx);
-        if (it == st.ptr.end()) continue;
-        int64_t n = std::min<int64_t>(inputs[i].n, st.elems[inputs[i].uop_idx]);
-        int rc = ah_upload(d, it->second, inputs[i].data, n, st.dtype[inputs[i].uop_idx]);
-        if (rc) return rc;
-    }
-    // Dispatch in schedule order.
-    for (int i = 0; i < n_items; i++) {
-        const ah_exec_item &it = items[i];
+}  // namespace
+
+struct ah_plan {
+    struct Buf {
+        uint32_t uop;
+        int64_t size;
+        int32_t dtype;
+        int32_t slot;
+        std::vector<int64_t> shape;
+        int64_t elems(int64_t n) const { return bound_size(size, shape, n); }
+    };
+    struct Item {
+        std::string source;
+        std::vector<Buf> bufs;
+        int n_sym = 0;
+        int32_t ls[3], wg[3];
         ah_kernel *k = nullptr;
-        int rc = ah_module_get(d, it.source, "kernel", &k);
-        if (rc) return set_error(rc, "ah_run: kernel %d: %s", i, ah_last_error());
-        std::vector<void *> ptrs;
-        for (int j = 0; j < it.n_bufs; j++) {
-            auto p = st.ptr.find(it.bufs[j].uop_idx);
-            if (p == st.ptr.end()) return set_error(AH_ERR_INVALID, "ah_run: kernel %d: missing GPU buffer %u", i, it.bufs[j].uop_idx);
-            ptrs.push_back(p->second);
+        std::vector<int> writes;   // PARAM positions written: 0 plus the template's side outputs
+        std::vector<bool> clear;   // per entry of writes: zero before the launch
+    };
+    // One device buffer per uop_idx (slot outputs share their slot's allocation).
+    struct Mem {
+        int32_t dtype = AH_F32;
+        int slot = -1;
+        bool leaf = true;          // not written by any item: filled from the inputs
+        std::vector<const Buf *> descs;
+        void *ptr = nullptr;
+        int64_t elems(int64_t n) const {
+            int64_t e = 0;
+            for (const Buf *b : descs) e = std::max(e, b->elems(n));
+            return e;
         }
+    };
+
+    ah_device *dev = nullptr;
+    std::vector<Item> items;
+    bool has_sym = false;
+    std::string symvar;            // SymVars[0] of the first symbolic item (executor.go:817-822)
+    std::map<uint32_t, Mem> mem;
+    std::vector<uint32_t> finals;  // final outputs in item order
+    std::vector<void *> owned;
+    int64_t alloc_n = -1;          // binding the allocations are sized for
+    std::map<int64_t, ah_graph *> graphs;
+    int64_t captures = 0, replays = 0;
+
+    ~ah_plan() {
+        if (dev) hipStreamSynchronize(dev->stream);
+        drop_graphs();
+        release();
+    }
+    void drop_graphs() {
+        for (auto &kv : graphs) ah_graph_destroy(kv.second);
+        graphs.clear();
+    }
+    void release() {
+        for (void *p : owned) hipFree(p);
+        owned.clear();
+        for (auto &kv : mem) kv.second.ptr = nullptr;
+    }
+};
+
+namespace ah {
+namespace {
+
+int plan_build(ah_device *d, const ah_exec_item *items, int32_t n_items, ah_plan *p) {
+    p->dev = d;
+    p->items.resize(n_items);
+    for (int i = 0; i < n_items; i++) {
+        const ah_exec_item &src = items[i];
+        if (src.n_bufs < 1 || !src.bufs || !src.source)
+            return set_error(AH_ERR_INVALID, "ah_run: kernel %d has no buffers or source", i);
+        ah_plan::Item &it = p->items[i];
+        it.source = src.source;
+        for (int j = 0; j < src.n_bufs; j++) {
+            const ah_buffer_desc &b = src.bufs[j];
+            ah_plan::Buf c{b.uop_idx, b.size, b.dtype, b.slot, {}};
+            if (b.shape && b.rank > 0) c.shape.assign(b.shape, b.shape + b.rank);
+            if (dtype_bytes(b.dtype) <= 0) return set_error(AH_ERR_UNSUPPORTED, "ah_run: kernel %d: dtype %d", i, b.dtype);
+            it.bufs.push_back(c);
+        }
+        it.n_sym = src.n_sym_vars > 0 && src.sym_vars ? src.n_sym_vars : 0;
+        if (it.n_sym && !p->has_sym) {
+            p->has_sym = true;
+            p->symvar = src.sym_vars[0] ? src.sym_vars[0] : "";
+        }
+        for (int a = 0; a < 3; a++) {
+            it.ls[a] = std::max(1, src.local_size[a]);
+            it.wg[a] = std::max(1, src.workgroup_count[a]);
+        }
+        int rc = ah_module_get(d, it.source.c_str(), "kernel", &it.k);
+        if (rc) return set_error(rc, "ah_run: kernel %d: %s", i, ah_last_error());
+        // Writes: data0 always; a template's side outputs too. Only templates are known to overwrite
+        // every element of data0, so other kernels' outputs are cleared before they run.
+        it.writes.push_back(0);
+        it.clear.push_back(it.k->tmpl == nullptr);
+        if (it.k->tmpl)
+            for (auto &s : it.k->tmpl->side) {
+                if (s.param >= (int)it.bufs.size())
+                    return set_error(AH_ERR_INVALID, "ah_run: kernel %d: %s writes PARAM %d of %zu", i,
+                                     it.k->tmpl->name.c_str(), s.param, it.bufs.size());
+                it.writes.push_back(s.param);
+                it.clear.push_back(s.zero);
+            }
+    }
+    // buffer table
+    std::set<uint32_t> read_any;
+    for (auto &it : p->items) {
+        for (size_t j = 0; j < it.bufs.size(); j++) {
+            ah_plan::Mem &m = p->mem[it.bufs[j].uop];
+            m.descs.push_back(&it.bufs[j]);
+            m.dtype = it.bufs[j].dtype;
+        }
+        for (int w : it.writes) {
+            ah_plan::Mem &m = p->mem[it.bufs[w].uop];
+            m.leaf = false;
+            m.dtype = it.bufs[w].dtype;
+            if (w == 0 && it.bufs[0].slot >= 0) m.slot = it.bufs[0].slot;
+        }
+    }
+    for (auto &it : p->items)
+        for (size_t j = 1; j < it.bufs.size(); j++) {
+            bool written_here = std::find(it.writes.begin(), it.writes.end(), (int)j) != it.writes.end();
+            if (!written_here) read_any.insert(it.bufs[j].uop);
+        }
+    for (auto &it : p->items)
+        for (int w : it.writes) {
+            uint32_t u = it.bufs[w].uop;
+            if (!read_any.count(u) && std::find(p->finals.begin(), p->finals.end(), u) == p->finals.end())
+                p->finals.push_back(u);
+        }
+    return AH_OK;
+}
+
+// Allocates every buffer for binding n (once, or again when n outgrows the allocation) and zeroes it.
+int plan_alloc(ah_plan *p, int64_t n) {
+    if (p->alloc_n >= 0 && (!p->has_sym || n <= p->alloc_n)) return AH_OK;
+    AH_HIP(hipStreamSynchronize(p->dev->stream));
+    p->drop_graphs();
+    p->release();
+    std::map<int, int64_t> slot_bytes;
+    for (auto &kv : p->mem)
+        if (kv.second.slot >= 0)
+            slot_bytes[kv.second.slot] = std::max(slot_bytes[kv.second.slot], std::max<int64_t>(kv.second.elems(n), 1) * 4);
+    std::map<int, void *> slot_ptr;
+    auto alloc = [&](int64_t bytes, void **out) -> int {
+        bytes = std::max<int64_t>(bytes, 4);
+        AH_HIP(hipMalloc(out, (size_t)bytes));
+        p->owned.push_back(*out);
+        AH_HIP(zero_fill(*out, bytes, p->dev->stream));
+        return AH_OK;
+    };
+    for (auto &kv : slot_bytes)
+        if (int rc = alloc(kv.second, &slot_ptr[kv.first])) return rc;
+    for (auto &kv : p->mem) {
+        ah_plan::Mem &m = kv.second;
+        if (m.slot >= 0) m.ptr = slot_ptr[m.slot];
+        else if (int rc = alloc(m.elems(n) * dtype_bytes(m.dtype), &m.ptr)) return rc;
+    }
+    p->alloc_n = p->has_sym ? n : 0;
+    return AH_OK;
+}
+
+// Enqueues the item list: clears, then each kernel with its buffers.
+int plan_enqueue(ah_plan *p, int64_t n, bool symbolic) {
+    ah_device *d = p->dev;
+    for (size_t i = 0; i < p->items.size(); i++) {
+        ah_plan::Item &it = p->items[i];
+        for (size_t w = 0; w < it.writes.size(); w++) {
+            if (!it.clear[w]) continue;
+            const ah_plan::Mem &m = p->mem[it.bufs[it.writes[w]].uop];
+            int64_t bytes = m.elems(n) * dtype_bytes(m.dtype);
+            if (m.slot >= 0) bytes = std::max<int64_t>(m.elems(n), 1) * 4;
+            AH_HIP(zero_fill(m.ptr, bytes, d->stream));
+        }
+        std::vector<void *> ptrs;
+        for (auto &b : it.bufs) ptrs.push_back(p->mem[b.uop].ptr);
         std::vector<int32_t> sc;
-        if (symbolic && it.n_sym_vars > 0) sc.assign(4, (int32_t)symval);   // params_n: 16-byte uniform
+        if (symbolic && it.n_sym > 0) sc.assign(4, (int32_t)n);   // params_n: a 16-byte uniform
         uint32_t grid[3], block[3];
         for (int a = 0; a < 3; a++) {
-            grid[a] = (uint32_t)std::max(1, it.workgroup_count[a]);
-            block[a] = (uint32_t)std::max(1, it.local_size[a]);
+            grid[a] = (uint32_t)it.wg[a];
+            block[a] = (uint32_t)it.ls[a];
         }
-        if (symbolic && it.n_sym_vars > 0) {   // 1-D dispatch over the bound output (executor.go:874-898)
-            int64_t out_elems = bound_size(it.bufs[0], symval);
-            grid[0] = (uint32_t)((out_elems + block[0] - 1) / block[0]);
+        if (symbolic && it.n_sym > 0) {   // 1-D dispatch over the bound output (executor.go:874-898)
+            int64_t out_elems = it.bufs[0].elems(n);
+            grid[0] = (uint32_t)std::max<int64_t>(1, (out_elems + block[0] - 1) / block[0]);
         }
-        rc = ah_launch(d, k, grid, block, ptrs.data(), (int32_t)ptrs.size(), sc.data(), (int32_t)sc.size());
-        if (rc) return set_error(rc, "ah_run: kernel %d: %s", i, ah_last_error());
+        int rc = ah_launch(d, it.k, grid, block, ptrs.data(), (int32_t)ptrs.size(), sc.data(), (int32_t)sc.size());
+        if (rc) return set_error(rc, "ah_run: kernel %zu: %s", i, ah_last_error());
     }
-    // Read back final outputs.
+    return AH_OK;
+}
+
+int plan_run(ah_plan *p, const ah_input *inputs, int32_t n_inputs, int64_t n, bool symbolic, bool graph,
+             ah_output **outputs, int32_t *n_outputs) {
+    ah_device *d = p->dev;
+    *outputs = nullptr;
+    *n_outputs = 0;
+    if (p->items.empty()) return AH_OK;
+    if (int rc = plan_alloc(p, n)) return rc;
+    // Template workspaces for this binding; a workspace that moves invalidates captured graphs.
+    for (size_t i = 0; i < p->items.size(); i++) {
+        TemplateKernel *t = p->items[i].k->tmpl;
+        if (!t) continue;
+        void *before = t->ws;
+        if (int rc = template_prepare(t, symbolic ? n : 0)) return set_error(rc, "ah_run: kernel %zu: %s", i, ah_last_error());
+        if (t->ws != before) p->drop_graphs();
+    }
+    // Leaves: the input's elements, zeros after them (fresh-buffer semantics); no input: all zeros.
+    std::map<uint32_t, const ah_input *> in;
+    for (int i = 0; i < n_inputs; i++) in[inputs[i].uop_idx] = &inputs[i];
+    for (auto &kv : p->mem) {
+        ah_plan::Mem &m = kv.second;
+        if (!m.leaf) continue;
+        const int64_t elems = m.elems(n);
+        auto f = in.find(kv.first);
+        const int64_t k = f == in.end() ? 0 : std::min<int64_t>(f->second->n, elems);
+        if (k < elems) AH_HIP(zero_fill(m.ptr, std::max<int64_t>(elems, 1) * dtype_bytes(m.dtype), d->stream));
+        if (k > 0) {
+            if (!f->second->data) return set_error(AH_ERR_INVALID, "ah_run: input %u has no data", kv.first);
+            if (int rc = ah_upload(d, m.ptr, f->second->data, k, m.dtype)) return rc;
+        }
+    }
+    const int64_t key = symbolic ? n : 0;
+    if (graph) {
+        auto g = p->graphs.find(key);
+        if (g == p->graphs.end()) {
+            if (int rc = ah_graph_begin(d)) return rc;
+            int rc = plan_enqueue(p, n, symbolic);
+            ah_graph *cg = nullptr;
+            int rc2 = ah_graph_end(d, &cg);
+            if (rc) { ah_graph_destroy(cg); return rc; }
+            if (rc2) return rc2;
+            g = p->graphs.emplace(key, cg).first;
+            p->captures++;
+        } else {
+            p->replays++;
+        }
+        if (int rc = ah_graph_replay(d, g->second)) return rc;
+    } else if (int rc = plan_enqueue(p, n, symbolic)) {
+        return rc;
+    }
+    // Final outputs, widened to f32 (ah_download applies the codec).
     std::vector<ah_output> outs;
-    for (int i = 0; i < n_items; i++) {
-        const ah_buffer_desc &o = items[i].bufs[0];
-        if (read_any.count(o.uop_idx)) continue;
-        bool dup = false;
-        for (auto &x : outs) dup |= x.uop_idx == o.uop_idx;
-        if (dup) continue;
+    for (uint32_t u : p->finals) {
+        const ah_plan::Mem &m = p->mem[u];
         ah_output r;
-        r.uop_idx = o.uop_idx;
-        r.n = st.elems[o.uop_idx];
+        r.uop_idx = u;
+        r.n = m.elems(n);
         r.data = (float *)malloc((size_t)std::max<int64_t>(r.n, 1) * 4);
-        int rc = ah_download(d, r.data, st.ptr[o.uop_idx], r.n, o.dtype);
+        int rc = r.data ? ah_download(d, r.data, m.ptr, r.n, m.dtype) : set_error(AH_ERR_NOMEM, "ah_run: output buffer");
         if (rc) {
             free(r.data);
             for (auto &x : outs) free(x.data);
@@ -230,6 +305,20 @@ int run_impl(ah_device *d, const ah_exec_item *items, int32_t n_items, const ah_
     return AH_OK;
 }
 
+// Binding of the plan's symbolic variable; like the reference, only SymVars[0] of the first symbolic
+// item is looked up (backend/webgpu/executor.go:817-822).
+int find_binding(const ah_plan *p, const char *const *names, const int64_t *values, int32_t n_bind, int64_t *n) {
+    *n = 0;
+    if (!p->has_sym) return AH_OK;
+    for (int b = 0; b < n_bind; b++)
+        if (names && names[b] && values && p->symvar == names[b]) {
+            if (values[b] < 0) return set_error(AH_ERR_INVALID, "binding %s = %lld is negative", names[b], (long long)values[b]);
+            *n = values[b];
+            return AH_OK;
+        }
+    return set_error(AH_ERR_INVALID, "no binding for %s", p->symvar.c_str());
+}
+
 }  // namespace
 }  // namespace ah
 
@@ -239,24 +328,58 @@ extern "C" {
 
 int ah_run(ah_device *d, const ah_exec_item *items, int32_t n_items, const ah_input *inputs, int32_t n_inputs,
            ah_output **outputs, int32_t *n_outputs) {
-    return run_impl(d, items, n_items, inputs, n_inputs, 0, false, outputs, n_outputs);
+    if (!d || (!items && n_items) || (!inputs && n_inputs) || !outputs || !n_outputs)
+        return set_error(AH_ERR_INVALID, "ah_run: null argument");
+    ah_plan p;
+    int rc = plan_build(d, items, n_items, &p);
+    if (rc == AH_OK) rc = plan_run(&p, inputs, n_inputs, 0, false, false, outputs, n_outputs);
+    return rc;
 }
 
 int ah_run_symbolic(ah_device *d, const ah_exec_item *items, int32_t n_items, const ah_input *inputs, int32_t n_inputs,
                     const char *const *bind_names, const int64_t *bind_values, int32_t n_bind, ah_output **outputs,
                     int32_t *n_outputs) {
-    // Like the reference, only the binding of the first symbolic item's SymVars[0] is used
-    // (backend/webgpu/executor.go:817-822).
-    int64_t n = -1;
-    for (int i = 0; i < n_items && n < 0; i++) {
-        if (items[i].n_sym_vars < 1 || !items[i].sym_vars) continue;
-        for (int b = 0; b < n_bind; b++)
-            if (bind_names && bind_names[b] && strcmp(bind_names[b], items[i].sym_vars[0]) == 0) n = bind_values[b];
-        if (n < 0) return set_error(AH_ERR_INVALID, "ah_run_symbolic: no binding for %s", items[i].sym_vars[0]);
+    if (!d || (!items && n_items) || (!inputs && n_inputs) || !outputs || !n_outputs)
+        return set_error(AH_ERR_INVALID, "ah_run_symbolic: null argument");
+    ah_plan p;
+    int rc = plan_build(d, items, n_items, &p);
+    int64_t n = 0;
+    if (rc == AH_OK) {
+        rc = find_binding(&p, bind_names, bind_values, n_bind, &n);
+        if (rc) rc = set_error(rc, "ah_run_symbolic: %s", ah_last_error());
     }
-    if (n < 0) n = 0;
-    return run_impl(d, items, n_items, inputs, n_inputs, n, true, outputs, n_outputs);
+    if (rc == AH_OK) rc = plan_run(&p, inputs, n_inputs, n, true, false, outputs, n_outputs);
+    return rc;
 }
+
+int ah_plan_create(ah_device *d, const ah_exec_item *items, int32_t n_items, ah_plan **out) {
+    if (!d || (!items && n_items) || !out) return set_error(AH_ERR_INVALID, "ah_plan_create: null argument");
+    ah_plan *p = new ah_plan();
+    int rc = plan_build(d, items, n_items, p);
+    if (rc) {
+        delete p;
+        return rc;
+    }
+    *out = p;
+    return AH_OK;
+}
+
+int ah_plan_run(ah_plan *p, const ah_input *inputs, int32_t n_inputs, const char *const *bind_names,
+                const int64_t *bind_values, int32_t n_bind, int32_t flags, ah_output **outputs, int32_t *n_outputs) {
+    if (!p || (!inputs && n_inputs) || !outputs || !n_outputs) return set_error(AH_ERR_INVALID, "ah_plan_run: null argument");
+    int64_t n = 0;
+    if (int rc = find_binding(p, bind_names, bind_values, n_bind, &n)) return set_error(rc, "ah_plan_run: %s", ah_last_error());
+    return plan_run(p, inputs, n_inputs, n, p->has_sym, (flags & AH_PLAN_GRAPH) != 0, outputs, n_outputs);
+}
+
+int ah_plan_stats(const ah_plan *p, int64_t *captures, int64_t *replays) {
+    if (!p) return set_error(AH_ERR_INVALID, "ah_plan_stats: null plan");
+    if (captures) *captures = p->captures;
+    if (replays) *replays = p->replays;
+    return AH_OK;
+}
+
+void ah_plan_destroy(ah_plan *p) { delete p; }
 
 void ah_outputs_free(ah_output *outputs, int32_t n) {
     if (!outputs) return;
@@ -270,14 +393,17 @@ int ah_benchmark(ah_device *d, const ah_exec_item *item, int32_t warmup, int32_t
     ah_kernel *k = nullptr;
     int rc = ah_module_get(d, item->source, "kernel", &k);
     if (rc) return rc;
+    if (k->tmpl && (rc = template_prepare(k->tmpl, 0))) return rc;
     std::vector<void *> ptrs;
     auto release = [&]() { for (void *p : ptrs) hipFree(p); };
     for (int j = 0; j < item->n_bufs; j++) {
         void *p = nullptr;
-        hipError_t e = hipMalloc(&p, (size_t)std::max<int64_t>(item->bufs[j].size, 1) * dtype_bytes(item->bufs[j].dtype));
+        const size_t bytes = (size_t)std::max<int64_t>(item->bufs[j].size, 1) * dtype_bytes(item->bufs[j].dtype);
+        hipError_t e = hipMalloc(&p, bytes);
         if (e != hipSuccess) { release(); return fail_hip(e, "benchmark: hipMalloc"); }
-        hipMemsetAsync(p, 0, (size_t)std::max<int64_t>(item->bufs[j].size, 1) * dtype_bytes(item->bufs[j].dtype), d->stream);
         ptrs.push_back(p);
+        e = zero_fill(p, (long)bytes, d->stream);
+        if (e != hipSuccess) { release(); return fail_hip(e, "benchmark: zero fill"); }
     }
     uint32_t grid[3], block[3];
     for (int a = 0; a < 3; a++) {
@@ -299,6 +425,7 @@ int ah_benchmark(ah_device *d, const ah_exec_item *item, int32_t warmup, int32_t
             us.push_back(ms * 1000.0);
         }
     }
+    hipStreamSynchronize(d->stream);
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     release();

@@ -1,0 +1,32 @@
+// itemops.h — host launchers for the stand-alone kernels behind the executor's "tmpl:" keys.
+#pragma once
+#include "ah_common.h"
+
+namespace ah {
+
+enum RedOp : int { RED_SUM = 0, RED_MAX = 1, RED_SUMSQ = 2 };
+constexpr int kRedRows = 64;   // rows per column-reduce chunk
+
+// Zeroes `bytes` (rounded up to whole 4-byte words) with a kernel, so graph capture records no memset node.
+hipError_t zero_fill(void *p, long bytes, hipStream_t s);
+// out[m] = scale * reduce_n G[m, n] (scale not applied to max); G is f32, or f16 when f16 is set, and the
+// reduction runs in f32.
+hipError_t reduce_rows(const void *G, bool f16, int M, int N, int op, float scale, float *out, hipStream_t s);
+// out[n] = scale * reduce_m G[m, n]; work holds reduce_cols_workspace(M, N) floats. Deterministic.
+long reduce_cols_workspace(int M, int N);
+hipError_t reduce_cols(const void *G, bool f16, int M, int N, int op, float scale, float *work, float *out, hipStream_t s);
+// MaxPool2D over [NC, H, W] with window kH x kW and stride sH x sW (no padding), and its backward.
+hipError_t maxpool_fwd(const float *X, long NC, int H, int W, int kH, int kW, int sH, int sW, float *out, hipStream_t s);
+hipError_t maxpool_bwd(const float *X, const float *adj, long NC, int H, int W, int kH, int kW, int sH, int sW,
+                       float *dX, hipStream_t s);
+// 3x3, padding 1, stride 1 convolution of [N, Ci, H, H] with w [Co, Ci, 3, 3], optional bias and tagged ReLU.
+hipError_t conv3x3_fwd(const float *X, int N, int Ci, int H, const float *w, const float *b, int Co, int relu, float *Y,
+                       hipStream_t s);
+// db[co] = sum of G[n, co, :, :] over n and the HW positions.
+hipError_t conv_bias_grad(const float *G, int N, int Co, int HW, float *db, hipStream_t s);
+// out = p - lr * (scale * g)
+hipError_t sgd_out(const float *p, const float *g, long n, float lr, float scale, float *out, hipStream_t s);
+// out[0] = f16(sum of parts[0..n)) * scale
+hipError_t mse_loss(const float *parts, long n, float scale, float *out, hipStream_t s);
+
+}  // namespace ah

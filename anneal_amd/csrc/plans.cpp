@@ -121,6 +121,8 @@ static hipError_t gemm_run(ah_device *dev, GemmDesc g, hipStream_t s) {
     return gemm_launch(g, s);
 }
 
+hipError_t ah::gemm_dispatch(ah_device *dev, const GemmDesc &g) { return gemm_run(dev, g, dev->stream); }
+
 // Times every f16 variant of g (as given: its epilogue runs on whatever outputs g names) and caches
 // the fastest for g's shape. Two passes over the variants, each variant's time the lower of its two
 // means of `iters` launches, so one disturbed measurement does not decide the choice.
@@ -241,7 +243,7 @@ struct MlpCeTrainer : ah_trainer {
 struct Mlp3Trainer : ah_trainer {
     int B, D0, D1, D2, D3;
     half_t *X, *T, *W1h, *W2h, *W3h, *b1h, *b2h, *b3h, *H1, *H2, *Dd, *dZ2, *dZ1;
-    float *W1, *W2, *W3, *b1, *b2, *b3, *acc, *loss, *gW1, *gW2, *gW3, *gb1, *gb2, *gb3;
+    float *W1, *W2, *W3, *b1, *b2, *b3, *acc, *loss, *lsum, *gW1, *gW2, *gW3, *gb1, *gb2, *gb3;
     int init() {
         B = (int)dims[0]; D0 = (int)dims[1]; D1 = (int)dims[2]; D2 = (int)dims[3]; D3 = (int)dims[4];
         if (B <= 0 || D0 <= 0 || D1 <= 0 || D2 <= 0 || D3 <= 0) return set_error(AH_ERR_INVALID, "MLP3: bad dims");
@@ -254,7 +256,7 @@ struct Mlp3Trainer : ah_trainer {
         rc |= alloc(&b3, D3); rc |= alloc(&b3h, D3);
         rc |= alloc(&H1, (size_t)B * D1); rc |= alloc(&H2, (size_t)B * D2); rc |= alloc(&Dd, (size_t)B * D3);
         rc |= alloc(&dZ2, (size_t)B * D2); rc |= alloc(&dZ1, (size_t)B * D1);
-        rc |= alloc(&acc, acc_floats()); rc |= alloc(&loss, 1);
+        rc |= alloc(&acc, acc_floats()); rc |= alloc(&loss, 1); rc |= alloc(&lsum, 1);
         rc |= alloc(&gW1, (size_t)D1 * D0); rc |= alloc(&gW2, (size_t)D2 * D1); rc |= alloc(&gW3, (size_t)D3 * D2);
         rc |= alloc(&gb1, D1); rc |= alloc(&gb2, D2); rc |= alloc(&gb3, D3);
         if (rc) return AH_ERR_HIP;
@@ -301,8 +303,9 @@ struct Mlp3Trainer : ah_trainer {
     int get(int slot, void *h, int64_t n) override {
         struct { void *p; int64_t n; } t[] = {{nullptr, 0}, {nullptr, 0}, {W1, (int64_t)D1 * D0}, {b1, D1},
             {W2, (int64_t)D2 * D1}, {b2, D2}, {W3, (int64_t)D3 * D2}, {b3, D3}, {loss, 1},
-            {gW1, (int64_t)D1 * D0}, {gb1, D1}, {gW2, (int64_t)D2 * D1}, {gb2, D2}, {gW3, (int64_t)D3 * D2}, {gb3, D3}};
-        if (slot < 2 || slot > 14) return set_error(AH_ERR_INVALID, "MLP3: bad slot %d", slot);
+            {gW1, (int64_t)D1 * D0}, {gb1, D1}, {gW2, (int64_t)D2 * D1}, {gb2, D2}, {gW3, (int64_t)D3 * D2}, {gb3, D3},
+            {lsum, 1}};
+        if (slot < 2 || slot > 15) return set_error(AH_ERR_INVALID, "MLP3: bad slot %d", slot);
         if (n > t[slot].n) return set_error(AH_ERR_INVALID, "MLP3: slot %d too small", slot);
         return copy_out(dev, h, t[slot].p, (size_t)n * 4);
     }
@@ -486,7 +489,7 @@ struct Mlp3Trainer : ah_trainer {
         ta.seg[1] = {b2, b2h, db2p(), sg ? gb2 : nullptr, D2, bs, R, D2};
         ta.seg[2] = {b1, b1h, db1p(), sg ? gb1 : nullptr, D1, bs, R, D1};
         ta.nseg = 3; ta.lr = lr; ta.loss_mode = 1; ta.lossacc = lossp(); ta.loss_parts = R * lblocks();
-        ta.loss_scale = sc; ta.loss_out = loss;
+        ta.loss_scale = sc; ta.loss_out = loss; ta.loss_sum = sg ? lsum : nullptr;
         LAUNCH("tail", step_tail(ta, s));
         return AH_OK;
     }

@@ -42,6 +42,7 @@ struct TailArgs {
     const float *rowloss;
     int nrow;
     float *loss_out;
+    float *loss_sum;  // loss_mode 1, optional: the f32 sum before the f16 narrowing
 };
 hipError_t step_tail(const TailArgs &t, hipStream_t s);
 

@@ -84,6 +84,7 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float *G, int M, int 
 // loss = Sum(onehot * logp) * a,  a = f32(-1/B); see the oracle's ora_softmax_ce for the op list.
 __global__ __launch_bounds__(256) void softmax_ce_kernel(const float *z, const int32_t *labels, int B, int C,
                                                           float a, float *dz, float *rowloss) {
+#pragma clang fp contract(off)   // each reference op rounds on its own (no fused multiply-add)
     int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     int lane = threadIdx.x & 63;
     if (row >= B) return;
@@ -369,9 +370,13 @@ __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
                 t.lossacc[i] = 0.0f;
             }
             acc = block_sum_512(acc, red);
-            if (threadIdx.x == 0) t.loss_out[0] = q16(acc) * t.loss_scale;
+            if (threadIdx.x == 0) {
+                t.loss_out[0] = q16(acc) * t.loss_scale;
+                if (t.loss_sum) t.loss_sum[0] = acc;
+            }
         } else if (t.loss_mode == 1) {
             if (threadIdx.x == 0) {
+                if (t.loss_sum) t.loss_sum[0] = t.lossacc[0];
                 t.loss_out[0] = q16(t.lossacc[0]) * t.loss_scale;   // f16(acc) narrowing, lower.go:712
                 t.lossacc[0] = 0.0f;
             }

@@ -289,7 +289,7 @@ int ah_module_get(ah_device *d, const char *source, const char *entry, ah_kernel
 int ah_launch(ah_device *d, ah_kernel *k, const uint32_t grid[3], const uint32_t block[3], void *const *ptrs,
               int32_t n_ptrs, const int32_t *scalars, int32_t n_scalars) {
     if (!d || !k) return set_error(AH_ERR_INVALID, "ah_launch: null argument");
-    if (k->tmpl) return k->tmpl->run(d, ptrs, n_ptrs, scalars, n_scalars);
+    if (k->tmpl) return k->tmpl->run(d, k->tmpl, ptrs, n_ptrs, scalars, n_scalars);
     if (!grid || !block) return set_error(AH_ERR_INVALID, "ah_launch: null grid/block");
     std::vector<void *> args;
     std::vector<void *> pv(ptrs, ptrs + n_ptrs);

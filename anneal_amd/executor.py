@@ -1,4 +1,5 @@
-"""backend.Executor / Benchmarker / SymbolicExecutor mirror over the C ABI (backend/device.go:10-37).
+"""backend.Executor / Benchmarker / SymbolicExecutor mirror over the C ABI (backend/device.go:10-37),
+and Plan, the device half of tensor.JIT (tensor/jit.go:47-359).
 
 ExecItem fields follow schedule/exec.go:6-32; `source` replaces the WGSL string and is HIP source
 (compiled once per device by hiprtc) or a "tmpl:" key naming a hand-written kernel.
@@ -85,6 +86,11 @@ class Executor:
         self.dev.lib.ah_outputs_free(outs, n)
         return res
 
+    def _bind(self, binding: dict):
+        names = (C.c_char_p * max(len(binding), 1))(*[k.encode() for k in binding])
+        vals = (C.c_int64 * max(len(binding), 1))(*binding.values())
+        return names, vals
+
     def run(self, items, inputs: dict) -> dict:
         m = _Marshal(items)
         ins, keep = self._inputs(inputs)
@@ -96,8 +102,7 @@ class Executor:
     def run_symbolic(self, items, inputs: dict, binding: dict) -> dict:
         m = _Marshal(items)
         ins, keep = self._inputs(inputs)
-        names = (C.c_char_p * max(len(binding), 1))(*[k.encode() for k in binding])
-        vals = (C.c_int64 * max(len(binding), 1))(*binding.values())
+        names, vals = self._bind(binding)
         outs, n = C.POINTER(L.ah_output)(), C.c_int32()
         L.check(self.dev.lib.ah_run_symbolic(self.dev.h, m.arr, len(items), ins, len(inputs), names, vals,
                                              len(binding), C.byref(outs), C.byref(n)))
@@ -109,3 +114,37 @@ class Executor:
         r = L.ah_bench_result()
         L.check(self.dev.lib.ah_benchmark(self.dev.h, m.arr, warmup, iterations, C.byref(r)))
         return BenchmarkResult(r.min_us, r.median_us, r.max_us, r.mean_us, r.stddev_us, r.cv)
+
+
+class Plan:
+    """An item list kept alive on the device: kernels resolved and buffers allocated once, and with
+    graph=True each binding's kernel sequence captured once as a HIP graph and replayed afterwards.
+    run() has Run / RunSymbolic's contract (binding None for a static list)."""
+
+    def __init__(self, device, items, graph: bool = True):
+        self.dev, self.ex, self.graph = device, Executor(device), graph
+        m = _Marshal(items)
+        h = C.c_void_p()
+        L.check(device.lib.ah_plan_create(device.h, m.arr, len(items), C.byref(h)))
+        self.h = h.value
+
+    def run(self, inputs: dict, binding: dict | None = None) -> dict:
+        ins, keep = self.ex._inputs(inputs)
+        binding = binding or {}
+        names, vals = self.ex._bind(binding)
+        outs, n = C.POINTER(L.ah_output)(), C.c_int32()
+        L.check(self.dev.lib.ah_plan_run(self.h, ins, len(inputs), names, vals, len(binding),
+                                         L.PLAN_GRAPH if self.graph else 0, C.byref(outs), C.byref(n)))
+        _ = keep
+        return self.ex._collect(outs, n)
+
+    def stats(self):
+        """(captures, replays), as tensor.JIT.JITStats."""
+        c, r = C.c_int64(), C.c_int64()
+        L.check(self.dev.lib.ah_plan_stats(self.h, C.byref(c), C.byref(r)))
+        return c.value, r.value
+
+    def close(self) -> None:
+        if self.h:
+            self.dev.lib.ah_plan_destroy(self.h)
+            self.h = None

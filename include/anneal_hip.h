@@ -31,6 +31,7 @@ typedef struct ah_device ah_device;
 typedef struct ah_kernel ah_kernel;
 typedef struct ah_graph ah_graph;
 typedef struct ah_trainer ah_trainer;
+typedef struct ah_plan ah_plan;
 
 typedef struct {
     int32_t has_f16;     /* shader-f16 equivalent (always 1 on gfx950) */
@@ -144,6 +145,21 @@ int ah_benchmark(ah_device *dev, const ah_exec_item *item, int32_t warmup, int32
                  ah_bench_result *out);                                     /* Benchmark, device.go:27-29 */
 void ah_outputs_free(ah_output *outputs, int32_t n);
 
+/* Persistent plans: the device half of tensor.JIT (tensor/jit.go:47-359), which captures one item list and
+ * replays it through Run / RunSymbolic with fresh leaf data every step (replayStatic / replaySym,
+ * jit.go:178-215). ah_plan_create copies the items, resolves every kernel once (compile errors surface here)
+ * and ah_plan_run runs them with Run's contract (zeroed buffers, leaves from `inputs`, final outputs
+ * returned as by ah_run). Buffers stay allocated between runs and grow when a larger symbolic binding
+ * arrives. With AH_PLAN_GRAPH the kernel sequence of each binding is captured once as a HIP graph and
+ * replayed afterwards (uploads and downloads stay outside the graph). ah_plan_stats reports
+ * (captures, replays) like JIT.JITStats (jit.go:71-74). A plan belongs to its device handle's stream. */
+#define AH_PLAN_GRAPH 1
+int ah_plan_create(ah_device *dev, const ah_exec_item *items, int32_t n_items, ah_plan **out);
+int ah_plan_run(ah_plan *plan, const ah_input *inputs, int32_t n_inputs, const char *const *bind_names,
+                const int64_t *bind_values, int32_t n_bind, int32_t flags, ah_output **outputs, int32_t *n_outputs);
+int ah_plan_stats(const ah_plan *plan, int64_t *captures, int64_t *replays);
+void ah_plan_destroy(ah_plan *plan);
+
 /* ── Hot-path kernels, callable directly ────────────────────────────────────── */
 
 /* GEMM-shaped REDUCE(ADD, MUL) with fused epilogue (tensor/reduce.go:105-166 as scheduled for
@@ -229,7 +245,7 @@ enum {
  *  CONVNET: 0 x, 1 labels, 2 cw1, 3 cb1, 4 cw2, 5 cb2, 6 fw, 7 fb, 8 loss, 9 dcw1, 10 dcb1, 11 dcw2,
  *           12 dcb2, 13 dfw, 14 dfb
  *  MLP3   : 0 x, 1 t, 2 W1, 3 b1, 4 W2, 5 b2, 6 W3, 7 b3, 8 loss, 9 dW1, 10 db1, 11 dW2, 12 db2,
- *           13 dW3, 14 db3
+ *           13 dW3, 14 db3, 15 loss_sum (the f32 sum of squares before the f16 narrowing of the loss)
  *  CHAIN  : 0 X, 1 g, 2 loss, 3 dX, 4 dg
  * Gradient slots are filled only by steps run with AH_STEP_STORE_GRADS.
  * Creating an MLP3 trainer tunes its f16 contractions for shapes the device has not tuned yet: each alone

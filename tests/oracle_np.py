@@ -14,7 +14,8 @@ def q16(a):
 
 
 def mlp3_step_np(p: dict, lr: float):
-    """Same contract as oracle_lib.mlp3_step: x, t f16-representable; returns (loss, grads, new params)."""
+    """Same contract as oracle_lib.mlp3_step: x, t f16-representable; returns (loss, grads, new params);
+    grads also holds "loss_sum", the f32 sum of squared differences before the f16 narrowing."""
     x, t = np.asarray(p["x"], np.float32), np.asarray(p["t"], np.float32)
     prm = {k: np.asarray(p[k], np.float32).copy() for k in ("W1", "b1", "W2", "b2", "W3", "b3")}
     w1, w2, w3 = q16(prm["W1"]), q16(prm["W2"]), q16(prm["W3"])
@@ -31,7 +32,7 @@ def mlp3_step_np(p: dict, lr: float):
     loss = float(q16(acc) * scale)
     d = q16(d32)
     gP = scale * d + scale * d
-    g = {}
+    g = {"loss_sum": float(acc)}   # the f32 sum of squares before the f16 narrowing
     g["db3"] = gP.sum(0, dtype=np.float64).astype(np.float32)
     g["dW3"] = gP.T @ H2
     dH2 = np.where(Z2 == H2, gP @ w3, np.float32(0))
@@ -56,3 +57,39 @@ def chain_dX_f64(X, g):
     G = np.asarray(g, np.float64)[:, None]
     dS = G * r - G * S.sum(1, keepdims=True) * r ** 3 * S / R
     return (S * (dS - (S * dS).sum(1, keepdims=True))).T
+
+
+def mlp_ce_step_f64(p: dict, lr: float):
+    """Float64 closed form of ora_mlp_ce_step (configs 1 and 4) for batches the C oracle's serial loops
+    take tens of seconds on: Linear ReLU Linear, loss = Sum(onehot * logsoftmax) * (-1/B), ReLU'(0) = 1
+    (Where(z == relu(z)), tensor/gradient_ruleset.go:153-161), dz = (softmax - onehot) / B (the row-max
+    path's tie share is zero in exact arithmetic). test_oracle_np_matches_c_oracle pins it to the C
+    oracle at small batches. Returns (loss, grads, new params) like oracle_lib.mlp_ce_step."""
+    x = np.asarray(p["x"], np.float64)
+    lab = np.asarray(p["labels"], np.int64)
+    W1, b1, W2, b2 = (np.asarray(p[k], np.float64) for k in ("W1", "b1", "W2", "b2"))
+    B = x.shape[0]
+    Z1 = x @ W1.T + b1
+    H1 = np.maximum(Z1, 0.0)
+    Z = H1 @ W2.T + b2
+    Zs = Z - Z.max(1, keepdims=True)
+    lse = np.log(np.exp(Zs).sum(1, keepdims=True))
+    logp = Zs - lse
+    onehot = np.zeros_like(Z)
+    onehot[np.arange(B), lab] = 1.0
+    loss = float((onehot * logp).sum() * (-1.0 / B))
+    dZ = (np.exp(logp) - onehot) / B
+    dZ1 = np.where(Z1 >= 0, dZ @ W2, 0.0)
+    g = {"dW2": dZ.T @ H1, "db2": dZ.sum(0), "dW1": dZ1.T @ x, "db1": dZ1.sum(0)}
+    new = {k: np.asarray(p[k], np.float64) - lr * g["d" + k] for k in ("W1", "b1", "W2", "b2")}
+    return loss, g, new
+
+
+def relu_ambiguous_units(p: dict, atol: float = 1e-5):
+    """Hidden units whose ReLU mask an f32 evaluation may set differently from another one: some batch
+    row has |z| below atol (about ten times the f32 rounding of these 512-term pre-activations). Rounding decides Where(z == relu(z)) there, so a gradient row of such
+    a unit is an O(1) difference between two correct f32 implementations; large-batch checks against the
+    float64 closed form leave these rows (a few of thousands) out."""
+    x = np.asarray(p["x"], np.float64)
+    Z1 = x @ np.asarray(p["W1"], np.float64).T + np.asarray(p["b1"], np.float64)
+    return np.nonzero((np.abs(Z1) < atol).any(0))[0]

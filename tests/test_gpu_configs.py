@@ -58,6 +58,30 @@ def test_config4_dynmlp_step_graph_replay(dev, N):
     check_mlp(run_mlp_ce(dev, p, N, 0.01, graph=True), p, 0.01)
 
 
+def test_config4_n4096_vs_f64_closed_form(dev):
+    """Config 4 at N = 4096 (graph replay) against the float64 closed form of the oracle's step, which
+    test_mlp_ce_f64_closed_form_matches_c_oracle pins to the C oracle (the C oracle alone needs about
+    20 s on 8 cores at this batch)."""
+    from oracle_np import mlp_ce_step_f64, relu_ambiguous_units
+    N = 4096
+    p = data.mlp_ce_inputs(N, 512, 2048, 512, x_lo=-1.0, x_hi=1.0)
+    out = run_mlp_ce(dev, p, N, 0.01, graph=True)
+    wl, g, new = mlp_ce_step_f64(p, 0.01)
+    # hidden units whose ReLU mask rounding may decide either way are left out of the layer-1 rows
+    amb = relu_ambiguous_units(p)
+    assert len(amb) < 128
+    keep1 = lambda a, n: np.delete(np.asarray(a).reshape(2048, n), amb, 0)   # noqa: E731
+    assert abs(out["loss"] - wl) <= 1e-4 * max(1, abs(wl))
+    assert O.relerr(keep1(out["dW1"], 512), keep1(g["dW1"], 512)) < 1e-4
+    assert O.relerr(keep1(out["db1"], 1), keep1(g["db1"], 1)) < 1e-4
+    for k in ("dW2", "db2"):
+        assert O.relerr(out[k], g[k].ravel()) < 1e-4, k
+    for k, n in (("W1", 512), ("b1", 1)):
+        assert check_update(keep1(out[k], n), keep1(p[k], n), keep1(new[k], n), 1e-4), k
+    for k in ("W2", "b2"):
+        assert check_update(out[k], p[k], new[k], 1e-4), k
+
+
 def test_config4_one_capture_many_batches(dev):
     """One trainer sized for 4096 replays captured graphs for N in {1, 7, 256}; each equals an eager step."""
     Bmax = 4096
@@ -115,7 +139,7 @@ def run_mlp3(dev, p, lr):
     for k in ("x", "t", "W1", "b1", "W2", "b2", "W3", "b3"):
         t.set(k, p[k])
     t.step(B, store_grads=True)
-    out = {"loss": t.get("loss", 1)[0]}
+    out = {"loss": t.get("loss", 1)[0], "loss_sum": t.get("loss_sum", 1)[0]}
     for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3", "W1", "b1", "W2", "b2", "W3", "b3"):
         out[k] = t.get(k, p[k.lstrip("d")].size if k.startswith("d") else p[k].size)
     t.close()
@@ -176,8 +200,13 @@ def test_config3_full_size_vs_numpy_restatement(dev):
         wl, g, new = mlp3_step_np(q, lr)
     out = run_mlp3(dev, p, lr)
     assert (np.isinf(out["loss"]) and np.isinf(wl)) or abs(out["loss"] - wl) < 2e-2 * abs(wl)
+    # the f32 sum of squares before the f16 narrowing is finite: compare it directly
+    margins = {"loss_sum": abs(out["loss_sum"] - g["loss_sum"]) / g["loss_sum"]}
     for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3"):
-        assert O.relerr(out[k], g[k].ravel()) < 2e-2, k
+        margins[k] = O.relerr(out[k], g[k].ravel())
+    print("config-3 full-size relative errors (bar 2e-2):", {k: f"{v:.2e}" for k, v in margins.items()})
+    for k, v in margins.items():
+        assert v < 2e-2, k
     for k in ("W1", "b1", "W2", "b2", "W3", "b3"):
         assert check_update(out[k], p[k], new[k], 2e-2), k
 

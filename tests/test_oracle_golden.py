@@ -338,3 +338,17 @@ def test_chain_closed_form_f64_matches_oracle():
     mask[X.argmax(0), np.arange(96)] = True
     assert np.max(np.abs(wdX - ex)[~mask]) / np.max(np.abs(ex)) < 1e-5
     assert np.max(np.abs(ex.sum(0))) < 1e-12 * X.shape[0]
+
+
+@pytest.mark.parametrize("B,D,H,Cn", [(64, 784, 128, 10), (256, 512, 2048, 512)])
+def test_mlp_ce_f64_closed_form_matches_c_oracle(B, D, H, Cn):
+    """The float64 closed form used for config 4 at N = 4096 agrees with the C oracle where the oracle is
+    fast (its f32 rounding is the only difference)."""
+    from anneal_amd import data
+    from oracle_np import mlp_ce_step_f64
+    p = data.mlp_ce_inputs(B, D, H, Cn, seed=11, x_lo=-1.0, x_hi=1.0)
+    wl, g, new = O.mlp_ce_step(p, 0.01)
+    fl, fg, fnew = mlp_ce_step_f64(p, 0.01)
+    assert abs(fl - wl) <= 1e-5 * max(1.0, abs(wl))
+    for k in g:
+        assert O.relerr(g[k], fg[k]) < 1e-5, k
