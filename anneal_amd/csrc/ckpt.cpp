@@ -16,6 +16,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <string.h>
+#include <zlib.h>
 
 #include <algorithm>
 #include <map>
@@ -54,34 +55,83 @@ struct Json {
     std::string err;
     void ws() { while (p < e && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) p++; }
     bool lit(char c) { ws(); if (p < e && *p == c) { p++; return true; } return false; }
+    // 4 hex digits at p (advances p); false if malformed
+    bool hex4(uint32_t &v) {
+        if (e - p < 4) return false;
+        v = 0;
+        for (int i = 0; i < 4; i++) {
+            const char c = *p++;
+            v <<= 4;
+            if (c >= '0' && c <= '9') v |= (uint32_t)(c - '0');
+            else if (c >= 'a' && c <= 'f') v |= (uint32_t)(c - 'a' + 10);
+            else if (c >= 'A' && c <= 'F') v |= (uint32_t)(c - 'A' + 10);
+            else return false;
+        }
+        return true;
+    }
+    static void utf8(std::string &out, uint32_t cp) {
+        if (cp < 0x80) out += (char)cp;
+        else if (cp < 0x800) { out += (char)(0xC0 | (cp >> 6)); out += (char)(0x80 | (cp & 0x3F)); }
+        else if (cp < 0x10000) {
+            out += (char)(0xE0 | (cp >> 12)); out += (char)(0x80 | ((cp >> 6) & 0x3F)); out += (char)(0x80 | (cp & 0x3F));
+        } else {
+            out += (char)(0xF0 | (cp >> 18)); out += (char)(0x80 | ((cp >> 12) & 0x3F));
+            out += (char)(0x80 | ((cp >> 6) & 0x3F)); out += (char)(0x80 | (cp & 0x3F));
+        }
+    }
+    // A JSON string with every escape JSON defines: \" \\ \/ \b \f \n \r \t and \uXXXX (surrogate
+    // pairs joined), decoded to UTF-8. Go's json.Marshal writes <, > and & as \u003c, \u003e, \u0026.
     bool str(std::string &out) {
         ws();
         if (p >= e || *p != '"') { err = "expected a string"; return false; }
         p++;
         out.clear();
         while (p < e && *p != '"') {
-            if (*p == '\\') {
-                p++;
-                if (p >= e) break;
-                char c = *p;
-                if (c == 'u') { out += '?'; p += 4; }   // names with escapes are not produced by the writers
-                else out += c == 'n' ? '\n' : c == 't' ? '\t' : c;
-                p++;
-            } else {
-                out += *p++;
+            if (*p != '\\') { out += *p++; continue; }
+            if (++p >= e) break;
+            const char c = *p++;
+            switch (c) {
+            case '"': case '\\': case '/': out += c; break;
+            case 'b': out += '\b'; break;
+            case 'f': out += '\f'; break;
+            case 'n': out += '\n'; break;
+            case 'r': out += '\r'; break;
+            case 't': out += '\t'; break;
+            case 'u': {
+                uint32_t cp;
+                if (!hex4(cp)) { err = "bad \\u escape"; return false; }
+                if (cp >= 0xD800 && cp < 0xDC00) {   // high surrogate: a low one must follow
+                    uint32_t lo;
+                    if (e - p < 6 || p[0] != '\\' || p[1] != 'u') { err = "unpaired surrogate"; return false; }
+                    p += 2;
+                    if (!hex4(lo) || lo < 0xDC00 || lo >= 0xE000) { err = "unpaired surrogate"; return false; }
+                    cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+                } else if (cp >= 0xDC00 && cp < 0xE000) {
+                    err = "unpaired surrogate";
+                    return false;
+                }
+                utf8(out, cp);
+                break;
+            }
+            default: err = "bad escape"; return false;
             }
         }
         if (p >= e) { err = "unterminated string"; return false; }
         p++;
         return true;
     }
+    // An integer bounded by the header's end (the digits are copied out, so strtoll never reads past e).
     bool integer(int64_t &v) {
         ws();
+        char buf[32];
+        int n = 0;
+        while (p + n < e && n < 31 && (p[n] == '-' || (p[n] >= '0' && p[n] <= '9'))) { buf[n] = p[n]; n++; }
+        buf[n] = 0;
         char *end = nullptr;
-        long long x = strtoll(p, &end, 10);
-        if (end == p) { err = "expected an integer"; return false; }
+        long long x = strtoll(buf, &end, 10);
+        if (n == 0 || end != buf + n || n == 31) { err = "expected an integer"; return false; }
         v = x;
-        p = end;
+        p += n;
         return true;
     }
     bool int_array(std::vector<int64_t> &v) {
@@ -122,6 +172,7 @@ struct Json {
 struct ah_ckpt {
     std::vector<unsigned char> bytes;
     std::vector<ah::Entry> entries;
+    std::vector<std::vector<unsigned char>> inflated;   // decompressed .npz members (entries point into them)
 };
 
 namespace ah {
@@ -263,17 +314,44 @@ bool parse_npz(ah_ckpt *c, std::string *err) {
     for (int k = 0; k < count; k++) {
         if (cd + 46 > b.size() || rd32(&b[cd]) != 0x02014b50u) { *err = "bad ZIP central directory"; return false; }
         const uint16_t method = rd16(&b[cd + 10]);
-        const uint32_t csize = rd32(&b[cd + 20]);
+        const uint32_t csize = rd32(&b[cd + 20]), usize = rd32(&b[cd + 24]);
         const uint16_t nlen = rd16(&b[cd + 28]), xlen = rd16(&b[cd + 30]), clen = rd16(&b[cd + 32]);
         const uint32_t lho = rd32(&b[cd + 42]);
+        if (cd + 46 + (size_t)nlen + xlen + clen > b.size()) { *err = "bad ZIP central directory entry"; return false; }
         std::string name((const char *)&b[cd + 46], nlen);
         cd += 46 + nlen + xlen + clen;
-        if (method != 0) { *err = "npz entry " + name + " is compressed; only stored entries are read"; return false; }
-        if (lho + 30 > b.size() || rd32(&b[lho]) != 0x04034b50u) { *err = "bad ZIP local header for " + name; return false; }
-        const size_t start = lho + 30 + rd16(&b[lho + 26]) + rd16(&b[lho + 28]);
+        if (method != 0 && method != 8) {
+            *err = "npz entry " + name + ": ZIP method " + std::to_string(method) + " (stored and deflate are read)";
+            return false;
+        }
+        if (csize == 0xFFFFFFFFu || usize == 0xFFFFFFFFu || lho == 0xFFFFFFFFu) {
+            *err = "npz entry " + name + " needs ZIP64, which is not read";
+            return false;
+        }
+        if ((size_t)lho + 30 > b.size() || rd32(&b[lho]) != 0x04034b50u) { *err = "bad ZIP local header for " + name; return false; }
+        const size_t start = (size_t)lho + 30 + rd16(&b[lho + 26]) + rd16(&b[lho + 28]);
         if (start + csize > b.size()) { *err = "truncated npz entry " + name; return false; }
+        const unsigned char *member = &b[start];
+        size_t member_size = csize;
+        if (method == 8) {   // raw deflate, as np.savez_compressed writes
+            std::vector<unsigned char> out(std::max<uint32_t>(usize, 1));
+            z_stream zs;
+            memset(&zs, 0, sizeof zs);
+            if (inflateInit2(&zs, -MAX_WBITS) != Z_OK) { *err = "inflate init failed"; return false; }
+            zs.next_in = const_cast<unsigned char *>(member);
+            zs.avail_in = csize;
+            zs.next_out = out.data();
+            zs.avail_out = usize;
+            const int zr = inflate(&zs, Z_FINISH);
+            const size_t got = zs.total_out;
+            inflateEnd(&zs);
+            if (zr != Z_STREAM_END || got != usize) { *err = "npz entry " + name + ": corrupt deflate data"; return false; }
+            c->inflated.push_back(std::move(out));
+            member = c->inflated.back().data();
+            member_size = usize;
+        }
         Entry en;
-        if (!parse_npy(&b[start], csize, en, err)) { *err = name + ": " + *err; return false; }
+        if (!parse_npy(member, member_size, en, err)) { *err = name + ": " + *err; return false; }
         if (name.size() > 4 && name.compare(name.size() - 4, 4, ".npy") == 0) name.resize(name.size() - 4);
         en.name = name;
         c->entries.push_back(en);

@@ -266,7 +266,7 @@ int ah_trainer_kernel_count(ah_trainer *t, int64_t batch, int32_t *count);
 
 /* ── Checkpoint formats (host side; no device needed) ─────────────────────────
  * Readers for safetensors (tensor/safetensors/safetensors.go:150-434 Load / LoadTensors), NumPy .npy and
- * stored .npz (tensor/npy/npy.go:41-466 Load / LoadNPZ), decoding every tensor to f32 with the reference's
+ * .npz with stored or deflated members (tensor/npy/npy.go:41-466 Load / LoadNPZ), decoding every tensor to f32 with the reference's
  * dtype policy (safetensors.go:21-35, npy.go:3-16): F32 exact, F64 -> f32, F16 / BF16 widened (safetensors),
  * integers by value with an error past 2^24, BOOL -> 0/1, any other dtype an error naming it; Fortran-order
  * arrays come back in C order. The decoded values are what a trainer uploads with ah_trainer_set. */

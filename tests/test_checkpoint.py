@@ -146,3 +146,70 @@ def test_missing_file_and_garbage(tmp_path):
     p.write_bytes(struct.pack("<Q", 1 << 40) + b"{}")
     with pytest.raises(L.AnnealHipError, match="header length"):
         ck.load_tensors(str(p))
+
+
+def test_npz_compressed_members(tmp_path):
+    """np.savez_compressed writes deflated ZIP members; Go's archive/zip (the reference's LoadNPZ,
+    tensor/npy/npy.go:51-78) reads them, and so does this reader."""
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((7, 5)).astype(np.float32)
+    b = np.arange(12, dtype=np.int32).reshape(3, 4)
+    p = tmp_path / "c.npz"
+    np.savez_compressed(p, a=a, b=b, empty=np.zeros((0, 3), np.float32))
+    t = ck.load_tensors(str(p))
+    np.testing.assert_array_equal(t["a"], a)
+    np.testing.assert_array_equal(t["b"], b.astype(np.float32))
+    assert t["empty"].shape == (0, 3)
+
+
+def _safetensors_with_header(p, header: bytes, data: bytes):
+    p.write_bytes(struct.pack("<Q", len(header)) + header + data)
+
+
+def test_safetensors_json_escapes_in_names(tmp_path):
+    """Go's json.Marshal (safetensors.Save) writes <, > and & as \\u003c, \\u003e and \\u0026; names with
+    every JSON escape, and a surrogate pair, decode to the same UTF-8 name."""
+    data = np.arange(2, dtype=np.float32).tobytes()
+    names = {r"a<b&c>": "a<b&c>", r"q\"\\\/\b\f\n\r\t": "q\"\\/\b\f\n\r\t",
+             r"é😀": "é\U0001F600"}
+    for raw, want in names.items():
+        p = tmp_path / "e.safetensors"
+        hdr = ('{"%s":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}' % raw).encode()
+        _safetensors_with_header(p, hdr, data)
+        t = ck.load_tensors(str(p))
+        assert list(t) == [want]
+        np.testing.assert_array_equal(t[want], [0, 1])
+
+
+def test_safetensors_writer_escapes_round_trip(tmp_path):
+    p = str(tmp_path / "w.safetensors")
+    name = "ctl\x01\ttab<&>é"
+    ck.save_safetensors(p, {name: np.ones(3, np.float32)})
+    assert list(ck.load_tensors(p)) == [name]
+
+
+@pytest.mark.parametrize("cut", [9, 20, 40, -3])
+def test_truncated_files_fail_cleanly(tmp_path, cut):
+    """Files cut short anywhere (header length, header, directory) raise an error, never read past the end."""
+    src = tmp_path / "full.npz"
+    np.savez(src, a=np.arange(6, dtype=np.float32))
+    raw = src.read_bytes()
+    p = tmp_path / "cut.npz"
+    p.write_bytes(raw[:cut])
+    with pytest.raises(L.AnnealHipError):
+        ck.load_tensors(str(p))
+    hdr = b'{"w":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}'
+    q = tmp_path / "cut.safetensors"
+    full = struct.pack("<Q", len(hdr)) + hdr + np.zeros(2, np.float32).tobytes()
+    q.write_bytes(full[:cut])
+    with pytest.raises(L.AnnealHipError):
+        ck.load_tensors(str(q))
+
+
+def test_bad_json_escapes_are_errors(tmp_path):
+    for raw in (r"bad\x", r"\ud83d", r"\u12"):
+        p = tmp_path / "b.safetensors"
+        hdr = ('{"%s":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}' % raw).encode()
+        _safetensors_with_header(p, hdr, np.zeros(2, np.float32).tobytes())
+        with pytest.raises(L.AnnealHipError):
+            ck.load_tensors(str(p))
