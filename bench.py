@@ -56,7 +56,21 @@ def config_workload(cfg: int):
         meta = {"workload": "config5_chain_8192x4096_permute_pad_shrink_softmax_rmsnorm", "batch": Cc,
                 "bytes_per_step": 8.0 * R * Cc + 8 * Cc, "dtype": "f32"}
         return L.TRAIN_CHAIN, [R, Cc], 0.0, R, p, ks, meta
-    raise SystemExit(f"bench: config {cfg} is a parity-test case; bench lines cover configs 3 and 5")
+    if cfg in (1, 4):
+        B, D, H, C = (64, 784, 128, 10) if cfg == 1 else (4096, 512, 2048, 512)
+        p = data.mlp_ce_inputs(B, D, H, C, **({} if cfg == 1 else {"x_lo": -1.0, "x_hi": 1.0}))
+        ks = mlp_ce_kernels(B, D, H, C)
+        wl = "config1_mlp_784-128-10_b64_f32" if cfg == 1 else "config4_dynmlp_512-2048-512_f32_N4096"
+        meta = {"workload": wl, "batch": B, "dtype": "f32",
+                "flop_per_step": sum(a for _, k, a in ks if k.startswith("flop"))}
+        return L.TRAIN_MLP_CE, [B, D, H, C], 0.01, B, p, ks, meta
+    if cfg == 2:
+        p = data.convnet_inputs()
+        ks = convnet_kernels()
+        meta = {"workload": "config2_convnet_b32_f32", "batch": 32, "dtype": "f32",
+                "flop_per_step": sum(a for _, k, a in ks if k.startswith("flop"))}
+        return L.TRAIN_CONVNET, [32, 28, 8, 16, 10], 0.01, 32, p, ks, meta
+    raise SystemExit(f"bench: unknown config {cfg}")
 
 
 def cpu_baseline(cfg: int, inputs: dict):
@@ -77,6 +91,26 @@ def cpu_baseline(cfg: int, inputs: dict):
         return {"value": 1.0 / full, "unit": "train steps/s", "cores": threads, "kind": "port",
                 "sample": f"one oracle step at batch {Bs} of 4096 (full layer widths), {dt:.1f} s, "
                           f"scaled x{4096 // Bs} to a full step"}
+    if cfg == 4:
+        Bs = 512
+        q = dict(inputs)
+        q["x"], q["labels"] = inputs["x"][:Bs], inputs["labels"][:Bs]
+        t0 = time.perf_counter()
+        O.mlp_ce_step(q, 0.01)
+        dt = time.perf_counter() - t0
+        return {"value": 1.0 / (dt * 4096 / Bs), "unit": "train steps/s", "cores": threads, "kind": "port",
+                "sample": f"one oracle step at batch {Bs} of 4096, {dt:.1f} s, scaled x{4096 // Bs} to a full step"}
+    if cfg in (1, 2):
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0:
+            if cfg == 2:
+                O.convnet_step(inputs, 0.01)
+            else:
+                O.mlp_ce_step(inputs, 0.01)
+            n += 1
+        dt = time.perf_counter() - t0
+        return {"value": n / dt, "unit": "train steps/s", "cores": threads, "kind": "port",
+                "sample": f"{n} full oracle steps in {dt:.1f} s"}
     if cfg == 5:
         n, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < 10.0:
@@ -88,9 +122,69 @@ def cpu_baseline(cfg: int, inputs: dict):
     return None
 
 
+def mlp_ce_kernels(B, D, H, C):
+    """The MLP_CE trainer's launches (configs 1 and 4) with their algorithmic work."""
+    f = lambda m, n, k: ("flop32", 2.0 * m * n * k)  # noqa: E731
+    return [("fc1", *f(B, H, D)), ("fc2", *f(B, C, H)), ("softmax_ce", "bytes", 8.0 * B * C + 8.0 * B),
+            ("db2", "bytes", 4.0 * B * C), ("dH1", *f(B, H, C)), ("dW2", *f(C, H, B)), ("dW1", *f(H, D, B)),
+            ("tail", "bytes", 4.0 * B + 16.0 * (H + C))]
+
+
+def convnet_kernels(N=32, Hin=28, C1=8, C2=16, NC=10):
+    """The CONVNET trainer's launches (config 2) with their algorithmic work (direct-convolution FLOPs)."""
+    P1, P2 = Hin // 2, Hin // 4
+    F = C2 * P2 * P2
+    c1 = 2.0 * N * C1 * Hin * Hin * 9          # conv1: Ci = 1
+    c2 = 2.0 * N * C2 * P1 * P1 * 9 * C1       # conv2
+    return [("conv1", "flop32", c1), ("conv2", "flop32", c2), ("fc", "flop32", 2.0 * N * NC * F),
+            ("softmax_ce", "bytes", 8.0 * N * NC + 8.0 * N), ("dfb", "bytes", 4.0 * N * NC),
+            ("dP2", "flop32", 2.0 * N * F * NC), ("dfw", "flop32", 2.0 * NC * F * N),
+            ("pool2_bwd", "bytes", 4.0 * N * C2 * (P1 * P1 * 2 + P2 * P2 * 2)), ("conv2_dx", "flop32", c2),
+            ("conv2_dw", "flop32", c2), ("conv2_dw_sgd", "bytes", 0.0),
+            ("pool1_bwd", "bytes", 4.0 * N * C1 * (Hin * Hin * 2 + P1 * P1 * 2)), ("conv1_dw", "flop32", c1),
+            ("conv1_dw_sgd", "bytes", 0.0), ("tail", "bytes", 4.0 * N + 16.0 * NC)]
+
+
+def kernel_table(t, batch, kernels, steps=10):
+    """Average duration of each launch of the step (hipEvents around it, eager steps), the dominant one's
+    roofline, and the per-kernel entries."""
+    nk = t.kernel_count(batch)
+    assert nk == len(kernels), (nk, len(kernels))
+    per = []
+    for i in range(nk):
+        t.probe(i)
+        for _ in range(steps):
+            t.step(batch)
+        ms, n = t.probe_read()
+        per.append(ms / max(n, 1))
+    t.probe(-1)
+    rows = []
+    for (kname, kkind, amt), ms in zip(kernels, per):
+        e = {"name": kname, "avg_us": round(ms * 1e3, 2)}
+        if kkind.startswith("flop"):
+            tf = amt / (ms / 1e3) / 1e12 if ms > 0 else 0.0
+            e.update(tflops=round(tf, 3), frac=round(tf * 1e12 / (PEAK_F16 if kkind == "flop16" else PEAK_F32), 4))
+        elif amt > 0:
+            gbs = amt / (ms / 1e3) / 1e9 if ms > 0 else 0.0
+            e.update(gbs=round(gbs, 1), frac=round(gbs * 1e9 / PEAK_HBM, 4))
+        rows.append(e)
+    dom = int(np.argmax(per))
+    name, kk, amount = kernels[dom]
+    s = per[dom] / 1e3
+    if kk.startswith("flop"):
+        peak = PEAK_F16 if kk == "flop16" else PEAK_F32
+        roof = {"kernel": name, "bound": "mfma", "achieved": amount / s / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s"}
+    else:
+        roof = {"kernel": name, "bound": "hbm", "achieved": amount / s / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["avg_us"] = per[dom] * 1e3
+    return roof, rows
+
+
 def other_configs(dev, skip: int) -> dict:
-    """Steps/s of the other BASELINE configs at their own shapes (graph replay of the device-resident
-    step, the tensor.JIT pattern; config 4 per bound batch N). Parity for each is in tests/."""
+    """Each other BASELINE config at its own shape: steps/s (graph replay of the device-resident step,
+    the tensor.JIT pattern; config 4 per bound batch N) and the roofline of its dominant kernel with the
+    per-kernel table (eager steps, hipEvents around each launch). Parity for each is in tests/."""
     from anneal_amd import _lib as L
     from anneal_amd import data
     from anneal_amd.backend import Trainer
@@ -105,41 +199,47 @@ def other_configs(dev, skip: int) -> dict:
         dev.sync()
         return steps / (time.perf_counter() - t0)
 
+    def entry(t, batch, kernels, steps=50):
+        r = rate(t, batch, steps)
+        roof, rows = kernel_table(t, batch, kernels)
+        return {"steps_per_s": r, "roofline": roof, "kernels": rows}
+
     out = {}
     if skip != 1:
         p = data.mlp_ce_inputs(64, 784, 128, 10)
         t = Trainer(dev, L.TRAIN_MLP_CE, [64, 784, 128, 10], 0.01)
         for k in ("x", "labels", "W1", "b1", "W2", "b2"):
             t.set(k, p[k])
-        out["config1_mlp_784-128-10_b64_f32"] = {"steps_per_s": rate(t, 64)}
+        out["config1_mlp_784-128-10_b64_f32"] = entry(t, 64, mlp_ce_kernels(64, 784, 128, 10))
         t.close()
     if skip != 2:
         p = data.convnet_inputs()
         t = Trainer(dev, L.TRAIN_CONVNET, [32, 28, 8, 16, 10], 0.01)
         for k in ("x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb"):
             t.set(k, p[k])
-        out["config2_convnet_b32_f32"] = {"steps_per_s": rate(t, 32)}
+        out["config2_convnet_b32_f32"] = entry(t, 32, convnet_kernels())
         t.close()
     if skip != 4:
         p = data.mlp_ce_inputs(4096, 512, 2048, 512, x_lo=-1.0, x_hi=1.0)
         t = Trainer(dev, L.TRAIN_MLP_CE, [4096, 512, 2048, 512], 0.01)
         for k in ("x", "labels", "W1", "b1", "W2", "b2"):
             t.set(k, p[k])
-        out["config4_dynmlp_512-2048-512_f32"] = {f"N={n}_steps_per_s": rate(t, n, 100) for n in (1, 7, 256, 4096)}
+        out["config4_dynmlp_512-2048-512_f32"] = {f"N={n}": entry(t, n, mlp_ce_kernels(n, 512, 2048, 512), 100)
+                                                  for n in (1, 7, 256, 4096)}
         t.close()
     if skip != 5:
-        kind, dims, lr, batch, p, _, _ = config_workload(5)
+        kind, dims, lr, batch, p, ks, _ = config_workload(5)
         t = Trainer(dev, kind, dims, lr)
         for k, v in p.items():
             t.set(k, v)
-        out["config5_chain_8192x4096_f32"] = {"steps_per_s": rate(t, batch)}
+        out["config5_chain_8192x4096_f32"] = entry(t, batch, ks)
         t.close()
     if skip != 3:
-        kind, dims, lr, batch, p, _, _ = config_workload(3)
+        kind, dims, lr, batch, p, ks, _ = config_workload(3)
         t = Trainer(dev, kind, dims, lr)
         for k, v in p.items():
             t.set(k, v)
-        out["config3_f16_mlp_b4096"] = {"steps_per_s": rate(t, batch, 20)}
+        out["config3_f16_mlp_b4096"] = entry(t, batch, ks, 20)
         t.close()
     return out
 
@@ -234,21 +334,12 @@ def main():
     t = Trainer(dev, kind, dims, lr)
     for k, v in p.items():
         t.set(k, v)
-    nk = t.kernel_count(batch)
-    assert nk == len(kernels), (nk, len(kernels))
     for _ in range(args.warmup):
         t.step(batch)
     dev.sync()
     # Calibration (outside the timed region): each kernel's average duration over 10 steps.
-    per = []
-    for i in range(nk):
-        t.probe(i)
-        for _ in range(10):
-            t.step(batch)
-        ms, n = t.probe_read()
-        per.append(ms / max(n, 1))
-    t.probe(-1)
-    dom = int(np.argmax(per))
+    _, kinfo = kernel_table(t, batch, kernels)
+    dom = int(np.argmax([k["avg_us"] for k in kinfo]))
     # Timed region: K steps, the dominant kernel bracketed by hipEvents on the library stream.
     t.probe(dom)
     dev.sync()
@@ -271,17 +362,6 @@ def main():
     roof["traffic"] = TRAFFIC_BYTES.get((args.config, name))
     roof["kernel"] = name
     roof["avg_us"] = dom_avg_s * 1e6
-
-    kinfo = []
-    for (kname, kkind, amt), ms in zip(kernels, per):
-        e = {"name": kname, "avg_us": round(ms * 1e3, 2)}
-        if kkind.startswith("flop"):
-            tf = amt / (ms / 1e3) / 1e12 if ms > 0 else 0.0
-            e.update(tflops=round(tf, 1), frac=round(tf * 1e12 / (PEAK_F16 if kkind == "flop16" else PEAK_F32), 3))
-        elif amt > 0:
-            gbs = amt / (ms / 1e3) / 1e9 if ms > 0 else 0.0
-            e.update(gbs=round(gbs, 1), frac=round(gbs * 1e9 / PEAK_HBM, 3))
-        kinfo.append(e)
 
     sps = args.steps / elapsed
     out = {
