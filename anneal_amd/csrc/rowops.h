@@ -4,8 +4,8 @@
 
 namespace ah {
 
-constexpr int kChainStatsRows = 128;  // rows per pass-1 block (chunk partials folded per column)
-constexpr int kChainGradRows = 64;    // rows per pass-2 block
+constexpr int kChainStatsRows = 64;   // rows per pass-1 block (chunk partials folded per column)
+constexpr int kChainGradRows = 32;    // rows per pass-2 block
 constexpr int kTailCols = 32;         // step tail: elements per block pass (one per thread of a chunk)
 constexpr int kTailChunks = 16;       // step tail: row chunks of a partial-row accumulator
 

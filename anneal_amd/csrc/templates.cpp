@@ -117,7 +117,7 @@ int need(const char *key, int32_t n_ptrs, int want) {
 }
 
 // Grows the template's own device workspace (kept for the device's lifetime; never under capture when
-// the caller prepares items first, as ah_plan does).
+// the caller prepares items first, as ah_plan does). A new workspace starts zeroed.
 int ensure_ws(TemplateKernel *t, int64_t bytes) {
     if (bytes <= t->ws_bytes) return AH_OK;
     if (t->ws) AH_HIP(hipFree(t->ws));
@@ -125,6 +125,7 @@ int ensure_ws(TemplateKernel *t, int64_t bytes) {
     t->ws_bytes = 0;
     AH_HIP(hipMalloc(&t->ws, (size_t)bytes));
     t->ws_bytes = bytes;
+    AH_HIP(hipMemset(t->ws, 0, (size_t)bytes));
     return AH_OK;
 }
 

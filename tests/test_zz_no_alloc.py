@@ -36,7 +36,7 @@ def test_noalloc_matches_allocating_entry_point(dev):
 
 
 def test_noalloc_rejects_shapes_beyond_the_workspace(dev):
-    R, Cc = 65536, 4096                            # needs 512*4096*4 floats > 2^21
+    R, Cc = 65536, 4096                            # needs 1024*4096*4 floats > 2^22
     bufs = [dev.buffer(4), dev.buffer(4), dev.buffer(4), dev.buffer(4), dev.buffer(1)]
     with pytest.raises(L.AnnealHipError, match="maximum"):
         dev.chain_step_noalloc(bufs[0], bufs[1], R, Cc, bufs[2], bufs[3], bufs[4])
