@@ -59,6 +59,17 @@ class ah_gemm_desc(C.Structure):
                 ("tile", C.c_int32), ("variant", C.c_int32)]
 
 
+class ah_opt(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("axis", C.c_int32), ("arg", C.c_int32)]
+
+
+class ah_beam_result(C.Structure):
+    _fields_ = [("min_us", C.c_double), ("base_us", C.c_double), ("searched", C.c_int32), ("from_cache", C.c_int32),
+                ("n_opts", C.c_int32), ("opts", ah_opt * 8)]
+
+
+OPT_IDENTITY, OPT_LOCAL, OPT_TILE, OPT_UPCAST, OPT_VECTORIZE, OPT_GROUP, OPT_SCHEDULE = range(7)
+
 # name -> (restype, argtypes)
 _P = C.c_void_p
 SIGNATURES = {
@@ -96,6 +107,13 @@ SIGNATURES = {
                               C.c_int32, C.c_int32, C.POINTER(C.POINTER(ah_output)), C.POINTER(C.c_int32)]),
     "ah_plan_stats": (C.c_int, [_P, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
     "ah_plan_destroy": (None, [_P]),
+    "ah_apply_opts": (C.c_int, [C.c_char_p, C.POINTER(ah_opt), C.c_int32, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
+    "ah_action_space": (C.c_int, [C.c_char_p, C.POINTER(ah_opt), C.c_int32, C.POINTER(C.c_int32)]),
+    "ah_beam_search": (C.c_int, [_P, C.POINTER(ah_exec_item), C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                 C.POINTER(ah_beam_result)]),
+    "ah_beam_apply": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
+    "ah_beam_cache": (C.c_int, [C.c_char_p, C.c_int32]),
+    "ah_beam_reset": (None, []),
     "ah_gemm": (C.c_int, [_P, C.POINTER(ah_gemm_desc)]),
     "ah_translate_wgsl": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
     "ah_ckpt_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),

@@ -76,6 +76,8 @@ struct ah_graph {
 
 namespace ah {
 int template_create(const std::string &source, TemplateKernel **out);
+// "tmpl:<name>;k=v;..." -> name and the k=v map.
+std::unordered_map<std::string, std::string> template_key_params(const std::string &key, std::string *name);
 // Grows the template's workspace for the binding symval (before a graph capture).
 int template_prepare(TemplateKernel *t, int64_t symval);
 std::string wgsl_to_hip(const std::string &src, std::string *err);

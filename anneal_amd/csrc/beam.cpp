@@ -1,0 +1,465 @@
+// beam.cpp — the Opt seam remapped onto the HIP templates' parameters, and BEAM retargeted to time HIP
+// candidates.
+//
+// The reference rewrites a kernel's AST with Opt{Kind, Axis, Arg} transforms (codegen/opt.go:29-72,
+// 559-567) and searches Opt sequences by timing the rendered WGSL (codegen/beam.go:41-541). On MI355X the
+// hot kernels are hand-written templates, so an Opt here edits a template's tuning parameters instead:
+//   LOCAL(axis 0|1, L in {8,16,32})   waves of the workgroup along M (axis 0) or N (axis 1): L/8, the
+//                                     tile unchanged (each wave's register tile adjusts)
+//   UPCAST(axis 0|1, f in {2,4})      MFMA register tile per wave along M or N: f blocks of 32, the waves
+//                                     unchanged (the tile grows or shrinks); f32 kernel: tile 64*f
+//   TILE(axis 2, TS in {8,16,32})     the reduce-axis tile staged through LDS: k per stage and stages in
+//                                     flight, (32, 4), (64, 2), (64, 3)
+//   VECTORIZE(axis 2, 4)              16-byte LDS-DMA staging issued from asm with the cross-barrier
+//                                     fragment prefetch (fetch mode 4)
+//   GROUP(axis 2, g in {2,4})         k-groups: g wave sets split K and reduce through LDS
+//   SCHEDULE(axis 0, m in {5,6,7})    where the DMAs and fragment reads sit between the MFMAs (fetch mode m)
+// Without VECTORIZE or SCHEDULE the fetch scheduling is left to the kernel (any of the compiler-scheduled
+// modes 0-3). A sequence is valid when the resulting parameter set is one the library instantiates (for
+// f16, a row of the variant table; the lowest-numbered match is used), and an Opt belongs to a kernel's
+// action space when it changes that kernel's parameters into another instantiated set, as ActionSpace
+// keeps only transforms that change the AST (beam.go:53-72).
+// BEAM keeps the reference's search: beam width W, depth D, candidates timed with Benchmark (min of N),
+// a value-identity guard that drops any candidate whose output is not bit-identical to the unmodified
+// kernel's on fixed inputs (beam.go:410-451), and a cache keyed by the kernel (here the FNV-64a hash of
+// its template key, epilogue and shape included) holding the winning Opts and the hash of the
+// specialised key (beam.go:100-215).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+
+#include "ah_internal.h"
+#include "gemm.h"
+
+namespace ah {
+namespace {
+
+uint64_t fnv64(const std::string &s) {
+    uint64_t h = 14695981039346656037ull;
+    for (unsigned char c : s) h = (h ^ c) * 1099511628211ull;
+    return h;
+}
+
+// Tuning parameters of a gemm key.
+struct Knobs {
+    bool f16 = true;
+    G16Params p{};   // f16
+    int tile = 0;    // f32 (0 = by shape)
+    int kg = 0;      // f32 (0 = by shape)
+    bool operator==(const Knobs &o) const {
+        return f16 == o.f16 && tile == o.tile && kg == o.kg &&
+               (!f16 || memcmp(&p, &o.p, sizeof p) == 0);
+    }
+};
+
+struct KeyInfo {
+    std::string name;
+    std::unordered_map<std::string, std::string> kv;
+    Knobs knobs;
+};
+
+long geti(const std::unordered_map<std::string, std::string> &kv, const char *k, long d) {
+    auto it = kv.find(k);
+    return it == kv.end() ? d : strtol(it->second.c_str(), nullptr, 10);
+}
+
+// The lowest-numbered variant with these parameters; fetch 0 means "compiler-scheduled" (modes 0-3, any
+// cross-barrier setting), 4-7 an asm-issued mode with the cross-barrier prefetch.
+int f16_variant_of(const G16Params &p) {
+    for (int v = 1; v <= kGemm16Variants; v++) {
+        G16Params q;
+        if (!gemm16_variant_params(v, &q)) continue;
+        if (q.bm != p.bm || q.bn != p.bn || q.wvm != p.wvm || q.wvn != p.wvn || q.bk != p.bk || q.ns != p.ns || q.kg != p.kg)
+            continue;
+        if (p.fetch == 0 ? q.fetch <= 3 : (q.fetch == p.fetch && q.xb == 1)) return v;
+    }
+    return 0;
+}
+
+// Parses a gemm key and its current parameters (variant 0: the variant the shape selects by default).
+int key_info(const std::string &key, KeyInfo *ki) {
+    if (key.compare(0, 5, "tmpl:") != 0) return set_error(AH_ERR_UNSUPPORTED, "opts: not a template key");
+    ki->kv = template_key_params(key, &ki->name);
+    if (ki->name != "gemm") return AH_OK;   // no tunable parameters: empty action space
+    auto dt = ki->kv.find("dtype");
+    ki->knobs.f16 = dt != ki->kv.end() && dt->second == "f16";
+    if (ki->knobs.f16) {
+        int v = (int)geti(ki->kv, "variant", 0);
+        if (v == 0) {
+            GemmDesc d;
+            memset(&d, 0, sizeof d);
+            auto dim = [&](const char *k) { auto it = ki->kv.find(k); return it == ki->kv.end() || it->second == "sym" ? 4096 : atoi(it->second.c_str()); };
+            d.M = dim("M"); d.N = dim("N");
+            v = gemm16_default_variant(d);
+        }
+        if (!gemm16_variant_params(v, &ki->knobs.p)) return set_error(AH_ERR_INVALID, "opts: variant %d", v);
+        G16Params &p = ki->knobs.p;
+        if (p.fetch <= 3) p.fetch = 0;   // compiler-scheduled class
+        p.xb = p.fetch ? 1 : 0;
+    } else {
+        ki->knobs.tile = (int)geti(ki->kv, "tile", 0);
+        ki->knobs.kg = (int)geti(ki->kv, "kg", 0);
+    }
+    return AH_OK;
+}
+
+// Applies one Opt to the parameters; false if the Opt does not apply to this kernel.
+bool apply_opt(Knobs &k, const ah_opt &o) {
+    if (o.kind == AH_OPT_IDENTITY) return true;
+    if (k.f16) {
+        G16Params &p = k.p;
+        switch (o.kind) {
+        case AH_OPT_LOCAL: {   // waves along the axis; the tile stays, each wave's register tile adjusts
+            if ((o.axis != 0 && o.axis != 1) || (o.arg != 8 && o.arg != 16 && o.arg != 32)) return false;
+            const int w = o.arg / 8;
+            const int span = o.axis == 0 ? p.bm : p.bn;
+            if (span % (32 * w)) return false;
+            if (o.axis == 0) p.wvm = w;
+            else p.wvn = w;
+            return true;
+        }
+        case AH_OPT_UPCAST:    // register tile per wave along the axis; the waves stay, the tile follows
+            if ((o.axis != 0 && o.axis != 1) || (o.arg != 2 && o.arg != 4)) return false;
+            if (o.axis == 0) p.bm = 32 * p.wvm * o.arg;
+            else p.bn = 32 * p.wvn * o.arg;
+            return true;
+        case AH_OPT_TILE:
+            if (o.axis != 2) return false;
+            if (o.arg == 8) { p.bk = 32; p.ns = 4; }
+            else if (o.arg == 16) { p.bk = 64; p.ns = 2; }
+            else if (o.arg == 32) { p.bk = 64; p.ns = 3; }
+            else return false;
+            return true;
+        case AH_OPT_VECTORIZE:
+            if (o.axis != 2 || o.arg != 4) return false;
+            p.fetch = 4; p.xb = 1;
+            return true;
+        case AH_OPT_GROUP:
+            if (o.axis != 2 || o.arg != 2) return false;
+            p.kg = 2;
+            return true;
+        case AH_OPT_SCHEDULE:
+            if (o.axis != 0 || o.arg < 5 || o.arg > 7) return false;
+            p.fetch = o.arg; p.xb = 1;
+            return true;
+        default: return false;
+        }
+    }
+    switch (o.kind) {
+    case AH_OPT_UPCAST:
+        if ((o.axis != 0 && o.axis != 1) || (o.arg != 2 && o.arg != 4)) return false;
+        k.tile = 64 * o.arg;
+        if (k.kg && !gemm32_kgroups_ok(k.tile, k.kg)) k.kg = 1;
+        return true;
+    case AH_OPT_GROUP:
+        if (o.axis != 2 || (o.arg != 2 && o.arg != 4)) return false;
+        if (!k.tile) k.tile = 64;
+        k.kg = o.arg;
+        return gemm32_kgroups_ok(k.tile, k.kg);
+    default: return false;
+    }
+}
+
+bool instantiated(const Knobs &k) {
+    if (k.f16) return f16_variant_of(k.p) != 0;
+    return k.tile == 0 || (k.tile == 64 || k.tile == 128 || k.tile == 256);
+}
+
+// The key with its tuning parameters replaced by k.
+std::string emit_key(const KeyInfo &ki, const Knobs &k) {
+    std::map<std::string, std::string> kv(ki.kv.begin(), ki.kv.end());
+    if (k.f16) {
+        kv["variant"] = std::to_string(f16_variant_of(k.p));
+    } else {
+        kv.erase("tile");
+        kv.erase("kg");
+        if (k.tile) kv["tile"] = std::to_string(k.tile);
+        if (k.kg) kv["kg"] = std::to_string(k.kg);
+    }
+    std::string out = "tmpl:" + ki.name;
+    for (auto &e : kv) out += ";" + e.first + "=" + e.second;
+    return out;
+}
+
+// Every Opt the search may try (the reference's argument lists, beam.go:41-47, plus GROUP and SCHEDULE).
+std::vector<ah_opt> all_opts() {
+    std::vector<ah_opt> v;
+    for (int axis = 0; axis < 4; axis++) {
+        for (int a : {8, 16, 32}) v.push_back({AH_OPT_LOCAL, axis, a});
+        for (int a : {8, 16, 32}) v.push_back({AH_OPT_TILE, axis, a});
+        for (int a : {2, 4}) v.push_back({AH_OPT_UPCAST, axis, a});
+        v.push_back({AH_OPT_VECTORIZE, axis, 4});
+        for (int a : {2, 4}) v.push_back({AH_OPT_GROUP, axis, a});
+        for (int a : {5, 6, 7}) v.push_back({AH_OPT_SCHEDULE, axis, a});
+    }
+    return v;
+}
+
+std::vector<ah_opt> action_space(const KeyInfo &ki, const Knobs &from) {
+    std::vector<ah_opt> out;
+    if (ki.name != "gemm") return out;
+    for (const ah_opt &o : all_opts()) {
+        Knobs k = from;
+        if (apply_opt(k, o) && !(k == from) && instantiated(k)) out.push_back(o);
+    }
+    return out;
+}
+
+int apply_opts_key(const std::string &key, const ah_opt *opts, int n, std::string *out) {
+    KeyInfo ki;
+    if (int rc = key_info(key, &ki)) return rc;
+    if (n > 0 && ki.name != "gemm") return set_error(AH_ERR_UNSUPPORTED, "opts: template %s has no tuning parameters", ki.name.c_str());
+    Knobs k = ki.knobs;
+    for (int i = 0; i < n; i++) {
+        if (!apply_opt(k, opts[i]))
+            return set_error(AH_ERR_UNSUPPORTED, "opts: opt %d (kind %d axis %d arg %d) does not apply", i, opts[i].kind,
+                             opts[i].axis, opts[i].arg);
+    }
+    if (!instantiated(k)) return set_error(AH_ERR_UNSUPPORTED, "opts: the resulting parameters are not an instantiated kernel");
+    *out = n > 0 ? emit_key(ki, k) : key;
+    return AH_OK;
+}
+
+// ── BEAM ─────────────────────────────────────────────────────────────────────
+
+struct CacheEntry {
+    std::vector<ah_opt> opts;
+    uint64_t src_hash = 0;   // FNV-64a of the specialised key
+};
+std::mutex g_cache_mu;
+std::map<uint64_t, CacheEntry> g_cache;   // kernel key hash -> winner (process-wide, like beamCacheMap)
+
+// Deterministic inputs, varying by buffer index (beam.go:410-421).
+std::vector<std::vector<float>> test_inputs(const ah_exec_item &it) {
+    std::vector<std::vector<float>> in;
+    for (int b = 1; b < it.n_bufs; b++) {
+        std::vector<float> v((size_t)std::max<int64_t>(it.bufs[b].size, 0));
+        for (size_t j = 0; j < v.size(); j++) v[j] = (float)((j + (size_t)(b - 1) * 17) % 13 + 1) * 0.01f;
+        in.push_back(std::move(v));
+    }
+    return in;
+}
+
+int run_single(ah_device *d, ah_exec_item it, const char *key, const std::vector<std::vector<float>> &in,
+               std::vector<float> *out) {
+    it.source = key;
+    std::vector<ah_input> ins;
+    for (int b = 1; b < it.n_bufs; b++) ins.push_back({it.bufs[b].uop_idx, in[b - 1].data(), (int64_t)in[b - 1].size()});
+    ah_output *outs = nullptr;
+    int32_t n = 0;
+    int rc = ah_run(d, &it, 1, ins.data(), (int32_t)ins.size(), &outs, &n);
+    if (rc) return rc;
+    out->clear();
+    for (int i = 0; i < n; i++)
+        if (outs[i].uop_idx == it.bufs[0].uop_idx) out->assign(outs[i].data, outs[i].data + outs[i].n);
+    ah_outputs_free(outs, n);
+    return AH_OK;
+}
+
+bool same_bits(const std::vector<float> &a, const std::vector<float> &b) {
+    return a.size() == b.size() && (a.empty() || memcmp(a.data(), b.data(), a.size() * 4) == 0);
+}
+
+struct Cand {
+    std::vector<ah_opt> opts;
+    Knobs knobs;
+    double us;
+};
+
+bool cand_less(const Cand &x, const Cand &y) {   // time, then shorter, then lexicographic (beam.go:364-384)
+    if (fabs(x.us - y.us) > 0.1) return x.us < y.us;
+    if (x.opts.size() != y.opts.size()) return x.opts.size() < y.opts.size();
+    for (size_t i = 0; i < x.opts.size(); i++) {
+        if (x.opts[i].kind != y.opts[i].kind) return x.opts[i].kind < y.opts[i].kind;
+        if (x.opts[i].axis != y.opts[i].axis) return x.opts[i].axis < y.opts[i].axis;
+        if (x.opts[i].arg != y.opts[i].arg) return x.opts[i].arg < y.opts[i].arg;
+    }
+    return false;
+}
+
+}  // namespace
+}  // namespace ah
+
+using namespace ah;
+
+extern "C" {
+
+int ah_apply_opts(const char *key, const ah_opt *opts, int32_t n, char *out, int64_t cap, int64_t *needed) {
+    if (!key || (n > 0 && !opts) || n < 0) return set_error(AH_ERR_INVALID, "ah_apply_opts: bad argument");
+    std::string s;
+    if (int rc = apply_opts_key(key, opts, n, &s)) return rc;
+    if (needed) *needed = (int64_t)s.size() + 1;
+    if (out && cap > 0) {
+        const size_t k = std::min<size_t>(s.size(), (size_t)cap - 1);
+        memcpy(out, s.data(), k);
+        out[k] = 0;
+    }
+    return AH_OK;
+}
+
+int ah_action_space(const char *key, ah_opt *out, int32_t cap, int32_t *n) {
+    if (!key || !n) return set_error(AH_ERR_INVALID, "ah_action_space: bad argument");
+    KeyInfo ki;
+    if (int rc = key_info(key, &ki)) return rc;
+    std::vector<ah_opt> acts = action_space(ki, ki.knobs);
+    *n = (int32_t)acts.size();
+    for (int i = 0; i < (int)acts.size() && i < cap && out; i++) out[i] = acts[i];
+    return AH_OK;
+}
+
+int ah_beam_search(ah_device *d, const ah_exec_item *item, int32_t width, int32_t depth, int32_t warmup,
+                   int32_t iters, ah_beam_result *res) {
+    if (!d || !item || !item->source || !res || width < 1 || depth < 0 || iters < 1 || item->n_bufs < 1)
+        return set_error(AH_ERR_INVALID, "ah_beam_search: bad argument");
+    memset(res, 0, sizeof *res);
+    const std::string key = item->source;
+    const uint64_t sk = fnv64(key);
+    KeyInfo ki;
+    if (int rc = key_info(key, &ki)) return rc;
+    ah_bench_result br;
+    auto bench = [&](const std::string &k, double *us) -> int {
+        ah_exec_item it = *item;
+        it.source = k.c_str();
+        int rc = ah_benchmark(d, &it, warmup, iters, &br);
+        if (rc == AH_OK) *us = br.min_us;
+        return rc;
+    };
+    double base_us = 0;
+    if (int rc = bench(key, &base_us)) return rc;
+    res->base_us = base_us;
+    {   // cache hit: the stored winner, re-timed (beam.go:287-309)
+        std::lock_guard<std::mutex> g(g_cache_mu);
+        auto it = g_cache.find(sk);
+        if (it != g_cache.end()) {
+            res->from_cache = 1;
+            res->n_opts = (int32_t)std::min<size_t>(it->second.opts.size(), 8);
+            for (int i = 0; i < res->n_opts; i++) res->opts[i] = it->second.opts[i];
+        }
+    }
+    if (res->from_cache) {
+        std::string k;
+        if (int rc = apply_opts_key(key, res->opts, res->n_opts, &k)) return rc;
+        double us = base_us;
+        if (res->n_opts && bench(k, &us) != AH_OK) us = base_us;
+        res->min_us = us;
+        return AH_OK;
+    }
+    const std::vector<std::vector<float>> in = test_inputs(*item);
+    std::vector<float> ref;
+    if (int rc = run_single(d, *item, key.c_str(), in, &ref)) return rc;
+    Cand best{{}, ki.knobs, base_us};
+    std::vector<Cand> cur{best};
+    for (int dep = 0; dep < depth; dep++) {
+        std::vector<Cand> next;
+        for (const Cand &c : cur) {
+            for (const ah_opt &a : action_space(ki, c.knobs)) {
+                Cand n = c;
+                apply_opt(n.knobs, a);
+                n.opts.push_back(a);
+                const std::string k = emit_key(ki, n.knobs);
+                std::vector<float> got;
+                if (run_single(d, *item, k.c_str(), in, &got) != AH_OK || !same_bits(got, ref)) continue;   // value guard
+                if (bench(k, &n.us) != AH_OK) continue;
+                res->searched++;
+                next.push_back(n);
+            }
+        }
+        std::stable_sort(next.begin(), next.end(), cand_less);
+        if ((int)next.size() > width) next.resize(width);
+        if (next.empty() || next[0].us >= best.us) break;
+        best = next[0];
+        cur = next;
+    }
+    res->min_us = best.us;
+    res->n_opts = (int32_t)std::min<size_t>(best.opts.size(), 8);
+    for (int i = 0; i < res->n_opts; i++) res->opts[i] = best.opts[i];
+    std::lock_guard<std::mutex> g(g_cache_mu);
+    g_cache[sk] = CacheEntry{best.opts, fnv64(best.opts.empty() ? key : emit_key(ki, best.knobs))};
+    return AH_OK;
+}
+
+int ah_beam_apply(const char *key, char *out, int64_t cap, int64_t *needed) {
+    if (!key) return set_error(AH_ERR_INVALID, "ah_beam_apply: null key");
+    std::vector<ah_opt> opts;
+    uint64_t h = 0;
+    {
+        std::lock_guard<std::mutex> g(g_cache_mu);
+        auto it = g_cache.find(fnv64(key));
+        if (it != g_cache.end()) {
+            opts = it->second.opts;
+            h = it->second.src_hash;
+        }
+    }
+    std::string s = key;
+    if (!opts.empty()) {
+        std::string k;
+        // the stored hash guards against two kernels sharing a key hash (beam.go:516-526)
+        if (apply_opts_key(key, opts.data(), (int)opts.size(), &k) == AH_OK && fnv64(k) == h) s = k;
+    }
+    if (needed) *needed = (int64_t)s.size() + 1;
+    if (out && cap > 0) {
+        const size_t k = std::min<size_t>(s.size(), (size_t)cap - 1);
+        memcpy(out, s.data(), k);
+        out[k] = 0;
+    }
+    return AH_OK;
+}
+
+// Disk cache (beam.go:100-150): one line per kernel, "<key hash> <specialised key hash> <n> k,a,g ...",
+// under a format line. Loading merges into the process cache; saving writes every entry.
+int ah_beam_cache(const char *path, int32_t save) {
+    if (!path) return set_error(AH_ERR_INVALID, "ah_beam_cache: null path");
+    std::lock_guard<std::mutex> g(g_cache_mu);
+    if (save) {
+        FILE *f = fopen(path, "w");
+        if (!f) return set_error(AH_ERR_INVALID, "beam cache: cannot write %s", path);
+        fprintf(f, "# anneal_hip beam cache v1\n");
+        for (auto &e : g_cache) {
+            fprintf(f, "%016llx %016llx %zu", (unsigned long long)e.first, (unsigned long long)e.second.src_hash,
+                    e.second.opts.size());
+            for (auto &o : e.second.opts) fprintf(f, " %d,%d,%d", o.kind, o.axis, o.arg);
+            fprintf(f, "\n");
+        }
+        if (fclose(f) != 0) return set_error(AH_ERR_INVALID, "beam cache: write to %s failed", path);
+        return AH_OK;
+    }
+    FILE *f = fopen(path, "r");
+    if (!f) return set_error(AH_ERR_INVALID, "beam cache: cannot read %s", path);
+    char line[1024];
+    int lineno = 0, rc = AH_OK;
+    std::map<uint64_t, CacheEntry> got;
+    while (fgets(line, sizeof line, f)) {
+        lineno++;
+        if (line[0] == '#' || line[0] == '\n') continue;
+        unsigned long long sk = 0, h = 0;
+        int n = 0, off = 0;
+        if (sscanf(line, "%llx %llx %d%n", &sk, &h, &n, &off) != 3 || n < 0 || n > 8) { rc = set_error(AH_ERR_INVALID, "beam cache %s: bad line %d", path, lineno); break; }
+        CacheEntry e;
+        e.src_hash = h;
+        const char *p = line + off;
+        for (int i = 0; i < n && rc == AH_OK; i++) {
+            ah_opt o;
+            int used = 0;
+            if (sscanf(p, " %d,%d,%d%n", &o.kind, &o.axis, &o.arg, &used) != 3) rc = set_error(AH_ERR_INVALID, "beam cache %s: bad opt on line %d", path, lineno);
+            p += used;
+            e.opts.push_back(o);
+        }
+        if (rc) break;
+        got[sk] = e;
+    }
+    fclose(f);
+    if (rc == AH_OK)
+        for (auto &e : got) g_cache[e.first] = e.second;
+    return rc;
+}
+
+void ah_beam_reset(void) {
+    std::lock_guard<std::mutex> g(g_cache_mu);
+    g_cache.clear();
+}
+
+}  // extern "C"

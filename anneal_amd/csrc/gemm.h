@@ -47,6 +47,7 @@ struct GemmDesc {
     float *lossacc;   // EPI_MSE scalar accumulator
     int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
     int variant;      // f16 kernel variant (0 = auto; table Var<V> in gemm16_kernel.h), the tuning hook
+    int kgroups;      // f32 tiled kernel: wave sets splitting K (0 = auto, else 1 / 2 / 4 as the tile admits)
     // Deterministic partial sums instead of atomics (0 = atomic accumulation into colsum[N] / lossacc[0]):
     // with colsum_ld > 0 each wave stores the column sums of its rows, which start at a multiple of 32,
     // to colsum[(row / 32) * colsum_ld + n]; with loss_ld > 0 each wave stores its MSE partial to
@@ -62,5 +63,18 @@ struct GemmDesc {
 
 hipError_t gemm_launch(const GemmDesc &d, hipStream_t s);
 bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err);
+
+// Template parameters of an f16 variant (table Var<V> in gemm16_kernel.h): tile BM x BN, wave layout
+// WVM x WVN, k per LDS stage BK, stages in flight NS, fetch mode, cross-barrier prefetch XB, k-groups KG.
+struct G16Params {
+    int bm, bn, wvm, wvn, bk, ns, fetch, xb, kg;
+};
+bool gemm16_variant_params(int variant, G16Params *out);
+// The variant an f16 contraction with variant 0 and no tuned choice runs (chosen by shape).
+int gemm16_default_variant(const GemmDesc &d);
+// k-groups an f32 tile size admits (LDS budget): 64 -> 1, 2, 4; 128 -> 1, 2; 256 -> 1.
+inline bool gemm32_kgroups_ok(int tile, int kg) {
+    return kg == 1 || (kg == 2 && tile <= 128) || (kg == 4 && tile == 64);
+}
 
 }  // namespace ah

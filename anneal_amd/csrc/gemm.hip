@@ -309,7 +309,9 @@ static hipError_t launch_t(const GemmDesc &d, hipStream_t s) {
     // are at most 4 workgroups' worth per CU and every group keeps at least 8 chunks
     // (LDS: 64-tile 4 groups 128 KiB, 128-tile 2 groups 128 KiB).
     int kg = 1;
-    if (BM <= 128) {
+    if (d.kgroups > 0 && gemm32_kgroups_ok(BM, d.kgroups)) {
+        kg = d.kgroups;   // fixed by the caller (a BEAM candidate)
+    } else if (BM <= 128) {
         const int maxkg = BM == 64 ? 4 : 2;
         while (kg < maxkg && tiles * kg <= 1024 && nk >= 16 * kg) kg *= 2;
     }

@@ -40,6 +40,32 @@ int variant_kgroups(int v) {
 }
 }  // namespace
 
+bool gemm16_variant_params(int v, G16Params *out) {
+    switch (v) {
+#define AH_G16_P(n)                                                                                          \
+    case n:                                                                                                  \
+        *out = {g16::Var<n>::BM, g16::Var<n>::BM, g16::Var<n>::WVM, g16::Var<n>::WVN, g16::Var<n>::BK,     \
+                g16::Var<n>::NS, g16::Var<n>::FETCH, g16::Var<n>::XB ? 1 : 0, g16::Var<n>::KG};            \
+        return true;
+        AH_G16_P(1) AH_G16_P(2) AH_G16_P(3) AH_G16_P(4) AH_G16_P(5) AH_G16_P(6) AH_G16_P(7)
+        AH_G16_P(8) AH_G16_P(9) AH_G16_P(10) AH_G16_P(11) AH_G16_P(12) AH_G16_P(13)
+        AH_G16_P(14) AH_G16_P(15) AH_G16_P(16) AH_G16_P(17) AH_G16_P(18) AH_G16_P(19)
+        AH_G16_P(20) AH_G16_P(21) AH_G16_P(22) AH_G16_P(23) AH_G16_P(24) AH_G16_P(25)
+        AH_G16_P(26) AH_G16_P(27) AH_G16_P(28) AH_G16_P(29) AH_G16_P(30) AH_G16_P(31)
+#undef AH_G16_P
+        default: return false;
+    }
+}
+
+int gemm16_default_variant(const GemmDesc &d) {
+    int tile = d.tile;
+    if (tile == 0) {
+        long t256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
+        tile = t256 >= 224 ? 256 : 128;
+    }
+    return tile == 256 ? 3 : 1;
+}
+
 // Returns true (and launches) when the shape/alignment admits the direct-to-LDS f16 kernel.
 bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
     using namespace g16;
@@ -47,14 +73,7 @@ bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
     if (d.tile != 0 && d.tile != 128 && d.tile != 256) return false;
     if (d.variant < 0 || d.variant > kMaxVariant) return false;
     int v = d.variant;
-    if (v == 0) {   // by shape: 256x256 tiles when they fill the chip, else 128x128
-        int tile = d.tile;
-        if (tile == 0) {
-            long t256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
-            tile = t256 >= 224 ? 256 : 128;
-        }
-        v = tile == 256 ? 3 : 1;
-    }
+    if (v == 0) v = gemm16_default_variant(d);   // by shape: 256x256 tiles when they fill the chip, else 128x128
     if (d.K % (64 * variant_kgroups(v))) return false;   // k-groups contract whole stages
     bool ok = (d.ta ? operand_ok<1>(d.A, d.lda, d.M) : operand_ok<0>(d.A, d.lda, d.M)) &&
               (d.tb ? operand_ok<1>(d.B, d.ldb, d.N) : operand_ok<0>(d.B, d.ldb, d.N));

@@ -39,11 +39,8 @@
 
 namespace ah {
 
-namespace {
-
-constexpr int kEpiGrad = 100;   // key-only epilogue: SGD on a zeroed array (see template_gemm)
-
-std::unordered_map<std::string, std::string> parse_params(const std::string &s, std::string *name) {
+// "tmpl:<name>;k=v;..." -> name and the k=v map.
+std::unordered_map<std::string, std::string> template_key_params(const std::string &s, std::string *name) {
     std::unordered_map<std::string, std::string> out;
     size_t p = s.find(';');
     *name = s.substr(5, p == std::string::npos ? std::string::npos : p - 5);
@@ -56,6 +53,11 @@ std::unordered_map<std::string, std::string> parse_params(const std::string &s, 
     }
     return out;
 }
+
+namespace {
+
+constexpr int kEpiGrad = 100;   // key-only epilogue: SGD on a zeroed array (see template_gemm)
+
 
 // Parsed parameters of one key; integers may be "sym" (resolved per launch).
 struct Params {
@@ -130,7 +132,8 @@ int ensure_ws(TemplateKernel *t, int64_t bytes) {
 }
 
 // ── gemm ─────────────────────────────────────────────────────────────────────────────────────────
-// "tmpl:gemm;dtype=f16|f32;epi=...;ta=0|1;tb=0|1;M=..;N=..;K=..[;scale=s][;lr=l][;variant=v]"
+// "tmpl:gemm;dtype=f16|f32;epi=...;ta=0|1;tb=0|1;M=..;N=..;K=..[;scale=s][;lr=l][;variant=v][;tile=t;kg=g]"
+// variant picks an f16 kernel variant, tile (64/128/256) and kg (k-groups) the f32 tiled kernel's shape.
 // M, N and K may be symbolic. PARAMs by epilogue:
 //   store      C, A, B                     C = scale*acc
 //   bias       C, A, B, bias               C = acc + bias[n]
@@ -167,6 +170,12 @@ int template_gemm(const Params &P, TemplateKernel *t) {
     base.lr = P.real("lr", 0.0f);
     base.variant = (int)P.integer("variant", 0);
     if (base.variant < 0 || base.variant > kGemm16Variants) return set_error(AH_ERR_INVALID, "tmpl gemm: variant %d", base.variant);
+    base.tile = (int)P.integer("tile", 0);
+    base.kgroups = (int)P.integer("kg", 0);
+    if (base.tile != 0 && base.tile != 64 && base.tile != 128 && base.tile != 256)
+        return set_error(AH_ERR_INVALID, "tmpl gemm: tile %d", base.tile);
+    if (base.kgroups != 0 && !(base.tile != 0 && gemm32_kgroups_ok(base.tile, base.kgroups)))
+        return set_error(AH_ERR_INVALID, "tmpl gemm: kg=%d needs a tile that admits it", base.kgroups);
     const int nbuf = (base.epi == EPI_STORE || grad) ? 3 : base.epi == EPI_MSE ? 6 : 4;
     if (base.epi == EPI_MSE) t->side = {{5, true}};
     const std::string key = t->key;
@@ -429,7 +438,7 @@ int template_prepare(TemplateKernel *t, int64_t symval) {
 
 int template_create(const std::string &source, TemplateKernel **out) {
     Params P;
-    P.kv = parse_params(source, &P.name);
+    P.kv = template_key_params(source, &P.name);
     auto *t = new TemplateKernel();
     t->key = source;
     t->name = P.name;

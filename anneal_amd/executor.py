@@ -116,6 +116,61 @@ class Executor:
         return BenchmarkResult(r.min_us, r.median_us, r.max_us, r.mean_us, r.stddev_us, r.cv)
 
 
+@dataclass
+class BeamResult:
+    opts: list          # [(kind, axis, arg), ...]; empty: the unmodified kernel won
+    min_us: float
+    base_us: float
+    searched: int
+    from_cache: bool
+
+
+def _key_out(fn, *args) -> str:
+    need = C.c_int64()
+    L.check(fn(*args, None, 0, C.byref(need)))
+    buf = C.create_string_buffer(need.value)
+    L.check(fn(*args, buf, need.value, C.byref(need)))
+    return buf.value.decode()
+
+
+def apply_opts(key: str, opts) -> str:
+    """codegen.ApplyOpts on a template key: the key with the Opt sequence applied to its parameters."""
+    arr = (L.ah_opt * max(len(opts), 1))(*[L.ah_opt(*o) for o in opts])
+    return _key_out(L.load().ah_apply_opts, key.encode(), arr, len(opts))
+
+
+def action_space(key: str) -> list:
+    """codegen.ActionSpace: every single Opt (kind, axis, arg) that changes the key's kernel."""
+    lib = L.load()
+    n = C.c_int32()
+    L.check(lib.ah_action_space(key.encode(), None, 0, C.byref(n)))
+    arr = (L.ah_opt * max(n.value, 1))()
+    L.check(lib.ah_action_space(key.encode(), arr, n.value, C.byref(n)))
+    return [(o.kind, o.axis, o.arg) for o in arr[:n.value]]
+
+
+def beam_apply(key: str) -> str:
+    """The cached BEAM winner's key for key (or key itself on a miss)."""
+    return _key_out(L.load().ah_beam_apply, key.encode())
+
+
+def beam_cache(path: str, save: bool) -> None:
+    L.check(L.load().ah_beam_cache(str(path).encode(), 1 if save else 0))
+
+
+def beam_reset() -> None:
+    L.load().ah_beam_reset()
+
+
+def beam_search(device, item, width: int = 4, depth: int = 4, warmup: int = 2, iters: int = 5) -> BeamResult:
+    """codegen.BeamSearch over the template parameters of a "tmpl:" item (cached per process)."""
+    m = _Marshal([item])
+    r = L.ah_beam_result()
+    L.check(device.lib.ah_beam_search(device.h, m.arr, width, depth, warmup, iters, C.byref(r)))
+    return BeamResult([(o.kind, o.axis, o.arg) for o in r.opts[:r.n_opts]], r.min_us, r.base_us, r.searched,
+                      bool(r.from_cache))
+
+
 class Plan:
     """An item list kept alive on the device: kernels resolved and buffers allocated once, and with
     graph=True each binding's kernel sequence captured once as a HIP graph and replayed afterwards.

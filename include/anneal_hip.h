@@ -210,6 +210,46 @@ int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int3
  * the file named by the environment variable AH_GEMM_TUNE_CACHE around its tuning. */
 int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save);
 
+/* ── The Opt seam and BEAM over the HIP templates ─────────────────────────────
+ * Replaces codegen/opt.go's ApplyOpt/ApplyOpts (:29-72, :559-567) and codegen/beam.go's ActionSpace,
+ * BeamSearch, BeamApplyToItems and disk cache (:41-541). An Opt {kind, axis, arg} (opt.go:41-46) edits a
+ * template key's tuning parameters instead of an AST: LOCAL(axis 0|1, 8|16|32) the waves along M or N
+ * (arg/8), UPCAST(axis 0|1, 2|4) the MFMA register tile per wave (f32 kernel: tile 64*arg), TILE(axis 2,
+ * 8|16|32) the LDS stage (k 32 x 4 stages, 64 x 2, 64 x 3), VECTORIZE(axis 2, 4) 16-byte asm LDS-DMA
+ * staging; GROUP(axis 2, 2|4) k-groups and SCHEDULE(axis 0, 5..7) the DMA/fragment-read interleave are
+ * MI355X additions. Only "tmpl:gemm" keys have tunable parameters. */
+enum { AH_OPT_IDENTITY = 0, AH_OPT_LOCAL = 1, AH_OPT_TILE = 2, AH_OPT_UPCAST = 3, AH_OPT_VECTORIZE = 4,
+       AH_OPT_GROUP = 5, AH_OPT_SCHEDULE = 6 };
+typedef struct {
+    int32_t kind, axis, arg;
+} ah_opt;
+/* ApplyOpts: the key with the sequence applied (NUL-terminated, at most cap bytes; *needed = full size);
+ * AH_ERR_UNSUPPORTED if an Opt does not apply or the result is not an instantiated kernel. */
+int ah_apply_opts(const char *key, const ah_opt *opts, int32_t n, char *out, int64_t cap, int64_t *needed);
+/* ActionSpace (beam.go:53-72): every single Opt that changes the key's kernel; *n = count, at most cap
+ * written to out. */
+int ah_action_space(const char *key, ah_opt *out, int32_t cap, int32_t *n);
+typedef struct {
+    double min_us, base_us;   /* winner's and the unmodified kernel's min-of-N times */
+    int32_t searched;         /* candidates benchmarked */
+    int32_t from_cache;
+    int32_t n_opts;
+    ah_opt opts[8];           /* the winning sequence (empty: identity) */
+} ah_beam_result;
+/* BeamSearch (beam.go:271-408) over item (a "tmpl:" item, buffers as for ah_benchmark): beam width and
+ * depth, each candidate timed by ah_benchmark (warmup, iters; min), kept only if its output is
+ * bit-identical to the unmodified kernel's on fixed inputs (beam.go:410-451). The winner is cached per
+ * process keyed by the FNV-64a hash of the item's key; a cached kernel is re-timed, not searched. */
+int ah_beam_search(ah_device *dev, const ah_exec_item *item, int32_t width, int32_t depth, int32_t warmup,
+                   int32_t iters, ah_beam_result *out);
+/* BeamApplyToItems' cache hit (beam.go:470-541): the cached specialised key for key, or key itself; the
+ * stored hash of the specialised key guards against key-hash collisions. */
+int ah_beam_apply(const char *key, char *out, int64_t cap, int64_t *needed);
+/* The persistent cache (beam.go:100-150): save (save != 0) every cached winner to path, or merge path
+ * into the process cache. */
+int ah_beam_cache(const char *path, int32_t save);
+void ah_beam_reset(void);   /* BeamCacheReset (beam.go:213) */
+
 /* Softmax cross-entropy forward+backward composed from reference ops (one wave64 per row):
  * m=Max, zs=z-m, e=Exp(zs), s=Sum e, logp=zs-Log(s), loss=Sum(onehot*logp)*(-1/B); dz includes the
  * row-max path with its tie split (tensor/gradient_ruleset.go:307-320). */
