@@ -67,6 +67,8 @@ struct ah_device {
     std::unordered_map<std::string, int> gemm_variant;
     // This device's address of the chain's file-scope workspace (ah_chain_step_noalloc), set by ah_open.
     float *chain_scratch = nullptr;
+    // Split-K workspace of the f32 tiled contractions (counters, then partial tiles), set up by ah_open.
+    void *splitk_ws = nullptr;
 };
 
 struct ah_graph {

@@ -15,6 +15,9 @@ namespace ah {
 
 // Number of f16 kernel variants (table Var<V> in gemm16_kernel.h); variant 0 means the tuned choice.
 constexpr int kGemm16Variants = 31;
+// Split-K workspace of a device: counters for up to kSplitKMaxTiles tiles, then kSplitKPartFloats floats.
+constexpr int kSplitKMaxTiles = 4096;
+constexpr long kSplitKPartFloats = 4L << 20;
 
 enum GemmDtype : int { GEMM_F32 = 0, GEMM_F16 = 1 };
 
@@ -47,7 +50,8 @@ struct GemmDesc {
     float *lossacc;   // EPI_MSE scalar accumulator
     int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
     int variant;      // f16 kernel variant (0 = auto; table Var<V> in gemm16_kernel.h), the tuning hook
-    int kgroups;      // f32 tiled kernel: wave sets splitting K (0 = auto, else 1 / 2 / 4 as the tile admits)
+    int kgroups;      // f32 tiled kernel: wave sets splitting K (0 = auto, else 1 / 2 / 4 as the tile admits;
+                      // a fixed value also turns off the split of K across workgroups)
     // Deterministic partial sums instead of atomics (0 = atomic accumulation into colsum[N] / lossacc[0]):
     // with colsum_ld > 0 each wave stores the column sums of its rows, which start at a multiple of 32,
     // to colsum[(row / 32) * colsum_ld + n]; with loss_ld > 0 each wave stores its MSE partial to
@@ -55,6 +59,12 @@ struct GemmDesc {
     // wave writes are left as they are, so the reader sums every entry and re-zeroes it.
     int colsum_ld;
     int loss_ld;
+    // Split-K workspace of the f32 tiled kernel (shapes with too few tiles for the CUs and a long K): one
+    // arrival counter and one ready counter per tile, zero between launches (the finishing workgroup
+    // resets them), then f32 partial tiles, sk_cap floats. Null: no split. Filled in by the dispatcher.
+    int *sk_sync;
+    float *sk_part;
+    long sk_cap;
     // The float scalars sit beside the ints, away from the pointers: the compiler may merge loads of
     // neighbouring fields into one vector, and a vector mixing pointers and floats is kept in memory.
     float scale;

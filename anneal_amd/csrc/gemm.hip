@@ -214,9 +214,12 @@ __global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = acc2[i][j] = (floatx16){};
 
+    // K is shared by the gridDim.y workgroups of a tile (split-K) and the KG groups of each: group
+    // (blockIdx.y, kg) contracts chunks [(blockIdx.y*KG + kg)*nkg, ... + nkg)
+    const int nsplit = gridDim.y, split = blockIdx.y;
     const int nk = (d.K + BK - 1) / BK;
-    const int nkg = (nk + KG - 1) / KG;       // chunks per group
-    const int kbeg = kg * nkg * BK;           // this group's first k (may lie past K: zeros)
+    const int nkg = (nk + KG * nsplit - 1) / (KG * nsplit);   // chunks per group
+    const int kbeg = (split * KG + kg) * nkg * BK;            // this group's first k (may lie past K: zeros)
     la.load(A, d.lda, m0, d.M, kbeg, d.K, avec, tid);
     lb.load(B, d.ldb, n0, d.N, kbeg, d.K, bvec, tid);
     la.store(gsm, tid);
@@ -285,17 +288,74 @@ __global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
                     for (int r = 0; r < 16; r++) red[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
         }
         __syncthreads();
+        if (kg == 0)
+            for (int g = 1; g < KG; g++) {
+                const float *red = (const float *)smem + ((g - 1) * 4 + wave) * NE * 64 + lane;
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * FN + j) * 16 + r) * 64];
+            }
+    }
+    if (nsplit > 1) {
+        // Split-K finish. Each workgroup but the last to arrive stores group 0's accumulators as its
+        // split's partial (element-major, thread-minor: coalesced) with device-scope stores, which are
+        // coherent across the XCDs' L2s; the last (an arrival counter picks it, so no workgroup waits on
+        // one that has not started) folds the splits in split order, its own from registers, so the sum
+        // does not depend on the arrival order, and runs the epilogue.
+        constexpr int NE = FM * FN * 16;
+        const int tile = tm * tiles_n + tn;
+        int *const sync = d.sk_sync + 2 * tile;
+        __shared__ int arrival;
+        if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        float *const part = d.sk_part + (long)tile * nsplit * (NE * kThreads) + tid;
+        if (arrival < nsplit - 1) {
+            if (kg == 0) {
+                float *const mine = part + (long)split * (NE * kThreads);
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++)
+                            __hip_atomic_store(mine + ((i * FN + j) * 16 + r) * kThreads, acc[i][j][r], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's stores have completed
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        // the partners have arrived, so they are running; the wait is bounded all the same
+        if (threadIdx.x == 0)
+            for (int spin = 0; spin < (1 << 22); spin++) {
+                if (__hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nsplit - 1) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        __syncthreads();
         if (kg > 0) return;
-        for (int g = 1; g < KG; g++) {
-            const float *red = (const float *)smem + ((g - 1) * 4 + wave) * NE * 64 + lane;
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++)
+            for (int j = 0; j < FN; j++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] += red[((i * FN + j) * 16 + r) * 64];
+                for (int r = 0; r < 16; r++) {
+                    const float *src = part + ((i * FN + j) * 16 + r) * kThreads;
+                    float v = split == 0 ? acc[i][j][r] : __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    for (int q = 1; q < nsplit; q++)
+                        v += q == split ? acc[i][j][r]
+                                        : __hip_atomic_load(src + (long)q * (NE * kThreads), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    acc[i][j][r] = v;
+                }
+        if (threadIdx.x == 0) {   // ready for the next launch
+            __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    if (kg > 0) return;
     epilogue_tile<EPI, T, FM, FN>(d, acc, m0 + wm0, n0 + wn0, lane);
 }
 
@@ -306,22 +366,34 @@ static hipError_t launch_t(const GemmDesc &d, hipStream_t s) {
     const int nk = (d.K + BK - 1) / BK;
     // k-groups: each of a tile's register-staged K iterations waits on its global loads, so long K
     // loops over few waves are latency bound. Add wave sets (each taking a share of K) while there
-    // are at most 4 workgroups' worth per CU and every group keeps at least 8 chunks
+    // are at most 4 workgroups' worth per CU and every group keeps at least 4 chunks
     // (LDS: 64-tile 4 groups 128 KiB, 128-tile 2 groups 128 KiB).
     int kg = 1;
     if (d.kgroups > 0 && gemm32_kgroups_ok(BM, d.kgroups)) {
         kg = d.kgroups;   // fixed by the caller (a BEAM candidate)
     } else if (BM <= 128) {
         const int maxkg = BM == 64 ? 4 : 2;
-        while (kg < maxkg && tiles * kg <= 1024 && nk >= 16 * kg) kg *= 2;
+        while (kg < maxkg && tiles * kg <= 1024 && nk >= 8 * kg) kg *= 2;   // at least 4 chunks per group
     }
+    // Split-K across workgroups only where the tiles (times their k-groups) leave most CUs idle and each
+    // group still runs a long K loop (16 chunks or more): the partials' device-scope round trip and the
+    // last workgroup's wait cost a few microseconds, which only a long loop pays back. Up to 16 splits,
+    // about 512 workgroups, at least 4 chunks per group.
+    int split = 1;
+    if (d.sk_sync && d.sk_part && d.kgroups == 0 && tiles <= kSplitKMaxTiles && (long)tiles * kg <= 128 &&
+        nk >= 16 * kg) {
+        while (split < 16 && (long)tiles * kg * split * 2 <= 512 && nk >= 4 * kg * split * 2 &&
+               (long)tiles * split * 2 * BM * BM <= d.sk_cap)
+            split *= 2;
+    }
+    const dim3 grid(tiles, split);
     if constexpr (BM == 64) {
-        if (kg == 4) { hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 4>), dim3(tiles), dim3(kThreads * 4), 0, s, d); return hipGetLastError(); }
+        if (kg == 4) { hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 4>), grid, dim3(kThreads * 4), 0, s, d); return hipGetLastError(); }
     }
     if constexpr (BM <= 128) {
-        if (kg == 2) { hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 2>), dim3(tiles), dim3(kThreads * 2), 0, s, d); return hipGetLastError(); }
+        if (kg == 2) { hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 2>), grid, dim3(kThreads * 2), 0, s, d); return hipGetLastError(); }
     }
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 1>), dim3(tiles), dim3(kThreads), 0, s, d);
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BM, TA, TB, EPI, 1>), grid, dim3(kThreads), 0, s, d);
     return hipGetLastError();
 }
 

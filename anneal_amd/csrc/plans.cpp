@@ -112,11 +112,18 @@ static std::string tune_key(const GemmDesc &g) {
     return b;
 }
 
-// Launch with the tuned variant when the caller left the choice open.
+// Launch with the tuned variant when the caller left the choice open, and with the device's split-K
+// workspace (used by the f32 tiled kernel for shapes with few tiles and a long K).
 static hipError_t gemm_run(ah_device *dev, GemmDesc g, hipStream_t s) {
     if (g.variant == 0 && g.dtype == GEMM_F16) {
         auto it = dev->gemm_variant.find(tune_key(g));
         if (it != dev->gemm_variant.end()) g.variant = it->second;
+    }
+    if (dev->splitk_ws) {
+        const size_t sync_bytes = (size_t)kSplitKMaxTiles * 2 * sizeof(int);
+        g.sk_sync = (int *)dev->splitk_ws;
+        g.sk_part = (float *)((char *)dev->splitk_ws + sync_bytes);
+        g.sk_cap = kSplitKPartFloats;
     }
     return gemm_launch(g, s);
 }

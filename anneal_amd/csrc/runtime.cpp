@@ -12,6 +12,7 @@
 
 #include "ah_internal.h"
 #include "rowops.h"
+#include "gemm.h"
 
 namespace ah {
 
@@ -117,6 +118,17 @@ int ah_open(int ordinal, ah_device **out) {
         delete d;
         return fail_hip(e, "ah_open: chain workspace address");
     }
+    {   // split-K counters start at zero; the kernels leave them at zero
+        const size_t sync_bytes = (size_t)kSplitKMaxTiles * 2 * sizeof(int);
+        e = hipMalloc(&d->splitk_ws, sync_bytes + (size_t)kSplitKPartFloats * sizeof(float));
+        if (e == hipSuccess) e = hipMemset(d->splitk_ws, 0, sync_bytes);
+        if (e != hipSuccess) {
+            if (d->splitk_ws) hipFree(d->splitk_ws);
+            hipStreamDestroy(d->stream);
+            delete d;
+            return fail_hip(e, "ah_open: split-K workspace");
+        }
+    }
     *out = d;
     return AH_OK;
 }
@@ -130,6 +142,7 @@ void ah_close(ah_device *d) {
         delete kv.second->tmpl;
         delete kv.second;
     }
+    if (d->splitk_ws) hipFree(d->splitk_ws);
     if (d->t0) hipEventDestroy(d->t0);
     if (d->t1) hipEventDestroy(d->t1);
     hipStreamDestroy(d->stream);
