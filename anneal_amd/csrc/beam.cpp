@@ -68,12 +68,14 @@ long geti(const std::unordered_map<std::string, std::string> &kv, const char *k,
 }
 
 // The lowest-numbered variant with these parameters; fetch 0 means "compiler-scheduled" (modes 0-3, any
-// cross-barrier setting), 4-7 an asm-issued mode with the cross-barrier prefetch.
+// cross-barrier setting), 4-7 an asm-issued mode with the cross-barrier prefetch; ns 0 means any number
+// of stages in flight (only TILE fixes it).
 int f16_variant_of(const G16Params &p) {
     for (int v = 1; v <= kGemm16Variants; v++) {
         G16Params q;
         if (!gemm16_variant_params(v, &q)) continue;
-        if (q.bm != p.bm || q.bn != p.bn || q.wvm != p.wvm || q.wvn != p.wvn || q.bk != p.bk || q.ns != p.ns || q.kg != p.kg)
+        if (q.bm != p.bm || q.bn != p.bn || q.wvm != p.wvm || q.wvn != p.wvn || q.bk != p.bk || q.kg != p.kg ||
+            (p.ns && q.ns != p.ns))
             continue;
         if (p.fetch == 0 ? q.fetch <= 3 : (q.fetch == p.fetch && q.xb == 1)) return v;
     }
@@ -100,6 +102,7 @@ int key_info(const std::string &key, KeyInfo *ki) {
         G16Params &p = ki->knobs.p;
         if (p.fetch <= 3) p.fetch = 0;   // compiler-scheduled class
         p.xb = p.fetch ? 1 : 0;
+        p.ns = 0;                        // stage count left open until a TILE opt fixes it
     } else {
         ki->knobs.tile = (int)geti(ki->kv, "tile", 0);
         ki->knobs.kg = (int)geti(ki->kv, "kg", 0);
@@ -233,12 +236,19 @@ struct CacheEntry {
 std::mutex g_cache_mu;
 std::map<uint64_t, CacheEntry> g_cache;   // kernel key hash -> winner (process-wide, like beamCacheMap)
 
-// Deterministic inputs, varying by buffer index (beam.go:410-421).
+// Deterministic inputs, varying by buffer index (beam.go:410-421). The reference fills
+// ((j + 17 i) % 13 + 1) * 0.01; here each value comes from an integer hash of (buffer, index), uniform
+// in [-1, 1): with the reference's few distinct small values, a candidate that sums K in another order
+// (k-groups) can match the unmodified kernel's bits by coincidence and pass the guard.
 std::vector<std::vector<float>> test_inputs(const ah_exec_item &it) {
     std::vector<std::vector<float>> in;
     for (int b = 1; b < it.n_bufs; b++) {
         std::vector<float> v((size_t)std::max<int64_t>(it.bufs[b].size, 0));
-        for (size_t j = 0; j < v.size(); j++) v[j] = (float)((j + (size_t)(b - 1) * 17) % 13 + 1) * 0.01f;
+        for (size_t j = 0; j < v.size(); j++) {
+            uint32_t h = (uint32_t)j * 0x9E3779B1u ^ (uint32_t)b * 0x85EBCA6Bu;
+            h ^= h >> 16; h *= 0x7FEB352Du; h ^= h >> 15; h *= 0x846CA68Bu; h ^= h >> 16;
+            v[j] = (float)(h >> 8) * (1.0f / 8388608.0f) - 1.0f;
+        }
         in.push_back(std::move(v));
     }
     return in;
