@@ -15,6 +15,7 @@
 
 #include "ah_internal.h"
 #include "conv.h"
+#include "convnet.h"
 #include "gemm.h"
 #include "rowops.h"
 
@@ -542,8 +543,9 @@ struct ChainTrainer : ah_trainer {
 struct ConvNetTrainer : ah_trainer {
     int N, Hin, C1, C2, NC, P1, P2, F;
     float *x, *cw1, *cb1, *cw2, *cb2, *fw, *fb, *H1, *Pl1, *H2, *Pl2, *lg, *dlg, *dP2, *dZ2, *dP1, *dZ1;
-    float *rowloss, *acc, *loss, *gcw1, *gcb1, *gcw2, *gcb2, *gfw, *gfb, *wpart1, *wpart2;
+    float *rowloss, *acc, *loss, *gcw1, *gcb1, *gcw2, *gcb2, *gfw, *gfb, *wpart1, *wpart2, *spart = nullptr;
     int32_t *lab;
+    bool fused = false;   // the one-workgroup-per-sample kernel (convnet.h) + the tail
     int init() {
         N = (int)dims[0]; Hin = (int)dims[1]; C1 = (int)dims[2]; C2 = (int)dims[3]; NC = (int)dims[4];
         if (N <= 0 || Hin <= 0 || Hin % 4 || C1 <= 0 || C2 <= 0 || NC <= 0) return set_error(AH_ERR_INVALID, "CONVNET: bad dims");
@@ -561,6 +563,8 @@ struct ConvNetTrainer : ah_trainer {
         rc |= alloc(&wpart1, (size_t)conv_bwd_w_splits(N, 1, Hin, C1) * C1 * 10);
         rc |= alloc(&wpart2, (size_t)conv_bwd_w_splits(N, C1, P1, C2) * C2 * C1 * 10);
         rc |= alloc(&gcw2, (size_t)C2 * C1 * 9); rc |= alloc(&gcb2, C2); rc |= alloc(&gfw, (size_t)NC * F); rc |= alloc(&gfb, NC);
+        fused = convnet_fused_ok(Hin, C1, C2, NC);
+        if (fused) rc |= alloc(&spart, (size_t)N * net_part(Hin, C1, C2, NC).total);
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * NC));
         return AH_OK;
@@ -588,6 +592,18 @@ struct ConvNetTrainer : ah_trainer {
         hipStream_t s = dev->stream;
         const bool sg = flags & AH_STEP_STORE_GRADS;
         const float a = (float)(-1.0 / (double)B);
+        if (fused) {
+            LAUNCH("convnet", convnet_step_fused(x, lab, cw1, cb1, cw2, cb2, fw, fb, B, Hin, C1, C2, NC, a, rowloss, spart, s));
+            const NetPart o = net_part(Hin, C1, C2, NC);
+            TailArgs ta{};
+            float *p[6] = {cw1, cb1, cw2, cb2, fw, fb}, *go[6] = {gcw1, gcb1, gcw2, gcb2, gfw, gfb};
+            const long off[6] = {o.cw1, o.cb1, o.cw2, o.cb2, o.fw, o.fb};
+            const long len[6] = {o.cb1 - o.cw1, o.cw2 - o.cb1, o.cb2 - o.cw2, o.fw - o.cb2, o.fb - o.fw, o.total - o.fb};
+            for (int i = 0; i < 6; i++) ta.seg[i] = {p[i], nullptr, spart + off[i], sg ? go[i] : nullptr, len[i], 1.0f, B, o.total, 1};
+            ta.nseg = 6; ta.lr = lr; ta.loss_mode = 2; ta.loss_scale = a; ta.rowloss = rowloss; ta.nrow = B; ta.loss_out = loss;
+            LAUNCH("tail", step_tail(ta, s));
+            return AH_OK;
+        }
         LAUNCH("conv1", conv_fwd_relu_pool(x, B, 1, Hin, cw1, cb1, C1, H1, Pl1, s));
         LAUNCH("conv2", conv_fwd_relu_pool(Pl1, B, C1, P1, cw2, cb2, C2, H2, Pl2, s));
         GemmDesc g = gdesc(GEMM_F32, EPI_BIAS, 0, 0, B, NC, F, Pl2, F, fw, F, lg, NC);

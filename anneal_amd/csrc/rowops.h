@@ -30,9 +30,10 @@ struct TailSeg {
     float scale;     // gradient = scale * acc
     int acc_rows;    // > 0: acc holds acc_rows partial rows (row stride acc_ld), summed in row order
     long acc_ld;
+    int keep;        // nonzero: leave acc as it is (its producer rewrites it every step)
 };
 struct TailArgs {
-    TailSeg seg[4];
+    TailSeg seg[6];
     int nseg;
     float lr;
     int loss_mode;   // 0 none, 1 f16-narrowed accumulator * loss_scale, 2 sum(rowloss) * loss_scale

@@ -14,11 +14,9 @@
 #include <algorithm>
 #include "ah_common.h"
 #include "rowops.h"
+#include "softmax_row.h"
 
 namespace ah {
-
-#define AH_INV_LN2 ((float)(1.0 / 0.693147180559945309417232121458176568))
-#define AH_LN2 ((float)0.693147180559945309417232121458176568)
 
 // ── small elementwise kernels ───────────────────────────────────────────────
 
@@ -84,41 +82,11 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float *G, int M, int 
 // loss = Sum(onehot * logp) * a,  a = f32(-1/B); see the oracle's ora_softmax_ce for the op list.
 __global__ __launch_bounds__(256) void softmax_ce_kernel(const float *z, const int32_t *labels, int B, int C,
                                                           float a, float *dz, float *rowloss) {
-#pragma clang fp contract(off)   // each reference op rounds on its own (no fused multiply-add)
     int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     int lane = threadIdx.x & 63;
     if (row >= B) return;
-    const float *zr = z + (long)row * C;
-    int lab = labels[row];
-    float m = -FLT_MAX;
-    for (int c = lane; c < C; c += 64) m = fmaxf(m, zr[c]);
-    m = wave_max(m);
-    float tie = 0.0f, s = 0.0f;
-    for (int c = lane; c < C; c += 64) {
-        float v = zr[c];
-        tie += (v == m) ? 1.0f : 0.0f;
-        s += exp2f((v - m) * AH_INV_LN2);
-    }
-    tie = wave_sum(tie);
-    s = wave_sum(s);
-    float ls = log2f(s) * AH_LN2;
-    if (lane == 0) rowloss[row] = (lab >= 0 && lab < C) ? ((zr[lab] - m) - ls) : 0.0f;
-    float gls = (lab >= 0 && lab < C) ? -a : 0.0f;       // Sum_c -(a*onehot)
-    float glog2 = gls * AH_LN2;
-    float gs = glog2 * (1.0f / (s * AH_LN2));
-    float gm = 0.0f;
-    for (int c = lane; c < C; c += 64) {
-        float v = zr[c];
-        float e = exp2f((v - m) * AH_INV_LN2);
-        float glogp = (c == lab) ? a : 0.0f;
-        float gzs = glogp + ((gs * e) * AH_LN2) * AH_INV_LN2;
-        gm += -gzs;
-        dz[(long)row * C + c] = gzs;
-    }
-    gm = wave_sum(gm);
-    float share = gm * (1.0f / tie);
-    for (int c = lane; c < C; c += 64)
-        if (zr[c] == m) dz[(long)row * C + c] += share;
+    const float rl = softmax_ce_row(z + (long)row * C, labels[row], C, a, dz + (long)row * C, lane);
+    if (lane == 0) rowloss[row] = rl;
 }
 
 // out[0] = (Sum_i v[i]) * a   (single block, fixed-order tree)
@@ -427,7 +395,7 @@ __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
 #pragma unroll
                     for (int j = 0; j < 16; j++) {
                         p[j] += v[j];
-                        if (r + j < r1) col[(long)(r + j) * g.acc_ld] = 0.0f;
+                        if (r + j < r1 && !g.keep) col[(long)(r + j) * g.acc_ld] = 0.0f;
                     }
                 }
 #pragma unroll
@@ -437,7 +405,7 @@ __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
                 a = p[0];
             } else if (q == 0) {
                 a = g.acc[k];
-                g.acc[k] = 0.0f;
+                if (!g.keep) g.acc[k] = 0.0f;
             }
         }
         part[q][e] = a;

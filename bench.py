@@ -131,18 +131,16 @@ def mlp_ce_kernels(B, D, H, C):
 
 
 def convnet_kernels(N=32, Hin=28, C1=8, C2=16, NC=10):
-    """The CONVNET trainer's launches (config 2) with their algorithmic work (direct-convolution FLOPs)."""
+    """The CONVNET trainer's launches (config 2) with their algorithmic work: the fused per-sample step
+    (direct-convolution and fc FLOPs, forward and backward; conv1 has no input gradient), then the tail,
+    which reads the N per-sample gradient rows and reads/writes each parameter and its gradient."""
     P1, P2 = Hin // 2, Hin // 4
     F = C2 * P2 * P2
     c1 = 2.0 * N * C1 * Hin * Hin * 9          # conv1: Ci = 1
     c2 = 2.0 * N * C2 * P1 * P1 * 9 * C1       # conv2
-    return [("conv1", "flop32", c1), ("conv2", "flop32", c2), ("fc", "flop32", 2.0 * N * NC * F),
-            ("softmax_ce", "bytes", 8.0 * N * NC + 8.0 * N), ("dfb", "bytes", 4.0 * N * NC),
-            ("dP2", "flop32", 2.0 * N * F * NC), ("dfw", "flop32", 2.0 * NC * F * N),
-            ("pool2_bwd", "bytes", 4.0 * N * C2 * (P1 * P1 * 2 + P2 * P2 * 2)), ("conv2_dx", "flop32", c2),
-            ("conv2_dw", "flop32", c2), ("conv2_dw_sgd", "bytes", 0.0),
-            ("pool1_bwd", "bytes", 4.0 * N * C1 * (Hin * Hin * 2 + P1 * P1 * 2)), ("conv1_dw", "flop32", c1),
-            ("conv1_dw_sgd", "bytes", 0.0), ("tail", "bytes", 4.0 * N + 16.0 * NC)]
+    fc = 2.0 * N * NC * F
+    nparam = C1 * 10 + C2 * C1 * 9 + C2 + NC * F + NC
+    return [("convnet", "flop32", 2 * c1 + 3 * c2 + 3 * fc), ("tail", "bytes", 4.0 * N * nparam + 12.0 * nparam)]
 
 
 def kernel_table(t, batch, kernels, steps=10):

@@ -117,6 +117,25 @@ def test_config2_convnet_step(dev):
     t.close()
 
 
+def test_convnet_per_op_path(dev):
+    """A plane too large for one workgroup's LDS takes the per-op kernels (conv.hip) instead of the fused
+    per-sample step; same parity bar."""
+    p = data.convnet_inputs(N=4, Hin=64, seed=7)
+    lr = 0.01
+    wl, g, new = O.convnet_step(p, lr)
+    t = Trainer(dev, L.TRAIN_CONVNET, [4, 64, 8, 16, 10], lr)
+    assert t.kernel_count(4) > 2
+    for k in ("x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+        t.set(k, p[k])
+    t.step(4, store_grads=True)
+    assert abs(t.get("loss", 1)[0] - wl) < 1e-4 * max(1, abs(wl))
+    for k in ("dcw1", "dcb1", "dcw2", "dcb2", "dfw", "dfb"):
+        assert O.relerr(t.get(k, g[k].size), g[k].ravel()) < 1e-4, k
+    for k in ("cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+        assert check_update(t.get(k, new[k].size), p[k], new[k], 1e-4), k
+    t.close()
+
+
 def test_config2_tie_split_bit_exact(dev):
     """All-equal pooling windows (ReLU zeros) must split the adjoint exactly like the oracle."""
     p = data.convnet_inputs(N=4, seed=3)
