@@ -1,4 +1,4 @@
-// convnet.h — host launcher of the fused one-sample-per-workgroup conv-net train step (config 2).
+// convnet.h — host launcher of the sample-parallel conv-net train step (config 2).
 #pragma once
 #include "ah_common.h"
 
@@ -22,14 +22,20 @@ __host__ __device__ inline NetPart net_part(int Hin, int C1, int C2, int NC) {
     return o;
 }
 
-// True when a sample's working set fits one workgroup's LDS (64 KiB); otherwise the per-op kernels of
-// conv.h serve the step.
+// True when the two kernels' LDS working sets fit 64 KiB per workgroup (and the fc sizes fit their
+// register/thread mapping); otherwise the per-op kernels of conv.h serve the step.
 bool convnet_fused_ok(int Hin, int C1, int C2, int NC);
-size_t convnet_fused_lds_bytes(int Hin, int C1, int C2, int NC);
-// One workgroup per sample: forward, softmax-CE (rowloss[n] = the label's log-probability, the logit
-// gradient scaled by a) and backward; writes sample n's parameter gradients to part[n * total ..].
-hipError_t convnet_step_fused(const float *x, const int32_t *lab, const float *cw1, const float *cb1, const float *cw2,
-                              const float *cb2, const float *fw, const float *fb, int B, int Hin, int C1, int C2, int NC,
-                              float a, float *rowloss, float *part, hipStream_t s);
+// Floats of the workspace the two kernels exchange through, for batches up to N.
+long convnet_fused_ws_floats(int N, int Hin, int C1, int C2, int NC);
+// Forward: workgroups over samples x conv2 channel groups; writes the pooled planes, window bytes and
+// partial logits to ws.
+hipError_t convnet_fwd_fused(const float *x, const float *cw1, const float *cb1, const float *cw2, const float *cb2,
+                             const float *fw, int B, int Hin, int C1, int C2, int NC, float *ws, hipStream_t s);
+// Backward: workgroups over samples x conv1 channels; softmax-CE (rowloss[n] = the label's
+// log-probability, the logit gradient scaled by a), then sample n's parameter gradients to
+// part[n * total ..].
+hipError_t convnet_bwd_fused(const float *x, const int32_t *lab, const float *cw2, const float *fw, const float *fb, int B,
+                             int Hin, int C1, int C2, int NC, float a, const float *ws, float *rowloss, float *part,
+                             hipStream_t s);
 
 }  // namespace ah

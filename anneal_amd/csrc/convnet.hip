@@ -1,12 +1,16 @@
-// convnet.hip — the config-2 train step of one sample in one workgroup (gfx950).
+// convnet.hip — the config-2 train step as two sample-parallel kernels (gfx950).
 //
-// conv1(1->C1) ReLU pool2 -> conv2(C1->C2) ReLU pool2 -> flatten -> Linear -> softmax-CE, forward and
-// backward, with every intermediate of the sample resident in LDS: the padded input, the padded
-// pooled conv1 planes, the pooled conv2 vector (reused for its gradient), the logits, the padded conv2
-// output gradient (reused for the conv1 output gradient) and conv1's pooled gradient. A pooling
-// window's ReLU/argmax facts are kept as one byte (4 tie bits, 4 dead-ReLU bits), so the conv outputs
-// themselves never leave registers. The sample's parameter gradients go to one row of `part`; the
-// step's tail kernel sums the rows in sample order and applies SGD.
+// conv1(1->C1) ReLU pool2 -> conv2(C1->C2) ReLU pool2 -> flatten -> Linear -> softmax-CE.
+// Forward: workgroup (n, g) stages sample n's padded input in LDS, computes all of conv1 (cheap: one
+// input channel) and conv2's output-channel group g, and the group's share of the logits. It stores
+// the pooled planes, the per-window ReLU/argmax bytes (4 tie bits, 4 dead-ReLU bits; the conv outputs
+// themselves never leave registers) and the partial logits.
+// Backward: workgroup (n, c) owns conv1 channel c (conv2's input channel c). It sums the partial logits,
+// evaluates softmax-CE, rebuilds dP2 and the padded conv2 output gradient of the whole sample in LDS
+// (cheap), then computes conv2's input gradient for channel c, conv2's weight gradient for the pairs
+// (all co, c), the pool/ReLU backward of channel c, and conv1's weight gradient for channel c. The
+// sample's parameter gradients go to one row of `part`; the step's tail kernel sums the rows in sample
+// order and applies SGD.
 //
 // The reference evaluates the same graph op by op (tensor/nn/nn.go:217-303 conv as im2col + matmul,
 // nn.go:350-372 max-pool, gradient_ruleset.go:153-161 ReLU mask and :307-320 the tie split). The
@@ -21,9 +25,10 @@
 
 namespace ah {
 
-constexpr int kNetThreads = 1024;
+constexpr int kFwdThreads = 512;
+constexpr int kBwdThreads = 1024;
 constexpr int kNetMaxNC = 16;   // the fc weights of a thread's feature stay in registers
-constexpr int kNetWaves = kNetThreads / 64;
+constexpr int kFwdGroupCh = 4;  // conv2 output channels per forward workgroup
 
 // A plane of `rows` rows in LDS: row stride ld, plane stride ps. ld = 2 (mod 8) and ps = 1 (mod 32)
 // spread the lanes of a wave over the banks when they differ by channel and by a run of four rows
@@ -38,44 +43,25 @@ __host__ __device__ inline Plane net_plane(int rows, int width) {
     return p;
 }
 
-// LDS layout, in floats (the mask bytes at the end). Host and device evaluate the same function.
-struct NetLayout {
-    Plane px, p1, pz1;
-    int xs, p1s, p2s, lg, dlg, red, gs, dp1s, w1, w2, masks, total;
-};
-__host__ __device__ inline NetLayout net_layout(int Hin, int C1, int C2, int NC) {
-    const int P1 = Hin / 2, P2 = Hin / 4;
-    NetLayout L;
-    L.px = net_plane(Hin + 2, Hin + 2);   // the input, zero-padded by one
-    L.p1 = net_plane(P1 + 2, P1 + 2);     // pooled conv1 (conv2's input) and dZ2, zero-padded by one
-    L.pz1 = net_plane(Hin, Hin);          // dZ1
-    int o = 0;
-    L.xs = o;    o += L.px.ps;
-    L.p1s = o;   o += C1 * L.p1.ps;
-    L.p2s = o;   o += C2 * P2 * P2;            // pooled conv2 (= the fc input), then its gradient
-    L.lg = o;    o += NC;
-    L.dlg = o;   o += NC;
-    L.red = o;   o += kNetMaxNC * kNetWaves;   // per-wave logit partials
-    L.gs = o;    o += (C2 * L.p1.ps > C1 * L.pz1.ps) ? C2 * L.p1.ps : C1 * L.pz1.ps;   // dZ2, then dZ1
-    L.dp1s = o;  o += C1 * P1 * P1;            // gradient of pooled conv1
-    L.w1 = o;    o += C1 * 9 + C1;             // conv weights and biases (read wave-uniform: LDS broadcasts)
-    L.w2 = o;    o += C2 * C1 * 9 + C2;
-    L.masks = o; o += (C1 * P1 * P1 + C2 * P2 * P2 + 3) / 4;
-    L.total = o;
-    return L;
-}
-
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// A filter's 9 taps, stored at a 16-byte aligned LDS address with a stride of 12 floats, read as three
+// 16-byte loads (issued together, rather than one load and wait per tap).
+#define WEIGHTS9(p)                                                                                      \
+    {((const float4 *)(p))[0].x, ((const float4 *)(p))[0].y, ((const float4 *)(p))[0].z,                  \
+     ((const float4 *)(p))[0].w, ((const float4 *)(p))[1].x, ((const float4 *)(p))[1].y,                  \
+     ((const float4 *)(p))[1].z, ((const float4 *)(p))[1].w, ((const float4 *)(p))[2].x}
 
 // conv3x3 (pad 1) + bias + ReLU (tagged) + 2x2 max-pool over zero-padded input planes. A wave owns an
 // output channel (so the weights are wave-uniform) and a lane a pooling window: the window's four conv
-// outputs share one 4x4 input patch per input channel. Pooled value -> out[c*out.ps + (ph+off)*out.ld +
+// outputs share one 4x4 input patch per input channel. Weights w[c][ci][12] (taps 0-8), biases b[c].
+// Pooled value -> out[c*out.ps + (ph+off)*out.ld +
 // pw+off]; the window's tie and dead-ReLU bits -> mask[c*P*P + win].
 __device__ void net_conv_pool(const float *in, Plane pin, int Ci, int H, const float *w, const float *b, int Co,
-                              float *out, Plane pout, int off, uint8_t *mask) {
+                              float *out, Plane pout, int off, uint8_t *mask, int nw) {
     const int P = H / 2, lane = threadIdx.x & 63;
-    for (int c = wave_id(); c < Co; c += kNetWaves) {
-        const float *wc = w + c * Ci * 9;
+    for (int c = wave_id(); c < Co; c += nw) {
+        const float *wc = w + c * Ci * 12;
         const float bc = b[c];
         for (int win = lane; win < P * P; win += 64) {
             const int ph = win / P, pw = win % P;
@@ -88,11 +74,12 @@ __device__ void net_conv_pool(const float *in, Plane pin, int Ci, int H, const f
                 for (int r = 0; r < 4; r++)
 #pragma unroll
                     for (int q = 0; q < 4; q++) t[r][q] = xp[r * pin.ld + q];
+                const float wr[9] = WEIGHTS9(wc + ci * 12);
 #pragma unroll
                 for (int kh = 0; kh < 3; kh++)
 #pragma unroll
                     for (int kw = 0; kw < 3; kw++) {
-                        const float wt = wc[ci * 9 + kh * 3 + kw];
+                        const float wt = wr[kh * 3 + kw];
                         a0 = a0 + t[kh][kw] * wt;
                         a1 = a1 + t[kh][kw + 1] * wt;
                         a2 = a2 + t[kh + 1][kw] * wt;
@@ -114,7 +101,7 @@ __device__ void net_conv_pool(const float *in, Plane pin, int Ci, int H, const f
 
 // Pool backward (equal split over tied maxima) fused with the ReLU mask, from the window bytes.
 __device__ void net_pool_bwd(const float *dP, int C, int P, const uint8_t *mask, float *out, Plane pout, int off) {
-    for (int i = threadIdx.x; i < C * P * P; i += kNetThreads) {
+    for (int i = threadIdx.x; i < C * P * P; i += blockDim.x) {
         const int c = i / (P * P), win = i % (P * P), ph = win / P, pw = win % P;
         const unsigned bits = mask[i];
         const float tie = (float)__builtin_popcount(bits & 15u);
@@ -128,76 +115,86 @@ __device__ void net_pool_bwd(const float *dP, int C, int P, const uint8_t *mask,
     }
 }
 
-// dX[ci][y][x] = sum over (kh, kw) of (sum over co of G[co][y-kh+1][x-kw+1] * w[co][ci][kh][kw]), G in
-// zero-padded planes. A wave (of the first nw) owns an input channel, a lane a 2x2 output block (one 4x4
-// G patch per co).
-__device__ void net_conv_dx(const float *G, Plane pg, int Co, int H, const float *w, int Ci, float *dX, int nw) {
-    const int Q = H / 2, lane = threadIdx.x & 63;
-    if (wave_id() >= nw) return;
-    for (int ci = wave_id(); ci < Ci; ci += nw)
-        for (int blk = lane; blk < Q * Q; blk += 64) {
-            const int by = blk / Q, bx = blk % Q;
-            float p[4][9];
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int k = 0; k < 9; k++) p[q][k] = 0.0f;
-#pragma unroll 2
-            for (int co = 0; co < Co; co++) {
-                const float *gp = G + co * pg.ps + 2 * by * pg.ld + 2 * bx;
-                float t[4][4];
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) t[r][q] = gp[r * pg.ld + q];
-                const float *wc = w + (co * Ci + ci) * 9;
-#pragma unroll
-                for (int kh = 0; kh < 3; kh++)
-#pragma unroll
-                    for (int kw = 0; kw < 3; kw++) {
-                        const float wt = wc[kh * 3 + kw];
-#pragma unroll
-                        for (int q = 0; q < 4; q++)
-                            p[q][kh * 3 + kw] = p[q][kh * 3 + kw] + t[(q >> 1) - kh + 2][(q & 1) - kw + 2] * wt;
-                    }
-            }
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 9; k++) acc += p[q][k];
-                dX[ci * H * H + (2 * by + (q >> 1)) * H + 2 * bx + (q & 1)] = acc;
-            }
-        }
+// The sum of a wave's 64 values, in every lane, in a fixed order: DPP within each row of 16 lanes
+// (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four row sums in order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);   // row_half_mirror
+    v += dpp_mov<0x140>(v);   // row_mirror
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
-// One sample's weight and bias gradients: dW[co][ci][tap] = sum_p G[co][p] * X[ci][p + tap] and
-// db[co] = sum_p G[co][p]. G[co][y][x] = G[co*pg.ps + y*pg.ld + x]; X in zero-padded planes. Each
-// (co, ci) pair is split over RS = R*S consecutive lanes (R row ranges times S column ranges), each
-// lane sweeping a 3x3 window along its part of the rows; the RS partial sums are combined with a fixed
-// shuffle tree. Waves w0 .. w0+nw-1 take part.
-__device__ void net_conv_dw(const float *G, Plane pg, const float *X, Plane px, int Ci, int H, int Co,
-                            float *__restrict__ dw, float *__restrict__ db, int w0, int nw) {
-    const int lane = threadIdx.x & 63, pairs = Co * Ci, wv = wave_id() - w0;
+// dX[y][x] = sum over (kh, kw) of (sum over co of G[co][y-kh+1][x-kw+1] * w[co][kh][kw]) for one input
+// channel, G in zero-padded planes: the order of the per-op kernel. A lane owns one output; waves
+// w0 .. w0+nw-1 take part. Weights w[co][12] (taps 0-8).
+__device__ void net_conv_dx1(const float *G, Plane pg, int Co, int H, const float *w, float *dX, int w0, int nw) {
+    const int wv = wave_id() - w0;
     if (wv < 0 || wv >= nw) return;
-    int R = 1, S = 1;
-    while (R * S < 64 && pairs * R * S * 2 <= nw * 64) {   // rows first, then columns
-        if (R * 2 <= H) R *= 2;
-        else if (S * 2 <= H / 4) S *= 2;
-        else break;
+    for (int o = wv * 64 + (threadIdx.x & 63); o < H * H; o += nw * 64) {
+        const int y = o / H, x = o % H;
+        float p[9];
+#pragma unroll
+        for (int k = 0; k < 9; k++) p[k] = 0.0f;
+        const float *gp = G + y * pg.ld + x;   // padded rows y..y+2 = G rows y-1..y+1
+#pragma unroll 2
+        for (int co = 0; co < Co; co++) {
+            float t[3][3];
+#pragma unroll
+            for (int r = 0; r < 3; r++)
+#pragma unroll
+                for (int q = 0; q < 3; q++) t[r][q] = gp[co * pg.ps + r * pg.ld + q];
+            const float wr[9] = WEIGHTS9(w + co * 12);
+#pragma unroll
+            for (int kh = 0; kh < 3; kh++)
+#pragma unroll
+                for (int kw = 0; kw < 3; kw++) p[kh * 3 + kw] = p[kh * 3 + kw] + t[2 - kh][2 - kw] * wr[kh * 3 + kw];
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 9; k++) acc += p[k];
+        dX[o] = acc;
     }
-    const int RS = R * S, rows = (H + R - 1) / R, cols = (H + S - 1) / S;
-    for (int base = wv * 64; base < pairs * RS; base += nw * 64) {
-        const int item = base + lane, pair = item / RS, r = (item % RS) / S, sc = item % S;
-        const bool live = item < pairs * RS;
-        const int co = live ? pair / Ci : 0, ci = live ? pair % Ci : 0;
+}
+
+// DPP sum over each row of 16 lanes (quad xor 1, quad xor 2, half-row mirror, row mirror); every lane
+// of the row holds the row's sum.
+__device__ __forceinline__ float row16_total(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    return v;
+}
+
+// Weight and bias gradients of one sample for Co output channels and one input channel:
+// dW[co][tap] = sum_p G[co][p] * X[p + tap], db[co] = sum_p G[co][p], G[co][y][x] = G[co*pg.ps + y*pg.ld
+// + x], X zero-padded. A block of Lb lanes (16 when H <= 16, else 64) owns a channel: lane b sweeps
+// row b % Ry (Ry = 16 or 32) over column segment b / Ry with a sliding 3x3 window; the block's partial
+// sums are combined in a fixed DPP order. Waves w0 .. w0+nw-1 take part. Results: dw[co * dw_stride +
+// tap], and db[co] when db is not null.
+__device__ void net_conv_dw_rows(const float *G, Plane pg, const float *X, Plane px, int H, int Co,
+                                 float *__restrict__ dw, int dw_stride, float *__restrict__ db, int w0, int nw) {
+    const int wv = wave_id() - w0, lane = threadIdx.x & 63;
+    if (wv < 0 || wv >= nw) return;
+    const int Lb = H <= 16 ? 16 : 64, Ry = H <= 16 ? 16 : 32, S = Lb / Ry, cols = (H + S - 1) / S;
+    const int per_wave = 64 / Lb;
+    for (int cb = wv * per_wave; cb < Co; cb += nw * per_wave) {   // wave-uniform loop
+        const int b = lane % Lb, co = cb + lane / Lb, y = b % Ry, x0 = (b / Ry) * cols, x1 = min(H, x0 + cols);
         float acc[10];
 #pragma unroll
         for (int k = 0; k < 10; k++) acc[k] = 0.0f;
-        const int y0 = live ? r * rows : H, y1 = min(H, y0 + rows);
-        const int x0 = sc * cols, x1 = min(H, x0 + cols);
-        for (int y = y0; y < y1; y++) {
-            const float *xr = X + ci * px.ps + y * px.ld;   // padded rows y..y+2 are input rows y-1..y+1
+        if (co < Co && y < H) {
+            const float *xr = X + y * px.ld;   // padded rows y..y+2 are input rows y-1..y+1
             const float *gr = G + co * pg.ps + y * pg.ld;
             float c0[3], c1[3], c2[3];
 #pragma unroll
@@ -217,134 +214,308 @@ __device__ void net_conv_dw(const float *G, Plane pg, const float *X, Plane px, 
                 for (int k = 0; k < 3; k++) { c0[k] = c1[k]; c1[k] = c2[k]; }
             }
         }
-        for (int o = RS / 2; o >= 1; o >>= 1)
 #pragma unroll
-            for (int k = 0; k < 10; k++) acc[k] += __shfl_xor(acc[k], o, 64);
-        if (live && item % RS == 0) {
+        for (int k = 0; k < 10; k++) acc[k] = row16_total(acc[k]);
+        if (Lb == 64) {
 #pragma unroll
-            for (int k = 0; k < 9; k++) dw[pair * 9 + k] = acc[k];
-            if (ci == 0) db[co] = acc[9];
+            for (int k = 0; k < 10; k++) {
+                const int bits = __builtin_bit_cast(int, acc[k]);
+                acc[k] = (__builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0)) +
+                          __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16))) +
+                         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32)) +
+                          __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 48)));
+            }
+        }
+        if (b < 10 && co < Co) {
+            float mine = acc[0];
+#pragma unroll
+            for (int k = 1; k < 10; k++) mine = b == k ? acc[k] : mine;
+            if (b < 9) dw[co * dw_stride + b] = mine;
+            else if (db) db[co] = mine;
         }
     }
 }
 
-__global__ __launch_bounds__(kNetThreads) void convnet_step_kernel(
-    const float *__restrict__ x, const int32_t *__restrict__ lab, const float *__restrict__ cw1,
-    const float *__restrict__ cb1, const float *__restrict__ cw2, const float *__restrict__ cb2,
-    const float *__restrict__ fw, const float *__restrict__ fb, int Hin, int C1, int C2, int NC, float a,
-    float *__restrict__ rowloss, float *__restrict__ part, long part_ld) {
+// ── the two kernels ─────────────────────────────────────────────────────────
+
+// Global workspace between the kernels, offsets in floats (mask bytes packed four to a float).
+struct NetWs {
+    long p1, p2, lgp, m1, m2, total;
+};
+__host__ __device__ inline int net_groups(int C2) { return (C2 + kFwdGroupCh - 1) / kFwdGroupCh; }
+__host__ __device__ inline NetWs net_ws(int N, int Hin, int C1, int C2, int NC) {
+    const long P1 = Hin / 2, P2 = Hin / 4, F = (long)C2 * P2 * P2;
+    NetWs w;
+    long o = 0;
+    w.p1 = o;  o += (long)N * C1 * P1 * P1;              // pooled conv1, [n][c][P1][P1]
+    w.p2 = o;  o += (long)N * F;                         // pooled conv2 (the fc input), [n][F]
+    w.lgp = o; o += (long)N * net_groups(C2) * NC;       // partial logits, [n][group][NC]
+    w.m1 = o;  o += ((long)N * C1 * P1 * P1 + 3) / 4;    // conv1 window bytes, [n][c][P1*P1]
+    w.m2 = o;  o += ((long)N * F + 3) / 4;               // conv2 window bytes, [n][F]
+    w.total = o;
+    return w;
+}
+
+// Forward LDS layout (floats; the mask bytes at the end).
+struct FwdLayout {
+    Plane px, p1;
+    int xs, p1s, w1, w2, b1, b2, p2g, red, m1, total;
+};
+__host__ __device__ inline FwdLayout fwd_layout(int Hin, int C1) {
+    const int P1 = Hin / 2, P2 = Hin / 4;
+    FwdLayout L;
+    L.px = net_plane(Hin + 2, Hin + 2);   // the input, zero-padded by one
+    L.p1 = net_plane(P1 + 2, P1 + 2);     // pooled conv1, zero-padded by one (conv2's input)
+    int o = 0;
+    L.xs = o;  o += L.px.ps;
+    L.p1s = o; o += C1 * L.p1.ps;
+    o = (o + 3) & ~3;
+    L.w1 = o;  o += C1 * 12;                          // conv1 weights [c][12]
+    L.w2 = o;  o += kFwdGroupCh * C1 * 12;            // the group's conv2 weights [c][ci][12]
+    L.b1 = o;  o += C1;
+    L.b2 = o;  o += kFwdGroupCh;
+    L.p2g = o; o += kFwdGroupCh * P2 * P2;            // the group's pooled conv2 planes
+    L.red = o; o += kNetMaxNC * (kFwdThreads / 64);   // per-wave logit partials
+    L.m1 = o;  o += (C1 * P1 * P1 + 3) / 4;
+    L.total = o;
+    return L;
+}
+
+__global__ __launch_bounds__(kFwdThreads) void convnet_fwd_kernel(
+    const float *__restrict__ x, const float *__restrict__ cw1, const float *__restrict__ cb1,
+    const float *__restrict__ cw2, const float *__restrict__ cb2, const float *__restrict__ fw, int Hin, int C1,
+    int C2, int NC, float *__restrict__ ws) {
     extern __shared__ float lds[];
-    const int n = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    constexpr int NW = kFwdThreads / 64;
+    const int n = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63, G = gridDim.y;
     const int P1 = Hin / 2, P2 = Hin / 4, F = C2 * P2 * P2;
-    const NetLayout L = net_layout(Hin, C1, C2, NC);
-    float *xs = lds + L.xs, *p1s = lds + L.p1s, *p2s = lds + L.p2s, *lg = lds + L.lg, *dlg = lds + L.dlg;
-    float *gs = lds + L.gs, *dp1s = lds + L.dp1s, *w1s = lds + L.w1, *w2s = lds + L.w2;
-    uint8_t *m1 = (uint8_t *)(lds + L.masks), *m2 = m1 + C1 * P1 * P1;
+    const int c0 = g * kFwdGroupCh, nc = min(C2, c0 + kFwdGroupCh) - c0, Fg = nc * P2 * P2, fbase = c0 * P2 * P2;
+    const FwdLayout L = fwd_layout(Hin, C1);
+    const NetWs W = net_ws(gridDim.x, Hin, C1, C2, NC);
+    float *xs = lds + L.xs, *p1s = lds + L.p1s, *w1s = lds + L.w1, *w2s = lds + L.w2, *p2g = lds + L.p2g;
+    uint8_t *m1s = (uint8_t *)(lds + L.m1);
+
+    // the fc weights of this thread's feature, loaded now and used after the convolutions
+    float fwv[kNetMaxNC];
+#pragma unroll
+    for (int k = 0; k < kNetMaxNC; k++) fwv[k] = (k < NC && tid < Fg) ? fw[(long)k * F + fbase + tid] : 0.0f;
+
+    // every global load of the staging is issued before the first LDS store
+    const float *xn = x + (long)n * Hin * Hin;
+    float xv[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int i = tid + j * kFwdThreads, yy = i / L.px.ld, xx = i % L.px.ld;
+        const bool in = i < L.px.ps && yy >= 1 && yy <= Hin && xx >= 1 && xx <= Hin;
+        xv[j] = in ? xn[(yy - 1) * Hin + xx - 1] : 0.0f;
+    }
+    const float w1v = tid < C1 * 9 ? cw1[tid] : 0.0f;
+    const float w2v = tid < nc * C1 * 9 ? cw2[(long)c0 * C1 * 9 + tid] : 0.0f;
+    const float b1v = tid < C1 ? cb1[tid] : 0.0f;
+    const float b2v = tid < nc ? cb2[c0 + tid] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+        if (tid + j * kFwdThreads < L.px.ps) xs[tid + j * kFwdThreads] = xv[j];
+    if (tid < C1 * 9) w1s[(tid / 9) * 12 + tid % 9] = w1v;
+    if (tid < nc * C1 * 9) w2s[(tid / 9) * 12 + tid % 9] = w2v;
+    if (tid < C1) lds[L.b1 + tid] = b1v;
+    if (tid < nc) lds[L.b2 + tid] = b2v;
+    for (int i = tid; i < C1 * L.p1.ps; i += kFwdThreads) p1s[i] = 0.0f;
+    __syncthreads();
+
+    net_conv_pool(xs, L.px, 1, Hin, w1s, lds + L.b1, C1, p1s, L.p1, 1, m1s, NW);
+    __syncthreads();
+    net_conv_pool(p1s, L.p1, C1, P1, w2s, lds + L.b2, nc, p2g, Plane{P2, P2 * P2}, 0,
+                  (uint8_t *)(ws + W.m2) + (long)n * F + fbase, NW);
+    if (g == 0) {   // conv1's pooled planes and window bytes, for the backward
+        float *p1g = ws + W.p1 + (long)n * C1 * P1 * P1;
+        for (int i = tid; i < C1 * P1 * P1; i += kFwdThreads) {
+            const int c = i / (P1 * P1), y = (i / P1) % P1, xx = i % P1;
+            p1g[i] = p1s[c * L.p1.ps + (y + 1) * L.p1.ld + xx + 1];
+        }
+        uint8_t *m1g = (uint8_t *)(ws + W.m1) + (long)n * C1 * P1 * P1;
+        for (int i = tid; i < C1 * P1 * P1; i += kFwdThreads) m1g[i] = m1s[i];
+    }
+    __syncthreads();
+
+    // the group's share of the logits: per-wave sums, then the waves in order
+    const float pv = tid < Fg ? p2g[tid] : 0.0f;
+    if (tid < Fg) ws[W.p2 + (long)n * F + fbase + tid] = pv;
+    float v[kNetMaxNC];
+#pragma unroll
+    for (int k = 0; k < kNetMaxNC; k++) v[k] = k < NC ? wave_total(pv * fwv[k]) : 0.0f;
+    float *red = lds + L.red;
+    if (lane < NC) {
+        float mine = v[0];
+#pragma unroll
+        for (int k = 1; k < kNetMaxNC; k++) mine = lane == k ? v[k] : mine;
+        red[lane * NW + wave_id()] = mine;
+    }
+    __syncthreads();
+    if (tid < NC) {
+        float s = 0.0f;
+        for (int q = 0; q < NW; q++) s += red[tid * NW + q];
+        ws[W.lgp + ((long)n * G + g) * NC + tid] = s;
+    }
+}
+
+// Backward LDS layout (floats; the mask bytes at the end).
+struct BwdLayout {
+    Plane px, p1, pz1;
+    int xs, p1c, gs, p2, lg, dlg, dp1, z1, w2c, lgp, m2, m1, total;
+};
+__host__ __device__ inline BwdLayout bwd_layout(int Hin, int C1, int C2, int NC) {
+    const int P1 = Hin / 2, P2 = Hin / 4;
+    BwdLayout L;
+    L.px = net_plane(Hin + 2, Hin + 2);
+    L.p1 = net_plane(P1 + 2, P1 + 2);
+    L.pz1 = net_plane(Hin, Hin);
+    int o = 0;
+    L.xs = o;  o += L.px.ps;                 // the input, zero-padded (conv1's weight gradient)
+    L.p1c = o; o += L.p1.ps;                 // pooled conv1 channel c, zero-padded
+    L.gs = o;  o += C2 * L.p1.ps;            // conv2's output gradient, zero-padded
+    L.p2 = o;  o += C2 * P2 * P2;            // pooled conv2, then its gradient
+    L.lg = o;  o += NC;
+    L.dlg = o; o += NC;
+    L.dp1 = o; o += P1 * P1;                 // gradient of pooled conv1 channel c
+    L.z1 = o;  o += L.pz1.ps;                // conv1's output gradient, channel c
+    o = (o + 3) & ~3;
+    L.w2c = o; o += C2 * 12;                 // conv2 weights of input channel c, [co][12]
+    L.lgp = o; o += net_groups(C2) * NC + NC + 1;   // partial logits, fc bias, label
+    L.m2 = o;  o += (C2 * P2 * P2 + 3) / 4;
+    L.m1 = o;  o += (P1 * P1 + 3) / 4;
+    L.total = o;
+    return L;
+}
+
+__global__ __launch_bounds__(kBwdThreads) void convnet_bwd_kernel(
+    const float *__restrict__ x, const int32_t *__restrict__ lab, const float *__restrict__ cw2,
+    const float *__restrict__ fw, const float *__restrict__ fb, int Hin, int C1, int C2, int NC, int G, float a,
+    const float *__restrict__ ws, float *__restrict__ rowloss, float *__restrict__ part, long part_ld) {
+    extern __shared__ float lds[];
+    constexpr int NW = kBwdThreads / 64;
+    const int n = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int P1 = Hin / 2, P2 = Hin / 4, F = C2 * P2 * P2;
+    const BwdLayout L = bwd_layout(Hin, C1, C2, NC);
+    const NetWs W = net_ws(gridDim.x, Hin, C1, C2, NC);
     const NetPart O = net_part(Hin, C1, C2, NC);
+    float *xs = lds + L.xs, *p1c = lds + L.p1c, *gs = lds + L.gs, *p2 = lds + L.p2, *lg = lds + L.lg;
+    float *dlg = lds + L.dlg, *dp1 = lds + L.dp1, *z1 = lds + L.z1, *w2c = lds + L.w2c;
+    uint8_t *m2 = (uint8_t *)(lds + L.m2), *m1 = (uint8_t *)(lds + L.m1);
     float *row = part + (long)n * part_ld;
 
-    // the fc weights of this thread's feature f = tid, and the label, are loaded now and used after the
-    // convolutions
     float fwv[kNetMaxNC];
 #pragma unroll
     for (int k = 0; k < kNetMaxNC; k++) fwv[k] = (k < NC && tid < F) ? fw[(long)k * F + tid] : 0.0f;
-    const int label = lab[n];
-
-    // stage the padded input and the conv parameters; clear the planes whose borders must read as zero
+    // every global load of the staging is issued before the first LDS store
     const float *xn = x + (long)n * Hin * Hin;
-    const int W1 = Hin + 2;
-    for (int i = tid; i < W1 * W1; i += kNetThreads) {
-        const int yy = i / W1, xx = i % W1;
-        const bool in = yy >= 1 && yy <= Hin && xx >= 1 && xx <= Hin;
-        xs[yy * L.px.ld + xx] = in ? xn[(yy - 1) * Hin + xx - 1] : 0.0f;
+    const float *p1n = ws + W.p1 + ((long)n * C1 + c) * P1 * P1;
+    const uint8_t *m2n = (const uint8_t *)(ws + W.m2) + (long)n * F;
+    const uint8_t *m1n = (const uint8_t *)(ws + W.m1) + ((long)n * C1 + c) * P1 * P1;
+    float xv[2], p1v, p2v, w2v, lgv = 0.0f;
+    uint8_t m2v, m1v;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int i = tid + j * kBwdThreads, yy = i / L.px.ld, xx = i % L.px.ld;
+        const bool in = i < L.px.ps && yy >= 1 && yy <= Hin && xx >= 1 && xx <= Hin;
+        xv[j] = in ? xn[(yy - 1) * Hin + xx - 1] : 0.0f;
     }
-    for (int i = tid; i < C1 * L.p1.ps; i += kNetThreads) p1s[i] = 0.0f;
-    for (int i = tid; i < C2 * L.p1.ps; i += kNetThreads) gs[i] = 0.0f;
-    for (int i = tid; i < C1 * 9; i += kNetThreads) w1s[i] = cw1[i];
-    for (int i = tid; i < C1; i += kNetThreads) w1s[C1 * 9 + i] = cb1[i];
-    for (int i = tid; i < C2 * C1 * 9; i += kNetThreads) w2s[i] = cw2[i];
-    for (int i = tid; i < C2; i += kNetThreads) w2s[C2 * C1 * 9 + i] = cb2[i];
-    __syncthreads();
-
-    net_conv_pool(xs, L.px, 1, Hin, w1s, w1s + C1 * 9, C1, p1s, L.p1, 1, m1);
-    __syncthreads();
-    net_conv_pool(p1s, L.p1, C1, P1, w2s, w2s + C2 * C1 * 9, C2, p2s, Plane{P2, P2 * P2}, 0, m2);
-    __syncthreads();
-
-    // fc: thread f multiplies its feature into every logit; per-wave sums, then the waves in order
     {
-        const float pv = tid < F ? p2s[tid] : 0.0f;
-        float *red = lds + L.red;
-        float v[kNetMaxNC];   // all logits' shuffle trees in flight together (fwv[k] = 0 for k >= NC)
+        const int yy = tid / L.p1.ld, xx = tid % L.p1.ld;
+        const bool in = tid < L.p1.ps && yy >= 1 && yy <= P1 && xx >= 1 && xx <= P1;
+        p1v = in ? p1n[(yy - 1) * P1 + xx - 1] : 0.0f;
+    }
+    p2v = tid < F ? ws[W.p2 + (long)n * F + tid] : 0.0f;
+    m2v = tid < F ? m2n[tid] : 0;
+    m1v = tid < P1 * P1 ? m1n[tid] : 0;
+    w2v = tid < C2 * 9 ? cw2[((long)(tid / 9) * C1 + c) * 9 + tid % 9] : 0.0f;
+    if (tid < G * NC) lgv = ws[W.lgp + (long)n * G * NC + tid];
+    else if (tid < G * NC + NC) lgv = fb[tid - G * NC];
+    else if (tid == G * NC + NC) lgv = __int_as_float(lab[n]);
 #pragma unroll
-        for (int k = 0; k < kNetMaxNC; k++) v[k] = pv * fwv[k];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-            for (int k = 0; k < kNetMaxNC; k++) v[k] += __shfl_xor(v[k], o, 64);
-        if (lane < NC) {
-            float mine = v[0];
-#pragma unroll
-            for (int k = 1; k < kNetMaxNC; k++) mine = lane == k ? v[k] : mine;
-            red[lane * kNetWaves + wave_id()] = mine;
-        }
-        __syncthreads();
-        if (tid < NC) {
+    for (int j = 0; j < 2; j++)
+        if (tid + j * kBwdThreads < L.px.ps) xs[tid + j * kBwdThreads] = xv[j];
+    if (tid < L.p1.ps) p1c[tid] = p1v;
+    if (tid < F) { p2[tid] = p2v; m2[tid] = m2v; }
+    if (tid < P1 * P1) m1[tid] = m1v;
+    if (tid < C2 * 9) w2c[(tid / 9) * 12 + tid % 9] = w2v;
+    if (tid <= G * NC + NC) lds[L.lgp + tid] = lgv;
+    for (int i = tid; i < C2 * L.p1.ps; i += kBwdThreads) gs[i] = 0.0f;
+    __syncthreads();
+    if (wave_id() == 0) {   // the logits: the groups' partial sums in order, then the bias
+        const float *lgs = lds + L.lgp;
+        for (int k = lane; k < NC; k += 64) {
             float v = 0.0f;
-            for (int q = 0; q < kNetWaves; q++) v += red[tid * kNetWaves + q];
-            lg[tid] = v + fb[tid];
+            for (int q = 0; q < G; q++) v += lgs[q * NC + k];
+            lg[k] = v + lgs[G * NC + k];
         }
-        __syncthreads();
-        if (wave_id() == 0) {
-            const float rl = softmax_ce_row(lg, label, NC, a, dlg, lane);
-            if (lane == 0) rowloss[n] = rl;
-        }
-        __syncthreads();
-        // fc backward: this sample's dfw row (rank one) and dfb, and dP2 in place of P2
-        if (tid < F) {
-            float d = 0.0f;
+        const float rl = softmax_ce_row(lg, __float_as_int(lgs[G * NC + NC]), NC, a, dlg, lane);
+        if (lane == 0 && c == 0) rowloss[n] = rl;
+    }
+    __syncthreads();
+
+    // fc backward: dP2 in place of P2; this workgroup's slice of the sample's dfw row (rank one), dfb
+    if (tid < F) {
+        const float pv = p2[tid];
+        const int Fs = (F + gridDim.y - 1) / gridDim.y;
+        const bool mine = tid >= c * Fs && tid < (c + 1) * Fs;
+        float d = 0.0f;
 #pragma unroll
-            for (int k = 0; k < kNetMaxNC; k++) {
-                if (k >= NC) break;
-                const float g = dlg[k];
-                row[O.fw + (long)k * F + tid] = g * pv;
-                d += g * fwv[k];
-            }
-            p2s[tid] = d;
+        for (int k = 0; k < kNetMaxNC; k++) {
+            if (k >= NC) break;
+            const float gk = dlg[k];
+            if (mine) row[O.fw + (long)k * F + tid] = gk * pv;
+            d += gk * fwv[k];
         }
-        if (tid < NC) row[O.fb + tid] = dlg[tid];
+        p2[tid] = d;
     }
+    if (c == 0 && tid < NC) row[O.fb + tid] = dlg[tid];
     __syncthreads();
 
-    net_pool_bwd(p2s, C2, P2, m2, gs, L.p1, 1);   // dZ2, padded
+    net_pool_bwd(p2, C2, P2, m2, gs, L.p1, 1);   // dZ2 of the whole sample, padded
     __syncthreads();
-    {   // the input gradient and the weight gradient of conv2 side by side, on disjoint waves
-        const int nx = C1 < kNetWaves / 2 ? C1 : kNetWaves / 2;
-        net_conv_dx(gs, L.p1, C2, P1, w2s, C1, dp1s, nx);
-        net_conv_dw(gs + L.p1.ld + 1, L.p1, p1s, L.p1, C1, P1, C2, row + O.cw2, row + O.cb2, nx, kNetWaves - nx);
-    }
+    // conv2's input gradient for channel c (waves 0-3) beside its weight gradient for the pairs (co, c)
+    net_conv_dx1(gs, L.p1, C2, P1, w2c, dp1, 0, 4);
+    net_conv_dw_rows(gs + L.p1.ld + 1, L.p1, p1c, L.p1, P1, C2, row + O.cw2 + c * 9, C1 * 9, c == 0 ? row + O.cb2 : nullptr,
+                     4, NW - 4);
     __syncthreads();
-    net_pool_bwd(dp1s, C1, P1, m1, gs, L.pz1, 0);   // dZ1 over dZ2's space
+    net_pool_bwd(dp1, 1, P1, m1, z1, L.pz1, 0);   // dZ1 of channel c
     __syncthreads();
-    net_conv_dw(gs, L.pz1, xs, L.px, 1, Hin, C1, row + O.cw1, row + O.cb1, 0, kNetWaves);
+    net_conv_dw_rows(z1, L.pz1, xs, L.px, Hin, 1, row + O.cw1 + c * 9, 9, row + O.cb1 + c, 0, NW);
 }
 
-size_t convnet_fused_lds_bytes(int Hin, int C1, int C2, int NC) {
-    return (size_t)net_layout(Hin, C1, C2, NC).total * sizeof(float);
+static size_t fwd_lds_bytes(int Hin, int C1) { return (size_t)fwd_layout(Hin, C1).total * sizeof(float); }
+static size_t bwd_lds_bytes(int Hin, int C1, int C2, int NC) {
+    return (size_t)bwd_layout(Hin, C1, C2, NC).total * sizeof(float);
 }
+
 bool convnet_fused_ok(int Hin, int C1, int C2, int NC) {
-    const long F = (long)C2 * (Hin / 4) * (Hin / 4);
-    return Hin % 4 == 0 && Hin > 0 && C1 > 0 && C2 > 0 && NC > 0 && NC <= kNetMaxNC && F <= kNetThreads &&
-           convnet_fused_lds_bytes(Hin, C1, C2, NC) <= 64 * 1024;
+    if (Hin % 4 || Hin <= 0 || C1 <= 0 || C2 <= 0 || NC <= 0 || NC > kNetMaxNC) return false;
+    const long P2 = Hin / 4, F = (long)C2 * P2 * P2;
+    const BwdLayout B = bwd_layout(Hin, C1, C2, NC);
+    const FwdLayout A = fwd_layout(Hin, C1);
+    return F <= kBwdThreads && kFwdGroupCh * P2 * P2 <= kFwdThreads && B.px.ps <= 2 * kBwdThreads &&
+           A.px.ps <= 3 * kFwdThreads && kFwdGroupCh * C1 * 9 <= kFwdThreads &&
+           net_groups(C2) * NC + NC + 1 <= kBwdThreads &&
+           B.p1.ps <= kBwdThreads && C2 * 9 <= kBwdThreads && fwd_lds_bytes(Hin, C1) <= 64 * 1024 &&
+           bwd_lds_bytes(Hin, C1, C2, NC) <= 64 * 1024;
+}
+long convnet_fused_ws_floats(int N, int Hin, int C1, int C2, int NC) { return net_ws(N, Hin, C1, C2, NC).total; }
+
+hipError_t convnet_fwd_fused(const float *x, const float *cw1, const float *cb1, const float *cw2, const float *cb2,
+                             const float *fw, int B, int Hin, int C1, int C2, int NC, float *ws, hipStream_t s) {
+    if (!convnet_fused_ok(Hin, C1, C2, NC) || B <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(convnet_fwd_kernel, dim3(B, net_groups(C2)), dim3(kFwdThreads), fwd_lds_bytes(Hin, C1), s, x,
+                       cw1, cb1, cw2, cb2, fw, Hin, C1, C2, NC, ws);
+    return hipGetLastError();
 }
 
-hipError_t convnet_step_fused(const float *x, const int32_t *lab, const float *cw1, const float *cb1, const float *cw2,
-                              const float *cb2, const float *fw, const float *fb, int B, int Hin, int C1, int C2, int NC,
-                              float a, float *rowloss, float *part, hipStream_t s) {
+hipError_t convnet_bwd_fused(const float *x, const int32_t *lab, const float *cw2, const float *fw, const float *fb, int B,
+                             int Hin, int C1, int C2, int NC, float a, const float *ws, float *rowloss, float *part,
+                             hipStream_t s) {
     if (!convnet_fused_ok(Hin, C1, C2, NC) || B <= 0) return hipErrorInvalidValue;
-    const NetPart O = net_part(Hin, C1, C2, NC);
-    hipLaunchKernelGGL(convnet_step_kernel, dim3(B), dim3(kNetThreads), convnet_fused_lds_bytes(Hin, C1, C2, NC), s, x,
-                       lab, cw1, cb1, cw2, cb2, fw, fb, Hin, C1, C2, NC, a, rowloss, part, O.total);
+    hipLaunchKernelGGL(convnet_bwd_kernel, dim3(B, C1), dim3(kBwdThreads), bwd_lds_bytes(Hin, C1, C2, NC), s, x, lab,
+                       cw2, fw, fb, Hin, C1, C2, NC, net_groups(C2), a, ws, rowloss, part, net_part(Hin, C1, C2, NC).total);
     return hipGetLastError();
 }
 

@@ -543,9 +543,9 @@ struct ChainTrainer : ah_trainer {
 struct ConvNetTrainer : ah_trainer {
     int N, Hin, C1, C2, NC, P1, P2, F;
     float *x, *cw1, *cb1, *cw2, *cb2, *fw, *fb, *H1, *Pl1, *H2, *Pl2, *lg, *dlg, *dP2, *dZ2, *dP1, *dZ1;
-    float *rowloss, *acc, *loss, *gcw1, *gcb1, *gcw2, *gcb2, *gfw, *gfb, *wpart1, *wpart2, *spart = nullptr;
+    float *rowloss, *acc, *loss, *gcw1, *gcb1, *gcw2, *gcb2, *gfw, *gfb, *wpart1, *wpart2, *spart = nullptr, *sws = nullptr;
     int32_t *lab;
-    bool fused = false;   // the one-workgroup-per-sample kernel (convnet.h) + the tail
+    bool fused = false;   // the sample-parallel forward and backward kernels (convnet.h) + the tail
     int init() {
         N = (int)dims[0]; Hin = (int)dims[1]; C1 = (int)dims[2]; C2 = (int)dims[3]; NC = (int)dims[4];
         if (N <= 0 || Hin <= 0 || Hin % 4 || C1 <= 0 || C2 <= 0 || NC <= 0) return set_error(AH_ERR_INVALID, "CONVNET: bad dims");
@@ -565,6 +565,7 @@ struct ConvNetTrainer : ah_trainer {
         rc |= alloc(&gcw2, (size_t)C2 * C1 * 9); rc |= alloc(&gcb2, C2); rc |= alloc(&gfw, (size_t)NC * F); rc |= alloc(&gfb, NC);
         fused = convnet_fused_ok(Hin, C1, C2, NC);
         if (fused) rc |= alloc(&spart, (size_t)N * net_part(Hin, C1, C2, NC).total);
+        if (fused) rc |= alloc(&sws, (size_t)convnet_fused_ws_floats(N, Hin, C1, C2, NC));
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * NC));
         return AH_OK;
@@ -593,7 +594,8 @@ struct ConvNetTrainer : ah_trainer {
         const bool sg = flags & AH_STEP_STORE_GRADS;
         const float a = (float)(-1.0 / (double)B);
         if (fused) {
-            LAUNCH("convnet", convnet_step_fused(x, lab, cw1, cb1, cw2, cb2, fw, fb, B, Hin, C1, C2, NC, a, rowloss, spart, s));
+            LAUNCH("convnet_fwd", convnet_fwd_fused(x, cw1, cb1, cw2, cb2, fw, B, Hin, C1, C2, NC, sws, s));
+            LAUNCH("convnet_bwd", convnet_bwd_fused(x, lab, cw2, fw, fb, B, Hin, C1, C2, NC, a, sws, rowloss, spart, s));
             const NetPart o = net_part(Hin, C1, C2, NC);
             TailArgs ta{};
             float *p[6] = {cw1, cb1, cw2, cb2, fw, fb}, *go[6] = {gcw1, gcb1, gcw2, gcb2, gfw, gfb};

@@ -131,16 +131,17 @@ def mlp_ce_kernels(B, D, H, C):
 
 
 def convnet_kernels(N=32, Hin=28, C1=8, C2=16, NC=10):
-    """The CONVNET trainer's launches (config 2) with their algorithmic work: the fused per-sample step
-    (direct-convolution and fc FLOPs, forward and backward; conv1 has no input gradient), then the tail,
-    which reads the N per-sample gradient rows and reads/writes each parameter and its gradient."""
+    """The CONVNET trainer's launches (config 2) with their algorithmic work: the forward and backward
+    kernels (direct-convolution and fc FLOPs; conv1 has no input gradient), then the tail, which reads
+    the N per-sample gradient rows and reads/writes each parameter and its gradient."""
     P1, P2 = Hin // 2, Hin // 4
     F = C2 * P2 * P2
     c1 = 2.0 * N * C1 * Hin * Hin * 9          # conv1: Ci = 1
     c2 = 2.0 * N * C2 * P1 * P1 * 9 * C1       # conv2
     fc = 2.0 * N * NC * F
     nparam = C1 * 10 + C2 * C1 * 9 + C2 + NC * F + NC
-    return [("convnet", "flop32", 2 * c1 + 3 * c2 + 3 * fc), ("tail", "bytes", 4.0 * N * nparam + 12.0 * nparam)]
+    return [("convnet_fwd", "flop32", c1 + c2 + fc), ("convnet_bwd", "flop32", c1 + 2 * c2 + 2 * fc),
+            ("tail", "bytes", 4.0 * N * nparam + 12.0 * nparam)]
 
 
 def kernel_table(t, batch, kernels, steps=10):
