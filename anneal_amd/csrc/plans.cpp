@@ -16,6 +16,7 @@
 #include "ah_internal.h"
 #include "conv.h"
 #include "convnet.h"
+#include "mlpce.h"
 #include "gemm.h"
 #include "rowops.h"
 
@@ -182,6 +183,7 @@ struct MlpCeTrainer : ah_trainer {
     int Bmax, D, H, C;
     float *x, *W1, *b1, *W2, *b2, *H1, *Z2, *dZ2, *dZ1, *rowloss, *acc, *loss, *gW1, *gb1, *gW2, *gb2;
     int32_t *lab;
+    bool fused = false;   // the three-kernel step of mlpce.h
     int init() {
         Bmax = (int)dims[0]; D = (int)dims[1]; H = (int)dims[2]; C = (int)dims[3];
         if (Bmax <= 0 || D <= 0 || H <= 0 || C <= 0) return set_error(AH_ERR_INVALID, "MLP_CE: bad dims");
@@ -192,6 +194,7 @@ struct MlpCeTrainer : ah_trainer {
         rc |= alloc(&dZ1, (size_t)Bmax * H); rc |= alloc(&rowloss, Bmax); rc |= alloc(&acc, H + C);
         rc |= alloc(&loss, 1); rc |= alloc(&gW1, (size_t)H * D); rc |= alloc(&gb1, H);
         rc |= alloc(&gW2, (size_t)C * H); rc |= alloc(&gb2, C);
+        fused = mlpce_fused_ok(Bmax, D, H, C);
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * (H + C)));
         return AH_OK;
@@ -216,6 +219,14 @@ struct MlpCeTrainer : ah_trainer {
         hipStream_t s = dev->stream;
         const bool sg = flags & AH_STEP_STORE_GRADS;
         const float a = (float)(-1.0 / (double)B);
+        if (fused) {
+            MlpSgd u{W1, b1, W2, b2, sg ? gW1 : nullptr, sg ? gb1 : nullptr, sg ? gW2 : nullptr, sg ? gb2 : nullptr,
+                     lr, a, loss};
+            LAUNCH("hidden", mlpce_hidden(x, W1, b1, B, D, H, H1, s));
+            LAUNCH("head", mlpce_head(lab, H1, W2, b2, B, H, C, a, dZ2, dZ1, rowloss, s));
+            LAUNCH("grad", mlpce_grad(x, H1, dZ2, dZ1, rowloss, B, D, H, C, u, s));
+            return AH_OK;
+        }
         float *db1 = acc, *db2 = acc + H;
         GemmDesc g1 = gdesc(GEMM_F32, EPI_BIAS_RELU, 0, 0, B, H, D, x, D, W1, D, H1, H);
         g1.bias = b1;

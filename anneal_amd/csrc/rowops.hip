@@ -381,6 +381,8 @@ __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
         if (i < total)
             while (k >= t.seg[s].n) { k -= t.seg[s].n; s++; }
         const TailSeg &g = t.seg[s];
+        // the parameter's old value is loaded with the gradient partials, not after their sum
+        const float pold = (q == 0 && i < total) ? g.p[k] : 0.0f;
         float a = 0.0f;
         if (i < total) {
             if (g.acc_rows > 0) {
@@ -416,7 +418,7 @@ __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
             for (int c = 0; c < kTailChunks; c++) sum += part[c][e];
             const float gv = g.scale * sum;
             if (g.gout) g.gout[k] = gv;
-            float w = g.p[k] - t.lr * gv;
+            float w = pold - t.lr * gv;
             asm volatile("" : "+v"(w));   // the f16 copy is f16 of the stored f32 value
             g.p[k] = w;
             if (g.p16) g.p16[k] = (half_t)w;

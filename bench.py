@@ -123,8 +123,13 @@ def cpu_baseline(cfg: int, inputs: dict):
 
 
 def mlp_ce_kernels(B, D, H, C):
-    """The MLP_CE trainer's launches (configs 1 and 4) with their algorithmic work."""
+    """The MLP_CE trainer's launches (configs 1 and 4) with their algorithmic work. Shapes up to
+    B = 64, D = 896, H = 128, C = 16 (config 1) take the three-kernel step (hidden layer; softmax-CE
+    and dH; weight gradients with SGD), larger ones the GEMM-based step."""
     f = lambda m, n, k: ("flop32", 2.0 * m * n * k)  # noqa: E731
+    if B <= 64 and D <= 896 and H <= 128 and C <= 16:
+        return [("hidden", *f(B, H, D)), ("head", "flop32", 2 * 2.0 * B * C * H),
+                ("grad", "flop32", 2.0 * B * H * D + 2.0 * B * C * H)]
     return [("fc1", *f(B, H, D)), ("fc2", *f(B, C, H)), ("softmax_ce", "bytes", 8.0 * B * C + 8.0 * B),
             ("db2", "bytes", 4.0 * B * C), ("dH1", *f(B, H, C)), ("dW2", *f(C, H, B)), ("dW1", *f(H, D, B)),
             ("tail", "bytes", 4.0 * B + 16.0 * (H + C))]
