@@ -29,4 +29,11 @@ hipError_t mlpce_head(const int32_t *lab, const float *Hin, const float *W2, con
 hipError_t mlpce_grad(const float *x, const float *Hin, const float *dz, const float *dH, const float *rowloss, int B,
                       int D, int H, int C, const MlpSgd &sgd, hipStream_t s);
 
+// Small batches (B <= 8) at wide layers (D % 4 == 0, H % 4 == 0, C <= 512; config 4 at N = 1 and 7):
+// part 0 the hidden layer into Hbuf, 1 the logits into Z, 2 softmax-CE (dz, rowloss) and dH, 3 every
+// weight gradient with SGD, the biases and the loss. Launched in that order on one stream.
+bool mlp_small_ok(int B, int D, int H, int C);
+hipError_t mlp_small_step(const float *x, const int32_t *lab, int B, int D, int H, int C, float a, float *Hbuf,
+                          float *Z, float *dz, float *dH, float *rowloss, const MlpSgd &S, hipStream_t s, int part);
+
 }  // namespace ah

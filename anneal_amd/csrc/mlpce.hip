@@ -206,6 +206,184 @@ __global__ __launch_bounds__(kMlpThreads) void mlpce_grad_kernel(const float *__
     }
 }
 
+// ── small batches at wide layers (config 4 at N <= 8) ──────────────────────
+// Four kernels instead of the GEMM step's eight: the two linear layers as dots over 16 lanes, the
+// hidden-layer gradient over column blocks of W2, and every weight gradient with its SGD update as
+// one streaming pass over W1 and W2.
+
+constexpr int kSmallB = 8, kSmallMaxC = 512;
+
+// out[n][j] = in[n] . W[j] + b[j] (ReLU, sign-tagged, when RELU): 8 samples x 8 rows per workgroup,
+// 16 lanes per output with 16-byte loads, 8 in flight per operand and lane. K % 4 == 0.
+template <bool RELU>
+__global__ __launch_bounds__(kMlpThreads) void mlp_lin_kernel(const float *__restrict__ in, const float *__restrict__ W,
+                                                              const float *__restrict__ b, int B, int K, int J,
+                                                              float *__restrict__ out) {
+    const int tid = threadIdx.x, o = tid / 16, ks = tid % 16;
+    const int n = blockIdx.x * 8 + o / 8, j = blockIdx.y * 8 + o % 8;
+    const bool live = n < B && j < J;
+    const float *ar = in + (long)(live ? n : 0) * K, *wr = W + (long)(live ? j : 0) * K;
+    float acc = 0.0f;
+    for (int k0 = 4 * ks; k0 < K; k0 += 4 * 16 * 8) {
+        floatx4 av[8], wv[8];
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const int k = k0 + 64 * m;
+            const bool ok = live && k < K;
+            av[m] = ok ? *(const floatx4 *)(ar + k) : (floatx4){};
+            wv[m] = ok ? *(const floatx4 *)(wr + k) : (floatx4){};
+        }
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) acc += av[m][u] * wv[m][u];
+    }
+    acc = mlp_row16(acc);
+    if (ks == 0 && live) {
+        const float z = acc + b[j];
+        out[(long)n * J + j] = RELU ? relu_tag(z) : z;
+    }
+}
+
+// Softmax-CE of every sample (each workgroup; workgroup 0 writes dz and rowloss), then dH for the 64
+// hidden units [64 * blockIdx.x, +64): wave w sums its share of the classes for every sample (all its
+// W2 loads in flight at once), the waves' sums are added in wave order, and the ReLU mask applied.
+__global__ __launch_bounds__(kMlpThreads) void mlp_small_dh_kernel(const int32_t *__restrict__ lab,
+                                                                   const float *__restrict__ Z,
+                                                                   const float *__restrict__ Hg,
+                                                                   const float *__restrict__ W2, int B, int H, int C,
+                                                                   float a, float *__restrict__ dz,
+                                                                   float *__restrict__ dH,
+                                                                   float *__restrict__ rowloss) {
+    constexpr int NW = kMlpThreads / 64, CW = kSmallMaxC / NW;   // classes per wave, at most
+    __shared__ float dzs[kSmallB * kSmallMaxC];
+    __shared__ float zr[NW * kSmallB * 64];   // the logits, then the per-wave sums
+    float *zs = zr;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, j = blockIdx.x * 64 + lane;
+    const int cw = (C + NW - 1) / NW, c0 = w * cw, c1 = min(C, c0 + cw);
+    float wv[CW];   // this lane's column of W2 over the wave's classes
+#pragma unroll
+    for (int q = 0; q < CW; q++) wv[q] = (c0 + q < c1 && j < H) ? W2[(long)(c0 + q) * H + j] : 0.0f;
+    for (int i = tid; i < B * C; i += kMlpThreads) zs[i] = Z[i];
+    __syncthreads();
+    for (int n = w; n < B; n += NW) {
+        const float r = softmax_ce_row(zs + n * C, lab[n], C, a, dzs + n * C, lane);
+        if (blockIdx.x == 0 && lane == 0) rowloss[n] = r;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0)
+        for (int i = tid; i < B * C; i += kMlpThreads) dz[i] = dzs[i];
+    float acc[kSmallB];
+#pragma unroll
+    for (int n = 0; n < kSmallB; n++) {
+        acc[n] = 0.0f;
+        if (n < B)
+#pragma unroll
+            for (int q = 0; q < CW; q++)
+                if (c0 + q < c1) acc[n] += dzs[n * C + c0 + q] * wv[q];
+    }
+#pragma unroll
+    for (int n = 0; n < kSmallB; n++) zr[(w * kSmallB + n) * 64 + lane] = acc[n];
+    __syncthreads();
+    if (tid < B * 64) {
+        const int n = tid / 64, jj = blockIdx.x * 64 + lane;
+        float g = 0.0f;
+        for (int q = 0; q < NW; q++) g += zr[(q * kSmallB + n) * 64 + lane];
+        if (jj < H) dH[(long)n * H + jj] = relu_dead(Hg[(long)n * H + jj]) ? 0.0f : g;
+    }
+}
+
+// dW1 = dH^T x and dW2 = dz^T H over the batch, with SGD, one float4 of W1 or W2 per thread; the last
+// workgroup takes b1, b2 and the loss.
+__global__ __launch_bounds__(256) void mlp_small_grad_kernel(const float *__restrict__ x, const float *__restrict__ Hg,
+                                                             const float *__restrict__ dz, const float *__restrict__ dH,
+                                                             const float *__restrict__ rowloss, int B, int D, int H,
+                                                             int C, MlpSgd S) {
+    const long n1 = (long)H * D / 4, n2 = (long)C * H / 4;
+    const long u = (long)blockIdx.x * 256 + threadIdx.x;
+    if (blockIdx.x == gridDim.x - 1) {   // biases and the loss
+        for (int j = threadIdx.x; j < H; j += 256) {
+            float g = 0.0f;
+            for (int n = 0; n < B; n++) g += dH[(long)n * H + j];
+            if (S.gb1) S.gb1[j] = g;
+            S.b1[j] = S.b1[j] - S.lr * g;
+        }
+        for (int c = threadIdx.x; c < C; c += 256) {
+            float g = 0.0f;
+            for (int n = 0; n < B; n++) g += dz[(long)n * C + c];
+            if (S.gb2) S.gb2[c] = g;
+            S.b2[c] = S.b2[c] - S.lr * g;
+        }
+        if (threadIdx.x < 64) {
+            float l = 0.0f;
+            for (int n = threadIdx.x; n < B; n += 64) l += rowloss[n];
+            l = wave_sum(l);
+            if (threadIdx.x == 0) S.loss[0] = l * S.loss_scale;
+        }
+        return;
+    }
+    float s[kSmallB];
+    floatx4 v[kSmallB];
+    float *Wp, *gp;
+    long e;
+    if (u < n1) {   // W1[j][i .. i+3]: dH[n][j] * x[n][i .. i+3]
+        e = 4 * u;
+        const int j = (int)(e / D), i = (int)(e % D);
+#pragma unroll
+        for (int n = 0; n < kSmallB; n++) {
+            s[n] = n < B ? dH[(long)n * H + j] : 0.0f;
+            v[n] = n < B ? *(const floatx4 *)(x + (long)n * D + i) : (floatx4){};
+        }
+        Wp = S.W1; gp = S.gW1;
+    } else if (u < n1 + n2) {   // W2[c][j .. j+3]: dz[n][c] * H[n][j .. j+3]
+        e = 4 * (u - n1);
+        const int c = (int)(e / H), j = (int)(e % H);
+#pragma unroll
+        for (int n = 0; n < kSmallB; n++) {
+            s[n] = n < B ? dz[(long)n * C + c] : 0.0f;
+            v[n] = n < B ? *(const floatx4 *)(Hg + (long)n * H + j) : (floatx4){};
+        }
+        Wp = S.W2; gp = S.gW2;
+    } else {
+        return;
+    }
+    const floatx4 wold = *(const floatx4 *)(Wp + e);
+    floatx4 g = {};
+#pragma unroll
+    for (int n = 0; n < kSmallB; n++) g += s[n] * v[n];
+    if (gp) *(floatx4 *)(gp + e) = g;
+    *(floatx4 *)(Wp + e) = wold - S.lr * g;
+}
+
+bool mlp_small_ok(int B, int D, int H, int C) {
+    return B > 0 && B <= kSmallB && D % 4 == 0 && H % 4 == 0 && C > 0 && C <= kSmallMaxC;
+}
+
+hipError_t mlp_small_step(const float *x, const int32_t *lab, int B, int D, int H, int C, float a, float *Hbuf,
+                          float *Z, float *dz, float *dH, float *rowloss, const MlpSgd &S, hipStream_t s, int part) {
+    if (!mlp_small_ok(B, D, H, C)) return hipErrorInvalidValue;
+    switch (part) {
+        case 0:
+            hipLaunchKernelGGL(mlp_lin_kernel<true>, dim3((B + 7) / 8, (H + 7) / 8), dim3(kMlpThreads), 0, s, x, S.W1,
+                               S.b1, B, D, H, Hbuf);
+            break;
+        case 1:
+            hipLaunchKernelGGL(mlp_lin_kernel<false>, dim3((B + 7) / 8, (C + 7) / 8), dim3(kMlpThreads), 0, s, Hbuf,
+                               S.W2, S.b2, B, H, C, Z);
+            break;
+        case 2:
+            hipLaunchKernelGGL(mlp_small_dh_kernel, dim3((H + 63) / 64), dim3(kMlpThreads), 0, s, lab, Z, Hbuf, S.W2, B,
+                               H, C, a, dz, dH, rowloss);
+            break;
+        default: {
+            const long n4 = ((long)H * D + (long)C * H) / 4;
+            hipLaunchKernelGGL(mlp_small_grad_kernel, dim3((unsigned)((n4 + 255) / 256) + 1), dim3(256), 0, s, x, Hbuf,
+                               dz, dH, rowloss, B, D, H, C, S);
+        }
+    }
+    return hipGetLastError();
+}
+
 bool mlpce_fused_ok(int B, int D, int H, int C) {
     return B > 0 && B <= kMlpMaxB && D > 0 && D <= kMlpMaxD && H > 0 && H <= kMlpMaxH && C > 0 && C <= kMlpMaxC;
 }

@@ -227,6 +227,15 @@ struct MlpCeTrainer : ah_trainer {
             LAUNCH("grad", mlpce_grad(x, H1, dZ2, dZ1, rowloss, B, D, H, C, u, s));
             return AH_OK;
         }
+        if (mlp_small_ok(B, D, H, C)) {
+            MlpSgd u{W1, b1, W2, b2, sg ? gW1 : nullptr, sg ? gb1 : nullptr, sg ? gW2 : nullptr, sg ? gb2 : nullptr,
+                     lr, a, loss};
+            LAUNCH("fc1", mlp_small_step(x, lab, B, D, H, C, a, H1, Z2, dZ2, dZ1, rowloss, u, s, 0));
+            LAUNCH("fc2", mlp_small_step(x, lab, B, D, H, C, a, H1, Z2, dZ2, dZ1, rowloss, u, s, 1));
+            LAUNCH("dH1", mlp_small_step(x, lab, B, D, H, C, a, H1, Z2, dZ2, dZ1, rowloss, u, s, 2));
+            LAUNCH("grad", mlp_small_step(x, lab, B, D, H, C, a, H1, Z2, dZ2, dZ1, rowloss, u, s, 3));
+            return AH_OK;
+        }
         float *db1 = acc, *db2 = acc + H;
         GemmDesc g1 = gdesc(GEMM_F32, EPI_BIAS_RELU, 0, 0, B, H, D, x, D, W1, D, H1, H);
         g1.bias = b1;
