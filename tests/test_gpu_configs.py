@@ -58,6 +58,53 @@ def test_config4_dynmlp_step_graph_replay(dev, N):
     check_mlp(run_mlp_ce(dev, p, N, 0.01, graph=True), p, 0.01)
 
 
+@pytest.mark.parametrize("shape", [(64, 37, 784, 128, 10), (64, 1, 97, 20, 3), (48, 48, 892, 128, 16)])
+def test_mlp_three_kernel_step_ragged(dev, shape):
+    """The three-kernel MLP step (B <= 64, D <= 896, H <= 128, C <= 16) at a batch below the trainer's
+    maximum, odd widths (D not a multiple of 4 takes the scalar loads) and the size limits."""
+    Bmax, B, D, H, C = shape
+    p = data.mlp_ce_inputs(B, D, H, C, seed=11)
+    t = Trainer(dev, L.TRAIN_MLP_CE, [Bmax, D, H, C], 0.01)
+    assert t.kernel_count(B) == 3
+    for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+        t.set(k, p[k])
+    t.step(B, store_grads=True)
+    out = {"loss": t.get("loss", 1)[0]}
+    for k, n in (("dW1", H * D), ("db1", H), ("dW2", C * H), ("db2", C), ("W1", H * D), ("b1", H),
+                 ("W2", C * H), ("b2", C)):
+        out[k] = t.get(k, n)
+    t.close()
+    check_mlp(out, p, 0.01)
+
+
+@pytest.mark.parametrize("N", [2, 8, 9])
+def test_config4_small_batch_paths(dev, N):
+    """Batches up to 8 take the four-kernel small-batch step, 9 the GEMM step; both against the oracle."""
+    p = data.mlp_ce_inputs(N, 512, 2048, 512, x_lo=-1.0, x_hi=1.0, seed=5)
+    t = Trainer(dev, L.TRAIN_MLP_CE, [4096, 512, 2048, 512], 0.01)
+    assert (t.kernel_count(N) == 4) == (N <= 8)
+    t.close()
+    check_mlp(run_mlp_ce(dev, p, N, 0.01), p, 0.01)
+
+
+def test_convnet_fused_batch_below_max(dev):
+    """The sample-parallel conv-net kernels at a batch below the trainer's maximum."""
+    p = data.convnet_inputs(N=5, seed=9)
+    lr = 0.01
+    wl, g, new = O.convnet_step(p, lr)
+    t = Trainer(dev, L.TRAIN_CONVNET, [32, 28, 8, 16, 10], lr)
+    assert t.kernel_count(5) == 3
+    for k in ("x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+        t.set(k, p[k])
+    t.step(5, store_grads=True)
+    assert abs(t.get("loss", 1)[0] - wl) < 1e-4 * max(1, abs(wl))
+    for k in ("dcw1", "dcb1", "dcw2", "dcb2", "dfw", "dfb"):
+        assert O.relerr(t.get(k, g[k].size), g[k].ravel()) < 1e-4, k
+    for k in ("cw1", "cb1", "cw2", "cb2", "fw", "fb"):
+        assert check_update(t.get(k, new[k].size), p[k], new[k], 1e-4), k
+    t.close()
+
+
 def test_config4_n4096_vs_f64_closed_form(dev):
     """Config 4 at N = 4096 (graph replay) against the float64 closed form of the oracle's step, which
     test_mlp_ce_f64_closed_form_matches_c_oracle pins to the C oracle (the C oracle alone needs about
