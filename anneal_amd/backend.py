@@ -174,6 +174,16 @@ class Trainer:
         L.check(self.dev.lib.ah_trainer_kernel_count(self.h, int(batch), C.byref(c)))
         return c.value
 
+    def kernel_names(self, batch: int) -> list:
+        """Names of the step's launches in order (ah_trainer_kernel_count, then ah_trainer_kernel_name)."""
+        n = self.kernel_count(batch)
+        buf = C.create_string_buffer(64)
+        out = []
+        for i in range(n):
+            L.check(self.dev.lib.ah_trainer_kernel_name(self.h, i, buf, 64))
+            out.append(buf.value.decode())
+        return out
+
     def close(self) -> None:
         if self.h:
             self.dev.lib.ah_trainer_destroy(self.h)

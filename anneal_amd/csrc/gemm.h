@@ -71,6 +71,22 @@ struct GemmDesc {
     float lr;
 };
 
+// Two independent f16 contractions in one launch (gemm16_pair.hip): d0's tiles split over K into
+// nsplit workgroups each, then d1's tiles (items1 of them; none for a split d0 alone).
+struct G16PairArgs {
+    GemmDesc d0, d1;
+    int nsplit;     // K splits of each d0 tile
+    int items0;     // d0 workgroups: tiles x nsplit
+    int *count;     // one arrival counter per d0 tile, zero before and after a launch
+    float *part;    // tiles x nsplit partial tiles of BM*BM floats
+};
+// Variants a paired launch can use (256x256 tiles, one k-group).
+constexpr int kG16PairVariants[] = {27, 30};
+// Launches the pair with `variant` when the shapes, layouts and epilogues admit it (every tile whole,
+// vector epilogues, K/nsplit whole stages); returns false, launching nothing, otherwise.
+bool gemm16_pair_try_launch(const GemmDesc &d0, int nsplit, const GemmDesc *d1, int variant, int *count,
+                            float *part, long part_floats, hipStream_t s, hipError_t *err);
+
 hipError_t gemm_launch(const GemmDesc &d, hipStream_t s);
 bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err);
 

@@ -82,4 +82,47 @@ bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
     return true;
 }
 
+hipError_t gemm16_pair_variant_27(const G16PairArgs &p, int items1, bool *supported, hipStream_t s);
+hipError_t gemm16_pair_variant_30(const G16PairArgs &p, int items1, bool *supported, hipStream_t s);
+
+namespace {
+// The vector (LDS-staged) epilogue's conditions with every tile whole.
+bool pair_operand_ok(const GemmDesc &d, int bm) {
+    using namespace g16;
+    if (d.dtype != GEMM_F16 || d.M % bm || d.N % bm || d.K % 64 || d.ldc % 4 || d.ldaux % 4) return false;
+    const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
+                        (uintptr_t)d.W16 | (uintptr_t)d.gout;
+    if (a & 15) return false;
+    return (d.ta ? operand_ok<1>(d.A, d.lda, d.M) : operand_ok<0>(d.A, d.lda, d.M)) &&
+           (d.tb ? operand_ok<1>(d.B, d.ldb, d.N) : operand_ok<0>(d.B, d.ldb, d.N));
+}
+}  // namespace
+
+bool gemm16_pair_try_launch(const GemmDesc &d0, int nsplit, const GemmDesc *d1, int variant, int *count,
+                            float *part, long part_floats, hipStream_t s, hipError_t *err) {
+    using namespace g16;
+    constexpr int BM = 256;
+    if (variant != 27 && variant != 30) return false;
+    static_assert(Var<27>::BM == BM && Var<30>::BM == BM && Var<27>::KG == 1 && Var<30>::KG == 1, "pair variants");
+    if (nsplit < 1 || nsplit > 8 || d0.K % (64 * nsplit)) return false;
+    if (!pair_operand_ok(d0, BM) || (d1 && !pair_operand_ok(*d1, BM))) return false;
+    const long tiles0 = (long)(d0.M / BM) * (d0.N / BM);
+    if (nsplit > 1 && (!count || !part || tiles0 * nsplit * BM * BM > part_floats)) return false;
+    G16PairArgs p;
+    p.d0 = d0;
+    if (d1) p.d1 = *d1;
+    else p.d1 = d0;
+    p.nsplit = nsplit;
+    p.items0 = (int)(tiles0 * nsplit);
+    p.count = count;
+    p.part = part;
+    const int items1 = d1 ? (d1->M / BM) * (d1->N / BM) : 0;
+    bool supported = false;
+    hipError_t e = variant == 27 ? gemm16_pair_variant_27(p, items1, &supported, s)
+                                 : gemm16_pair_variant_30(p, items1, &supported, s);
+    if (!supported) return false;
+    *err = e;
+    return true;
+}
+
 }  // namespace ah

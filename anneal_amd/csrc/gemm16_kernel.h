@@ -179,33 +179,53 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
 // contracts the g-th half of K through its own LDS stages; at the end the groups exchange halves of
 // their accumulators through LDS, and each adds and finishes one half of the tile. Two waves then
 // share each SIMD on tiles whose accumulators leave room for only one wave set (the 128x128 tile).
-template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG>
-__global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d) {
-    constexpr int NW = WVM * WVN;
-    constexpr int WM = BM / WVM, WN = BN / WVN, FM = WM / 32, FN = WN / 32;
-    constexpr int ABYTES = BM * BK * 2, BBYTES = BN * BK * 2, STAGE = ABYTES + BBYTES;
-    constexpr int KS = BK / 16;                                           // MFMA k-steps per stage
-    constexpr int PERSTAGE = Fetch<BM, TA, BK, NW>::PER + Fetch<BN, TB, BK, NW>::PER;
-    constexpr int SMEM0 = (NS * STAGE > NW * WM * 256) ? NS * STAGE : NW * WM * 256;
-    constexpr int SMEMG = FETCH == 3 ? SMEM0 + NW * 256 : SMEM0;      // + per-wave prefetch junk slots
-    constexpr int SMEMR = KG > 1 ? BM * BN * 4 : 0;                   // k-group reduction buffer
-    constexpr int SMEM = KG * SMEMG > SMEMR ? KG * SMEMG : SMEMR;
-    static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
-    static_assert(!XB || FETCH >= 2, "cross-barrier prefetch needs the fetches grouped at the barrier");
-    static_assert(FETCH < 5 || XB, "fetch modes 5-7 interleave the fetches with the k-step after the barrier (XB)");
-    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+// LDS bytes of a variant's tile program (operand stages, epilogue staging, k-group reduction).
+template <int BM, int BN, int BK, int NS, int WVM, int WVN, int FETCH, int KG>
+struct G16Smem {
+    static constexpr int NW = WVM * WVN, WM = BM / WVM;
+    static constexpr int STAGE = BM * BK * 2 + BN * BK * 2;
+    static constexpr int SMEM0 = (NS * STAGE > NW * WM * 256) ? NS * STAGE : NW * WM * 256;
+    static constexpr int SMEMG = FETCH == 3 ? SMEM0 + NW * 256 : SMEM0;   // + per-wave prefetch junk slots
+    static constexpr int SMEMR = KG > 1 ? BM * BN * 4 : 0;                // k-group reduction buffer
+    static constexpr int SMEM = KG * SMEMG > SMEMR ? KG * SMEMG : SMEMR;
+};
 
-    const int tiles_n = (d.N + BN - 1) / BN;
-    const int tiles_m = (d.M + BM - 1) / BM;
-    const int ntiles = tiles_m * tiles_n;
-    int L = blockIdx.x;
-    if ((ntiles & 7) == 0) L = (L & 7) * (ntiles >> 3) + (L >> 3);   // contiguous tile runs per XCD
+// Hook between a tile's main loop and its epilogue (single-k-group variants): run() may replace the
+// accumulators (e.g. with the sum of a K split's partials) and returns false when this workgroup is
+// not to run the epilogue. G16NoFold is the plain tile.
+struct G16NoFold {
+    template <int FM, int FN, int NT>
+    __device__ __forceinline__ bool run(floatx16 (&)[FM][FN], int) const { return true; }
+};
+
+// Tile origin of tile index L of a tiles_m x tiles_n grid: tile rows in groups of 4, walked
+// column-major within a group, so that concurrent tiles share operand panels in L2.
+__device__ __forceinline__ void g16_tile_origin(int L, int tiles_m, int tiles_n, int BM, int BN, int &m0, int &n0) {
     constexpr int G = 4;
     const int group = L / (G * tiles_n);
     const int gm0 = group * G;
     const int gsz = min(G, tiles_m - gm0);
     const int rem = L - group * G * tiles_n;
-    const int m0 = (gm0 + rem % gsz) * BM, n0 = (rem / gsz) * BN;
+    m0 = (gm0 + rem % gsz) * BM;
+    n0 = (rem / gsz) * BN;
+}
+
+// One output tile at (m0, n0) over k in [kbase, kbase + klen), then fold.run (single k-group) and
+// the epilogue. smem holds G16Smem<...>::SMEM bytes.
+template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG,
+          class Fold>
+__device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, int n0, long kbase, int klen,
+                                         const Fold &fold) {
+    using SM = G16Smem<BM, BN, BK, NS, WVM, WVN, FETCH, KG>;
+    constexpr int NW = WVM * WVN;
+    constexpr int WM = BM / WVM, WN = BN / WVN, FM = WM / 32, FN = WN / 32;
+    constexpr int ABYTES = BM * BK * 2, STAGE = SM::STAGE;
+    constexpr int KS = BK / 16;                                           // MFMA k-steps per stage
+    constexpr int PERSTAGE = Fetch<BM, TA, BK, NW>::PER + Fetch<BN, TB, BK, NW>::PER;
+    constexpr int SMEM0 = SM::SMEM0, SMEMG = SM::SMEMG;
+    static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
+    static_assert(!XB || FETCH >= 2, "cross-barrier prefetch needs the fetches grouped at the barrier");
+    static_assert(FETCH < 5 || XB, "fetch modes 5-7 interleave the fetches with the k-step after the barrier (XB)");
 
     const int lane = threadIdx.x & 63;
     const int kg = KG > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) / NW : 0;   // k-group
@@ -221,9 +241,9 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     fa.init(d.lda, m0, d.M, wave, lane);
     fb.init(d.ldb, n0, d.N, wave, lane);
     const char *Ab = (const char *)d.A, *Bb = (const char *)d.B;
-    const int nk = d.K / BK / KG;
-    if constexpr (KG > 1) {   // this group's half of K starts at kg * nk * BK
-        const long k0 = (long)kg * nk * BK;
+    const int nk = klen / BK / KG;
+    {   // this group's part of K starts at kbase + kg * nk * BK
+        const long k0 = kbase + (long)kg * nk * BK;
         Ab += TA == 0 ? k0 * 2 : k0 * d.lda * 2;
         Bb += TB == 0 ? k0 * 2 : k0 * d.ldb * 2;
     }
@@ -405,6 +425,9 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // drain the tail re-fetches before LDS reuse
 
     const int mb = m0 + wm0, nb = n0 + wn0;
+    if constexpr (KG == 1) {
+        if (!fold.template run<FM, FN, 64 * NW>(acc, tid)) return;
+    }
     if constexpr (KG > 1) {
         // The two k-groups split the finish: group g owns 32-row block g of each wave tile (which has
         // two). Each group hands the other group's block over through LDS (element e of lane l of
@@ -446,6 +469,19 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     } else {
         epilogue_tile<EPI, half_t, FM, FN>(d, acc, mb, nb, lane);
     }
+}
+
+template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG>
+__global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d) {
+    __shared__ __attribute__((aligned(1024))) char smem[G16Smem<BM, BN, BK, NS, WVM, WVN, FETCH, KG>::SMEM];
+    const int tiles_n = (d.N + BN - 1) / BN;
+    const int tiles_m = (d.M + BM - 1) / BM;
+    const int ntiles = tiles_m * tiles_n;
+    int L = blockIdx.x;
+    if ((ntiles & 7) == 0) L = (L & 7) * (ntiles >> 3) + (L >> 3);   // contiguous tile runs per XCD
+    int m0, n0;
+    g16_tile_origin(L, tiles_m, tiles_n, BM, BN, m0, n0);
+    g16_tile<BM, BN, TA, TB, EPI, VEPI, BK, NS, WVM, WVN, FETCH, XB, KG>(d, smem, m0, n0, 0, d.K, G16NoFold{});
 }
 
 template <int T>

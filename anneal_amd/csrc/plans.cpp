@@ -33,6 +33,8 @@ struct ah_trainer {
     std::vector<hipEvent_t> ev_a, ev_b;
     size_t n_probe = 0;
     std::map<int64_t, ah_graph *> graphs;
+    bool record_names = false;
+    std::vector<std::string> names;   // launch names of the last ah_trainer_kernel_count
 
     virtual ~ah_trainer() {
         if (dev) hipStreamSynchronize(dev->stream);
@@ -72,6 +74,7 @@ struct ah_trainer {
             }
             AH_HIP(hipEventRecord(ev_a[n_probe], dev->stream));
         }
+        if (record_names) names.push_back(what);
         hipError_t e = f();
         if (e != hipSuccess) return set_error(AH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
         if (probe) {
@@ -272,6 +275,14 @@ struct Mlp3Trainer : ah_trainer {
     int B, D0, D1, D2, D3;
     half_t *X, *T, *W1h, *W2h, *W3h, *b1h, *b2h, *b3h, *H1, *H2, *Dd, *dZ2, *dZ1;
     float *W1, *W2, *W3, *b1, *b2, *b3, *acc, *loss, *lsum, *gW1, *gW2, *gW3, *gb1, *gb2, *gb3;
+    // Paired launches (gemm16_pair.hip): pair 0 runs dW3 split over K beside dH1, pair 1 dW1 split
+    // over K beside dW2. pair_v[p] is the variant of pair p (0: the two contractions launch apart),
+    // chosen by timing whole steps at creation.
+    static constexpr int kPairSplit = 4;
+    int pair_v[2] = {0, 0};
+    int *pair_count = nullptr;   // split-K arrival counters (zero between launches)
+    float *pair_part = nullptr;  // split-K partial tiles
+    long pair_part_floats = 0;
     int init() {
         B = (int)dims[0]; D0 = (int)dims[1]; D1 = (int)dims[2]; D2 = (int)dims[3]; D3 = (int)dims[4];
         if (B <= 0 || D0 <= 0 || D1 <= 0 || D2 <= 0 || D3 <= 0) return set_error(AH_ERR_INVALID, "MLP3: bad dims");
@@ -287,8 +298,16 @@ struct Mlp3Trainer : ah_trainer {
         rc |= alloc(&acc, acc_floats()); rc |= alloc(&loss, 1); rc |= alloc(&lsum, 1);
         rc |= alloc(&gW1, (size_t)D1 * D0); rc |= alloc(&gW2, (size_t)D2 * D1); rc |= alloc(&gW3, (size_t)D3 * D2);
         rc |= alloc(&gb1, D1); rc |= alloc(&gb2, D2); rc |= alloc(&gb3, D3);
+        // the split contractions are dW3 [D3 x D2] and dW1 [D1 x D0], in whole 256x256 tiles
+        const long split_tiles = std::max((long)(D3 / 256) * (D2 / 256), (long)(D1 / 256) * (D0 / 256));
+        if (split_tiles > 0) {
+            pair_part_floats = split_tiles * kPairSplit * 65536;
+            rc |= alloc(&pair_count, split_tiles);
+            rc |= alloc(&pair_part, pair_part_floats);
+        }
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * acc_floats()));
+        if (pair_count) AH_HIP(hipMemset(pair_count, 0, sizeof(int) * split_tiles));
         return tune();
     }
     // Bias-gradient and loss accumulators as deterministic per-wave partials (GemmDesc::colsum_ld,
@@ -416,6 +435,7 @@ struct Mlp3Trainer : ah_trainer {
         hipFree(s16);
         hipFree(s32);
         if (rc == AH_OK) rc = refine(fresh);
+        if (rc == AH_OK) rc = choose_pairs();
         if (rc == AH_OK) rc = clear_state();
         if (rc == AH_OK && cache && *cache) rc = ah_gemm_tune_cache(dev, cache, 1);
         return rc;
@@ -485,6 +505,75 @@ struct Mlp3Trainer : ah_trainer {
         launch_idx = 0;
         return rc;
     }
+    // Paired launches: for each pair, whole steps are timed with the two contractions launched apart
+    // and paired with each pair variant (interleaved, three rounds, the best mean of 8 steps each), on
+    // hash-filled parameters and data; the fastest is kept. The choice is cached under the pair's key
+    // beside the variant choices.
+    std::string pair_key(int q) const {
+        const GemmDesc a = gemm(q == 0 ? 4 : 7, false), b = gemm(q == 0 ? 5 : 6, false);
+        return "pair" + std::to_string(kPairSplit) + "/" + tune_key(a) + "/" + tune_key(b);
+    }
+    bool pair_admitted(int q) const {
+        if (!pair_count) return false;
+        const GemmDesc a = gemm(q == 0 ? 4 : 7, false), b = gemm(q == 0 ? 5 : 6, false);
+        auto whole = [](const GemmDesc &g) { return g.M % 256 == 0 && g.N % 256 == 0 && g.K % 256 == 0; };
+        return whole(a) && whole(b) && a.K % (64 * kPairSplit) == 0 &&
+               (long)(a.M / 256) * (a.N / 256) * kPairSplit * 65536 <= pair_part_floats;
+    }
+    int choose_pairs() {
+        // AH_PAIR_VARIANT fixes the choice (0: apart, 27 or 30: paired) without timing or caching it
+        const char *force = getenv("AH_PAIR_VARIANT");
+        if (force && *force) {
+            const int v = atoi(force);
+            if (v != 0 && v != 27 && v != 30) return set_error(AH_ERR_INVALID, "AH_PAIR_VARIANT must be 0, 27 or 30");
+            for (int q = 0; q < 2; q++) pair_v[q] = pair_admitted(q) ? v : 0;
+            return AH_OK;
+        }
+        bool todo[2];
+        for (int q = 0; q < 2; q++) {
+            auto it = dev->gemm_variant.find(pair_key(q));
+            todo[q] = pair_admitted(q) && it == dev->gemm_variant.end();
+            pair_v[q] = pair_admitted(q) && it != dev->gemm_variant.end() ? it->second : 0;
+        }
+        if (!todo[0] && !todo[1]) return AH_OK;
+        hipStream_t s = dev->stream;
+        const float x_amp = 1.7320508f;
+        AH_HIP(fill_hash(nullptr, X, (long)B * D0, 1u, x_amp, s));
+        AH_HIP(fill_hash(nullptr, T, (long)B * D3, 2u, x_amp, s));
+        AH_HIP(fill_hash(W1, W1h, (long)D1 * D0, 3u, x_amp / sqrtf((float)D0), s));
+        AH_HIP(fill_hash(W2, W2h, (long)D2 * D1, 4u, x_amp / sqrtf((float)D1), s));
+        AH_HIP(fill_hash(W3, W3h, (long)D3 * D2, 5u, x_amp / sqrtf((float)D2), s));
+        hipEvent_t e0, e1;
+        AH_HIP(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence));
+        AH_HIP(hipEventCreateWithFlags(&e1, hipEventDisableSystemFence));
+        int rc = AH_OK;
+        const int opts[3] = {0, 27, 30};
+        for (int q = 0; q < 2 && rc == AH_OK; q++) {
+            if (!todo[q]) continue;
+            double best[3] = {1e30, 1e30, 1e30};
+            for (int round = 0; round < 3 && rc == AH_OK; round++)
+                for (int o = 0; o < 3 && rc == AH_OK; o++) {
+                    pair_v[q] = opts[o];
+                    for (int k = 0; k < 2 && rc == AH_OK; k++) { launch_idx = 0; rc = enqueue(B, 0); }
+                    if (rc == AH_OK && hipEventRecord(e0, s) != hipSuccess) rc = set_error(AH_ERR_HIP, "MLP3: pair timing");
+                    for (int k = 0; k < 8 && rc == AH_OK; k++) { launch_idx = 0; rc = enqueue(B, 0); }
+                    float ms = 0.0f;
+                    if (rc == AH_OK && (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                                        hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+                        rc = set_error(AH_ERR_HIP, "MLP3: pair timing");
+                    if (rc == AH_OK) best[o] = std::min(best[o], (double)ms);
+                }
+            int bo = 0;
+            for (int o = 1; o < 3; o++)
+                if (best[o] < best[bo]) bo = o;
+            pair_v[q] = opts[bo];
+            dev->gemm_variant[pair_key(q)] = opts[bo];
+        }
+        launch_idx = 0;
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+        return rc;
+    }
     // Parameters, data, loss and accumulators all zero (the state create returns, tuned or not).
     int clear_state() {
         hipStream_t s = dev->stream;
@@ -510,7 +599,26 @@ struct Mlp3Trainer : ah_trainer {
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
         static const char *names[kGemms] = {"fc1", "fc2", "fc3_mse", "dH2", "dW3", "dH1", "dW2", "dW1"};
-        for (int i = 0; i < kGemms; i++) LAUNCH(names[i], gemm_run(dev, gemm(i, sg), s));
+        for (int i = 0; i < 4; i++) LAUNCH(names[i], gemm_run(dev, gemm(i, sg), s));
+        // dW3 beside dH1, then dW1 beside dW2 (each pair reads only finished inputs and writes
+        // disjoint outputs)
+        static const int pairs[2][2] = {{4, 5}, {7, 6}};
+        for (int q = 0; q < 2; q++) {
+            const int a = pairs[q][0], b = pairs[q][1];
+            if (pair_v[q]) {
+                const GemmDesc ga = gemm(a, sg), gb = gemm(b, sg);
+                hipError_t perr = hipSuccess;
+                LAUNCH(q == 0 ? "dW3+dH1" : "dW1+dW2",
+                       gemm16_pair_try_launch(ga, kPairSplit, &gb, pair_v[q], pair_count, pair_part, pair_part_floats,
+                                              s, &perr) ? perr : hipErrorInvalidValue);
+            } else if (q == 0) {
+                LAUNCH(names[a], gemm_run(dev, gemm(a, sg), s));
+                LAUNCH(names[b], gemm_run(dev, gemm(b, sg), s));
+            } else {   // the order of the unpaired step: dW2, then dW1
+                LAUNCH(names[b], gemm_run(dev, gemm(b, sg), s));
+                LAUNCH(names[a], gemm_run(dev, gemm(a, sg), s));
+            }
+        }
         TailArgs ta{};
         const int R = rblocks();
         ta.seg[0] = {b3, b3h, db3p(), sg ? gb3 : nullptr, D3, bs, R, D3};
@@ -534,7 +642,9 @@ struct ChainTrainer : ah_trainer {
         int rc = 0;
         rc |= alloc(&X, (size_t)R * Cc); rc |= alloc(&g, Cc); rc |= alloc(&dX, (size_t)R * Cc);
         rc |= alloc(&dg, Cc); rc |= alloc(&work, chain_workspace_floats(R, Cc)); rc |= alloc(&loss, 1);
-        return rc ? AH_ERR_HIP : AH_OK;
+        if (rc) return AH_ERR_HIP;
+        AH_HIP(hipMemset(work, 0, sizeof(float) * chain_workspace_floats(R, Cc)));   // the arrival counter
+        return AH_OK;
     }
     int max_batch() const override { return R; }
     int set(int slot, const void *h, int64_t n) override {
@@ -550,6 +660,10 @@ struct ChainTrainer : ah_trainer {
         return set_error(AH_ERR_INVALID, "CHAIN: bad get slot %d / size", slot);
     }
     int enqueue(int64_t, int) override {
+        if (chain_resident_fits(R, Cc)) {   // each column strip held on chip: one pass over HBM
+            LAUNCH("chain_resident", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream, -1));
+            return AH_OK;
+        }
         LAUNCH("chain_stats", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream, 0));
         LAUNCH("chain_finalize", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream, 1));
         LAUNCH("chain_grad", chain_step(X, g, R, Cc, work, dX, dg, loss, dev->stream, 2));
@@ -749,7 +863,10 @@ int ah_trainer_kernel_count(ah_trainer *t, int64_t batch, int32_t *count) {
     int rc = ah_graph_begin(t->dev);
     if (rc) return rc;
     t->launch_idx = 0;
+    t->names.clear();
+    t->record_names = true;
     int rc2 = t->enqueue(batch, 0);
+    t->record_names = false;
     ah_graph *g = nullptr;
     rc = ah_graph_end(t->dev, &g);
     ah_graph_destroy(g);
@@ -757,6 +874,15 @@ int ah_trainer_kernel_count(ah_trainer *t, int64_t batch, int32_t *count) {
     if (rc2) return rc2;
     if (rc) return rc;
     *count = t->launch_idx;
+    return AH_OK;
+}
+
+int ah_trainer_kernel_name(ah_trainer *t, int32_t index, char *buf, int32_t cap) {
+    if (!t || !buf || cap <= 0) return set_error(AH_ERR_INVALID, "ah_trainer_kernel_name: null argument");
+    if (index < 0 || index >= (int32_t)t->names.size())
+        return set_error(AH_ERR_INVALID, "ah_trainer_kernel_name: index %d outside the %d launches counted", (int)index,
+                         (int)t->names.size());
+    snprintf(buf, (size_t)cap, "%s", t->names[index].c_str());
     return AH_OK;
 }
 
@@ -810,7 +936,9 @@ int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save) {
         }
         char key[128];
         int v = 0;
-        if (sscanf(line, "%127s %d", key, &v) != 2 || v < 1 || v > kGemm16Variants) {
+        const bool pair = sscanf(line, "%127s %d", key, &v) == 2 && strncmp(key, "pair", 4) == 0;
+        const bool ok = pair ? (v == 0 || v == 27 || v == 30) : v >= 1 && v <= kGemm16Variants;
+        if (sscanf(line, "%127s %d", key, &v) != 2 || !ok) {
             rc = set_error(AH_ERR_INVALID, "gemm tune cache %s: bad line %d", path, lineno);
             break;
         }
@@ -858,7 +986,8 @@ int ah_chain_step(ah_device *dev, const float *X, const float *g, int32_t R, int
         return set_error(AH_ERR_INVALID, "ah_chain_step: bad argument (Cc must be a multiple of 4)");
     float *w = nullptr;
     AH_HIP(hipMalloc(&w, (size_t)chain_workspace_floats(R, Cc) * 4));
-    hipError_t e = chain_step(X, g, R, Cc, w, dX, dg, loss, dev->stream);
+    hipError_t e = hipMemsetAsync(w, 0, 256, dev->stream);   // the resident path's arrival counter
+    if (e == hipSuccess) e = chain_step(X, g, R, Cc, w, dX, dg, loss, dev->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
     hipFree(w);
     if (e != hipSuccess) return fail_hip(e, "ah_chain_step");

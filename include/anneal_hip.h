@@ -303,6 +303,10 @@ int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags);
 int ah_trainer_probe(ah_trainer *t, int32_t kernel_index);
 int ah_trainer_probe_read(ah_trainer *t, double *total_ms, int64_t *count);
 int ah_trainer_kernel_count(ah_trainer *t, int64_t batch, int32_t *count);
+/* Name of the index-th launch of a step, as counted by the last ah_trainer_kernel_count (NUL-terminated,
+ * truncated to cap bytes). The reference's Benchmark reports per-kernel results by kernel
+ * (backend/webgpu/benchmark.go); this names the trainer's launches for the same purpose. */
+int ah_trainer_kernel_name(ah_trainer *t, int32_t index, char *buf, int32_t cap);
 
 /* ── Checkpoint formats (host side; no device needed) ─────────────────────────
  * Readers for safetensors (tensor/safetensors/safetensors.go:150-434 Load / LoadTensors), NumPy .npy and

@@ -251,6 +251,49 @@ def test_config3_steps_bit_repeatable(dev):
         np.testing.assert_array_equal(runs[0][k], runs[1][k], err_msg=k)
 
 
+@pytest.mark.parametrize("variant", [27, 30])
+def test_config3_paired_launches(dev, monkeypatch, variant):
+    """dW3 split over K beside dH1, and dW1 split over K beside dW2, each pair one launch: the step
+    matches the oracle at the f16 bar, agrees with the unpaired step to f32 summation order (the K
+    splits are added in split order), and repeats bit for bit."""
+    B, D0, D1, D2, D3 = 1024, 256, 512, 512, 256
+    p = data.mlp3_inputs(B, D0, D1, D2, D3)
+    q = dict(p)
+    q["x"], q["t"] = data.f16_quantize(p["x"]), data.f16_quantize(p["t"])
+    lr = 1e-3
+    keys = ("dW1", "db1", "dW2", "db2", "dW3", "db3", "W1", "b1", "W2", "b2", "W3", "b3")
+
+    def run(v, repeat=1):
+        monkeypatch.setenv("AH_PAIR_VARIANT", str(v))
+        t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], lr)
+        names = t.kernel_names(B)
+        outs = []
+        for _ in range(repeat):
+            for k in ("x", "t", "W1", "b1", "W2", "b2", "W3", "b3"):
+                t.set(k, p[k])
+            t.step(B, store_grads=True)
+            o = {k: t.get(k, p[k.lstrip("d")].size if k.startswith("d") else p[k].size) for k in keys}
+            o["loss"] = t.get("loss", 1)[0]
+            outs.append(o)
+        t.close()
+        return names, outs
+
+    names, paired = run(variant, repeat=2)
+    assert "dW3+dH1" in names and "dW1+dW2" in names, names
+    names0, (apart,) = run(0)
+    assert "dW3" in names0 and "dW1+dW2" not in names0, names0
+    for k in keys:
+        np.testing.assert_array_equal(paired[0][k].view(np.uint32), paired[1][k].view(np.uint32), err_msg=k)
+    wl, g, new = O.mlp3_step(q, lr)
+    got = paired[0]
+    assert (np.isinf(got["loss"]) and np.isinf(wl)) or abs(got["loss"] - wl) < 2e-2 * abs(wl)
+    for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3"):
+        assert O.relerr(got[k], g[k].ravel()) < 2e-2, k
+        assert O.relerr(got[k], apart[k]) < 1e-5, k
+    for k in ("W1", "b1", "W2", "b2", "W3", "b3"):
+        assert check_update(got[k], p[k], new[k], 2e-2), k
+
+
 def test_config3_full_size_vs_numpy_restatement(dev):
     """Full config-3 shape (4096x1024 -> 4096 -> 4096 -> 1024): one step vs the blocked numpy
     restatement of the oracle (pinned to the C oracle on CPU). The f16 loss accumulator overflows at
