@@ -316,6 +316,236 @@ __global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, 
     }
 }
 
+// ── config 5 in one pass over HBM: strips of X held on chip ─────────────────────
+// Every softmax / RMS row of the chain is one column of X, and dg, the loss terms and dX of a column
+// need only that column. So one workgroup per CU takes a strip of 16 columns x R rows (R = 8192:
+// 512 KiB), keeps all of it on chip (kResRegs float4 per thread in VGPRs, kResLds in LDS through
+// LDS-DMA), and runs the whole chain on it: the exact column max, then sum e, sum e^2 and the tie
+// count against that max (no rescaling), the per-column scalars of chain_finalize, dg, and dX written
+// once from the on-chip copy. HBM sees X read once and dX written once; the three-kernel chain reads X
+// twice and moves its column partials through memory. Thread t owns columns c0 + 4 (t & 3) .. + 3 of
+// rows (t >> 2) + 128 i. Every sum is a fixed tree (slots in order, then lanes by xor, then waves in
+// order), so results are deterministic. Each workgroup stores its 16 columns' loss terms summed in
+// column order; the last to arrive (arrival counter, zero before and after the launch) adds the strips'
+// sums in strip order.
+constexpr int kResThreads = 512, kResRowLanes = kResThreads / 4, kResCols = 16;
+constexpr int kResMaxRegs = 45, kResMaxLds = 19;   // float4 slots per thread in VGPRs / in LDS (152 KiB)
+
+__device__ __forceinline__ float res_tree_max(float v) {   // over the 16 lanes of a wave with equal lane & 3
+    v = fmaxf(v, __shfl_xor(v, 4, 64));
+    v = fmaxf(v, __shfl_xor(v, 8, 64));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float res_tree_sum(float v) {
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+// NS: float4 slots per thread, R = 128 * NS rows.
+template <int NS>
+__global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float *X, int R, int Cc, const float *g,
+                                                                      float *dX, float *dg, float *lossp, int *counter,
+                                                                      float *loss) {
+    constexpr int kResRegs = NS < kResMaxRegs ? NS : kResMaxRegs, kResLds = NS - kResRegs;
+    static_assert(kResLds <= kResMaxLds, "the strip does not fit on chip");
+    __shared__ __attribute__((aligned(1024))) floatx4 held[kResLds > 0 ? kResLds : 1][kResThreads];
+    __shared__ float red[kResThreads / 64][kResCols];
+    __shared__ __attribute__((aligned(16))) float colv[kResCols];
+    __shared__ float colsum3[3][kResCols];                        // sum e, sum e^2, ties per column
+    __shared__ __attribute__((aligned(16))) float coef[6][kResCols];   // rs, g*r, gsq, gs, share, loss term
+    __shared__ int ticket;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nstrips = Cc / kResCols;
+    int strip = blockIdx.x;
+    if ((nstrips & 7) == 0) strip = (strip & 7) * (nstrips >> 3) + (strip >> 3);   // neighbouring strips share an XCD
+    const int q = tid & 3, rl = tid >> 2;
+    const int col = strip * kResCols + 4 * q;
+    // Buffer accesses from the strip's first column: the lane's offset in one VGPR, the slot's row
+    // offset (wave-uniform) in the scalar offset, so the 64 slots cost no address registers. The
+    // caller guarantees R * Cc * 4 < 2^31.
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)(X + strip * kResCols), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc((void *)(dX + strip * kResCols), (short)0, 0x7fffffff, 0x00020000);
+    const int voff = (rl * Cc + 4 * q) * 4;
+    const int rstepB = kResRowLanes * Cc * 4;
+    // 1. the strip: register slots first (they are consumed first), then the LDS slots
+    floatx4 v[kResRegs];
+#pragma unroll
+    for (int i = 0; i < kResRegs; i++)
+        v[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(xr, voff, i * rstepB, 0));
+#pragma unroll
+    for (int j = 0; j < kResLds; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void *)&held[j][wave * 64], 16,
+                                                     voff, (kResRegs + j) * rstepB, 0, 0);
+    // 2. column max
+    float m[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+#pragma unroll
+    for (int i = 0; i < kResRegs; i++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) m[u] = fmaxf(m[u], v[i][u]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's LDS-DMA has landed (each lane reads its own)
+#pragma unroll 2
+    for (int j = 0; j < kResLds; j++) {
+        const floatx4 x = *(volatile floatx4 *)&held[j][tid];
+#pragma unroll
+        for (int u = 0; u < 4; u++) m[u] = fmaxf(m[u], x[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) m[u] = res_tree_max(m[u]);
+    // Cross-wave step of a column reduction: lanes 0-3 of each wave post their 4 columns, 16 threads
+    // fold the 8 waves in order, and every thread reads its 4 columns back as one vector (the per-thread
+    // live set stays at 4 values; the held strip fills most registers).
+    auto across_waves = [&](float (&x)[4], bool is_max, float *keep) {
+        if (lane < 4)
+#pragma unroll
+            for (int u = 0; u < 4; u++) red[wave][4 * lane + u] = x[u];
+        __syncthreads();
+        if (tid < kResCols) {
+            float a = red[0][tid];
+            for (int w = 1; w < kResThreads / 64; w++) a = is_max ? fmaxf(a, red[w][tid]) : a + red[w][tid];
+            colv[tid] = a;
+            if (keep) keep[tid] = a;
+        }
+        __syncthreads();
+        const floatx4 r4 = *(const floatx4 *)&colv[4 * q];
+#pragma unroll
+        for (int u = 0; u < 4; u++) x[u] = r4[u];
+        __syncthreads();   // colv and red are reused
+    };
+    across_waves(m, true, nullptr);
+    // Passes 3 and 5 walk the register slots, then the LDS slots two at a time. The LDS slots are read
+    // through volatile loads in every pass: otherwise the compiler may keep one pass's reads live in
+    // registers for the next, which the held strip leaves no room for.
+    auto each = [&](auto &&f) {
+#pragma unroll
+        for (int i = 0; i < kResRegs; i++) f(i, v[i]);
+#pragma unroll 2
+        for (int j = 0; j < kResLds; j++) {
+            const floatx4 x = *(volatile floatx4 *)&held[j][tid];
+            f(kResRegs + j, x);
+        }
+    };
+    // 3. sum e, sum e^2 and ties against the exact max
+    float se[4] = {}, sq[4] = {}, tc[4] = {};
+    each([&](int, const floatx4 &x) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float e = fast_exp2((x[u] - m[u]) * AH_INV_LN2);
+            se[u] += e;
+            sq[u] += e * e;
+            tc[u] += x[u] == m[u] ? 1.0f : 0.0f;
+        }
+        // materialise all three sums after every slot: left free, the compiler runs the e sums over
+        // all slots first and the e^2 sums after them, keeping every slot's e live in between
+        asm volatile("" : "+v"(se[0]), "+v"(se[1]), "+v"(se[2]), "+v"(se[3]), "+v"(sq[0]), "+v"(sq[1]), "+v"(sq[2]),
+                     "+v"(sq[3]), "+v"(tc[0]), "+v"(tc[1]), "+v"(tc[2]), "+v"(tc[3]));
+    });
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        se[u] = res_tree_sum(se[u]);
+        sq[u] = res_tree_sum(sq[u]);
+        tc[u] = res_tree_sum(tc[u]);
+    }
+    across_waves(se, false, colsum3[0]);
+    across_waves(sq, false, colsum3[1]);
+    across_waves(tc, false, colsum3[2]);
+    // 4. the per-column scalars (chain_finalize's rules): thread c < 16 evaluates column c, and every
+    // thread reads its 4 columns' scalars back (one column's temporaries per thread, not four)
+    if (tid < kResCols) {
+        const int c = strip * kResCols + tid;
+        const float eps = 1e-6f, rR = 1.0f / (float)R;
+        const float s_ = colsum3[0][tid], q_ = colsum3[1][tid], t_ = colsum3[2][tid];
+        const float r_s = 1.0f / s_;
+        const float sumS = s_ * r_s;
+        const float sqq = q_ * (r_s * r_s);
+        const float qm = sqq * rR;
+        const float T = sqrtf(qm + eps);
+        const float r = 1.0f / T;
+        const float gi = g[c];
+        const float gR = gi * sumS;
+        const float gT = ((-gR) * r) * r;
+        const float gu = gT * (1.0f / (2.0f * T));
+        const float gsq_ = gu * rR;
+        const float gRs = (gi * r) * s_ + 2.0f * gsq_ * (r_s * q_);
+        const float gs_ = ((-gRs) * r_s) * r_s;
+        const float gm = -(AH_LN2 * AH_INV_LN2) * (r_s * gRs + gs_ * s_);
+        coef[0][tid] = r_s;
+        coef[1][tid] = gi * r;
+        coef[2][tid] = gsq_;
+        coef[3][tid] = gs_;
+        coef[4][tid] = gm * (1.0f / t_);
+        coef[5][tid] = gi * (r * sumS);
+        dg[c] = r * sumS;
+    }
+    __syncthreads();
+    float rs[4], gr[4], gsq[4], gs[4], sh[4];
+    {
+        const floatx4 a = *(const floatx4 *)&coef[0][4 * q], b = *(const floatx4 *)&coef[1][4 * q],
+                      c2 = *(const floatx4 *)&coef[2][4 * q], d = *(const floatx4 *)&coef[3][4 * q],
+                      e = *(const floatx4 *)&coef[4][4 * q];
+#pragma unroll
+        for (int u = 0; u < 4; u++) { rs[u] = a[u]; gr[u] = b[u]; gsq[u] = c2[u]; gs[u] = d[u]; sh[u] = e[u]; }
+    }
+    // 5. dX from the held strip
+    each([&](int i, const floatx4 &x) {
+        floatx4 o;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float y = x[u];
+            const float e = fast_exp2((y - m[u]) * AH_INV_LN2);
+            const float S = e * rs[u];
+            const float t2 = gsq[u] * S;
+            const float gS = (gr[u] + t2) + t2;
+            const float ge = gS * rs[u] + gs[u];
+            const float gzs = ((ge * e) * AH_LN2) * AH_INV_LN2;
+            o[u] = gzs + (y == m[u] ? sh[u] : 0.0f);
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, o), dr, voff, i * rstepB, 0);
+    });
+    // 6. loss: this strip's 16 terms in column order, then the strips in order by the last to arrive
+    __syncthreads();
+    if (tid == 0) {
+        float a = 0.0f;
+        for (int c = 0; c < kResCols; c++) a += coef[5][c];
+        __hip_atomic_store(lossp + strip, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (ticket != (int)gridDim.x - 1 || wave != 0) return;
+    // lane k adds strips k*P .. k*P+P-1 in order, then the lanes in a fixed tree
+    const int per = (nstrips + 63) / 64;
+    float a = 0.0f;
+    for (int k = 0; k < per; k++) {
+        const int s2 = lane * per + k;
+        if (s2 < nstrips) a += __hip_atomic_load(lossp + s2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    a = wave_sum(a);
+    if (lane == 0) {
+        loss[0] = a;
+        __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Row counts with an instantiated strip program: R = 8192 (64 float4 slots per thread). An R = 4096
+// instantiation (32 slots, all in VGPRs) returned zero for one element of each float4 in lanes 12-15 of
+// every wave when tested, for a reason not found, so it is not built; other shapes take the three-kernel
+// chain.
+bool chain_resident_fits(int R, int Cc) {
+    return R == 128 * 64 && Cc >= kResCols && Cc % kResCols == 0 && (long)R * Cc * 4 < (1L << 31);
+}
+
+hipError_t chain_resident(const float *X, const float *g, int R, int Cc, float *lossp, int *counter, float *dX, float *dg,
+                          float *loss, hipStream_t s) {
+    if (!chain_resident_fits(R, Cc)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(chain_resident_kernel<64>, dim3(Cc / kResCols), dim3(kResThreads), 0, s, X, R, Cc, g, dX, dg, lossp,
+                       counter, loss);
+    return hipGetLastError();
+}
+
 // ── step tail: bias SGD for several parameters + loss finalize, in one launch ─────
 // Each accumulator element (or partial-row entry) is read and re-zeroed by the thread that sums it,
 // leaving the accumulators ready for the next step's atomics or partial stores (no zero-fill launch).
@@ -485,14 +715,21 @@ hipError_t mse_finalize(const float *acc, float scale, float *out, hipStream_t s
     return hipGetLastError();
 }
 
+// Workspace: word 0 is the resident path's arrival counter (zero before the first call, left zero by
+// every call; the three-kernel path never touches it), then from float 64 either path's arrays.
+constexpr long kChainHead = 64;
 long chain_workspace_floats(int R, int Cc) {
     int nch = (R + kChainStatsRows - 1) / kChainStatsRows;
-    return (long)nch * Cc * 4 + (long)Cc * 8 + (Cc + kFinCols - 1) / kFinCols;
+    const long three = (long)nch * Cc * 4 + (long)Cc * 8 + (Cc + kFinCols - 1) / kFinCols;
+    return kChainHead + std::max(three, (long)(Cc / kResCols));
 }
 
 hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work, float *dX, float *dg, float *loss,
                       hipStream_t s, int phase) {
     if (Cc % 4 != 0 || R <= 0) return hipErrorInvalidValue;
+    if (phase < 0 && chain_resident_fits(R, Cc))
+        return chain_resident(X, g, R, Cc, work + kChainHead, (int *)work, dX, dg, loss, s);
+    work += kChainHead;
     const int nch = (R + kChainStatsRows - 1) / kChainStatsRows;
     const int nfin = (Cc + kFinCols - 1) / kFinCols;
     ColStat *part = (ColStat *)work;
@@ -519,7 +756,9 @@ hipError_t chain_step(const float *X, const float *g, int R, int Cc, float *work
 // address until the process ends; host code must use the address hipGetSymbolAddress returned for the
 // current device, never the array's name (which is only a host-side stand-in).
 // The chain writes every workspace entry before reading it (chain_stats fills every chunk partial,
-// chain_finalize every coefficient and loss partial), so nothing needs clearing between calls.
+// chain_finalize every coefficient and loss partial; the resident path every strip's loss sum), except
+// the resident path's arrival counter in word 0: static storage starts at zero and every call leaves
+// it zero, so nothing needs clearing between calls.
 namespace ah {
 namespace {
 constexpr long kChainScratchFloats = 1L << 22;   // 16 MiB: R x Cc up to 16320 x 4096 (config 5, 8192 x 4096, needs 2.13M floats)

@@ -135,7 +135,8 @@ def test_softmax_ce_kernel(dev, B, C):
     assert abs(dloss.read()[0] - wl) <= 1e-5 * max(1.0, abs(wl))
 
 
-@pytest.mark.parametrize("R,Cc", [(64, 32), (257, 260), (1024, 512)])
+# (8192, 64) and (8192, 528): the column-strip kernel that holds X on chip; the others: the three-kernel chain
+@pytest.mark.parametrize("R,Cc", [(64, 32), (257, 260), (1024, 512), (4096, 256), (8192, 64), (8192, 528)])
 def test_chain_kernel_vs_oracle(dev, R, Cc):
     X = RNG.standard_normal((R, Cc)).astype(np.float32)
     X[5, :] = X.max() + 0.5                             # every row of Y gets a tie candidate
@@ -144,7 +145,16 @@ def test_chain_kernel_vs_oracle(dev, R, Cc):
     wl, wdX, wdg = O.chain_step(X, g)
     dXb, dgb, dX, dg, dl = dev.buffer(X), dev.buffer(g), dev.buffer(R * Cc), dev.buffer(Cc), dev.buffer(1)
     dev.chain_step(dXb, dgb, R, Cc, dX, dg, dl)
-    assert O.relerr(dX.read().reshape(R, Cc), wdX) < 1e-4
+    # Each column's max elements carry the max-path tie share, zero in exact arithmetic and a rounding
+    # residue in any f32 evaluation (it depends on how sum e was rounded): those are judged against the
+    # float64 closed form, no further from it than the oracle is (plus 1e-4); the rest against the oracle.
+    from oracle_np import chain_dX_f64
+    got = dX.read().reshape(R, Cc)
+    exact = chain_dX_f64(X, g)
+    mask = X == X.max(0, keepdims=True)
+    den = np.max(np.abs(wdX))
+    assert np.max(np.abs(got - wdX)[~mask]) / den < 1e-4
+    assert np.max(np.abs(got - exact)[mask]) / den <= np.max(np.abs(wdX - exact)[mask]) / den + 1e-4
     assert O.relerr(dg.read(), wdg) < 1e-5
     assert abs(dl.read()[0] - wl) < 1e-5 * abs(wl)
     for b in (dXb, dgb, dX, dg, dl):
