@@ -263,8 +263,8 @@ int ah_chain_step(ah_device *dev, const float *X, const float *g, int32_t R, int
 /* ah_chain_step without allocation. No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops). The chain's workspace is a
  * file-scope device array of 2^22 floats (16 MiB per GPU, held until the process ends), so
- * ceil(R/64)*Cc*4 + Cc*8 + ceil(Cc/16) must not exceed 2^22 (config 5, 8192 x 4096, needs 2.13M);
- * larger shapes fail with AH_ERR_INVALID. Asynchronous: the three kernels are enqueued on the device
+ * 64 + max(ceil(R/64)*Cc*4 + Cc*8 + ceil(Cc/16), Cc/16) must not exceed 2^22 (config 5, 8192 x 4096, needs 2.13M);
+ * larger shapes fail with AH_ERR_INVALID. Asynchronous: the chain kernels (one at R = 8192, else three) are enqueued on the device
  * stream and the call returns (ah_sync waits). Every call on one GPU shares that GPU's workspace, so
  * calls that overlap on one GPU (several device handles or host threads) race. */
 int ah_chain_step_noalloc(ah_device *dev, const float *X, const float *g, int32_t R, int32_t Cc, float *dX,
