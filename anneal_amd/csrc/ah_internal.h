@@ -83,4 +83,6 @@ std::unordered_map<std::string, std::string> template_key_params(const std::stri
 // Grows the template's workspace for the binding symval (before a graph capture).
 int template_prepare(TemplateKernel *t, int64_t symval);
 std::string wgsl_to_hip(const std::string &src, std::string *err);
+// A "tmpl:gemm" key for a WGSL kernel that is a plain contraction (wgsl_match.cpp), else false.
+bool wgsl_match_contraction(const std::string &src, std::string *key);
 }

@@ -150,6 +150,21 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
     float *const colsum = d.colsum;
     const int colsum_ld = d.colsum_ld;
     const int c4 = (lane & 15) * 4;
+    // every slab's bias columns, loaded before the first slab (one load latency, not one per slab)
+    floatx4 biasv[FN / 2];
+#pragma unroll
+    for (int jp = 0; jp < FN / 2; jp++) {
+        biasv[jp] = (floatx4){};
+        if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RELU || EPI == EPI_MSE) {
+            const int n = nb + jp * 64 + c4;
+            if constexpr (sizeof(T) == 2) {
+                T4 b = *(const T4 *)((const T *)d.bias + n);
+                biasv[jp] = (floatx4){(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+            } else {
+                biasv[jp] = *(const floatx4 *)((const float *)d.bias + n);
+            }
+        }
+    }
 #pragma unroll
     for (int jp = 0; jp < FN / 2; jp++) {
         // 1. accumulators -> LDS
@@ -163,15 +178,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
         __builtin_amdgcn_s_waitcnt(0xc07f);     // lgkmcnt(0): this wave's LDS writes have landed
         __builtin_amdgcn_wave_barrier();
         const int n = nb + jp * 64 + c4;
-        floatx4 bias = {};
-        if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RELU || EPI == EPI_MSE) {
-            if constexpr (sizeof(T) == 2) {
-                T4 b = *(const T4 *)((const T *)d.bias + n);
-                bias = (floatx4){(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
-            } else {
-                bias = *(const floatx4 *)((const float *)d.bias + n);
-            }
-        }
+        const floatx4 bias = biasv[jp];
         floatx4 cs = {};
         // 2. LDS -> global, 4 rows per instruction (row = 4t + lane/16), G row groups at a time
 #pragma unroll

@@ -22,7 +22,6 @@ namespace ah {
 
 constexpr int kMlpThreads = 1024;
 constexpr int kMlpMaxB = 64, kMlpMaxH = 128, kMlpMaxC = 16, kMlpMaxD = 896;
-constexpr int kW2Ld = kMlpMaxH + 16;
 constexpr int kHidTile = 8;    // samples and hidden units per hidden-layer workgroup
 constexpr int kGradCols = 8;   // input columns of W1 per gradient workgroup
 

@@ -244,7 +244,15 @@ int ah_module_get(ah_device *d, const char *source, const char *entry, ah_kernel
         return AH_OK;
     }
     ah_kernel *k = new ah_kernel();
-    if (strncmp(source, "tmpl:", 5) == 0) {
+    // A WGSL kernel that is a plain contraction runs the hand-written MFMA template instead of its
+    // rendering (wgsl_match.cpp); AH_WGSL_TEMPLATES=0 turns the selection off.
+    std::string matched;
+    const char *sel = getenv("AH_WGSL_TEMPLATES");
+    const bool select = !(sel && strcmp(sel, "0") == 0);
+    if (select && strstr(source, "@compute") && wgsl_match_contraction(source, &matched)) {
+        int rc = template_create(matched.c_str(), &k->tmpl);
+        if (rc != AH_OK) { delete k; return rc; }
+    } else if (strncmp(source, "tmpl:", 5) == 0) {
         int rc = template_create(source, &k->tmpl);
         if (rc != AH_OK) { delete k; return rc; }
     } else {
@@ -372,3 +380,14 @@ void ah_graph_destroy(ah_graph *g) {
 }
 
 }  // extern "C"
+
+extern "C" int ah_wgsl_template_key(const char *wgsl, char *buf, int32_t cap) {
+    if (!wgsl || !buf || cap <= 0) return set_error(AH_ERR_INVALID, "ah_wgsl_template_key: null argument");
+    std::string key;
+    if (!ah::wgsl_match_contraction(wgsl, &key)) {
+        buf[0] = 0;
+        return AH_OK;
+    }
+    snprintf(buf, (size_t)cap, "%s", key.c_str());
+    return AH_OK;
+}

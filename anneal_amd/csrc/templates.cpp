@@ -132,7 +132,8 @@ int ensure_ws(TemplateKernel *t, int64_t bytes) {
 }
 
 // ── gemm ─────────────────────────────────────────────────────────────────────────────────────────
-// "tmpl:gemm;dtype=f16|f32;epi=...;ta=0|1;tb=0|1;M=..;N=..;K=..[;scale=s][;lr=l][;variant=v][;tile=t;kg=g]"
+// "tmpl:gemm;dtype=f16|f32;epi=...;ta=0|1;tb=0|1;M=..;N=..;K=..[;scale=s][;lr=l][;variant=v][;tile=t;kg=g]
+//  [;swap_ab=1]" (swap_ab: A is the second input PARAM and B the first)
 // variant picks an f16 kernel variant, tile (64/128/256) and kg (k-groups) the f32 tiled kernel's shape.
 // M, N and K may be symbolic. PARAMs by epilogue:
 //   store      C, A, B                     C = scale*acc
@@ -176,10 +177,11 @@ int template_gemm(const Params &P, TemplateKernel *t) {
         return set_error(AH_ERR_INVALID, "tmpl gemm: tile %d", base.tile);
     if (base.kgroups != 0 && !(base.tile != 0 && gemm32_kgroups_ok(base.tile, base.kgroups)))
         return set_error(AH_ERR_INVALID, "tmpl gemm: kg=%d needs a tile that admits it", base.kgroups);
+    const bool swap_ab = P.integer("swap_ab", 0) != 0;
     const int nbuf = (base.epi == EPI_STORE || grad) ? 3 : base.epi == EPI_MSE ? 6 : 4;
     if (base.epi == EPI_MSE) t->side = {{5, true}};
     const std::string key = t->key;
-    t->run = [base, M, N, K, nbuf, grad, key](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs,
+    t->run = [base, M, N, K, nbuf, grad, key, swap_ab](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs,
                                          const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, nbuf)) return rc;
         GemmDesc g = base;
@@ -187,8 +189,8 @@ int template_gemm(const Params &P, TemplateKernel *t) {
         AT(N, n);
         AT(K, k);
         g.M = (int)m; g.N = (int)n; g.K = (int)k;
-        g.A = ptrs[1];
-        g.B = ptrs[2];
+        g.A = ptrs[swap_ab ? 2 : 1];   // swap_ab: the first-bound input is B
+        g.B = ptrs[swap_ab ? 1 : 2];
         g.lda = g.ta ? g.M : g.K;
         g.ldb = g.tb ? g.N : g.K;
         g.ldc = g.N;

@@ -79,6 +79,14 @@ int ah_module_get(ah_device *dev, const char *source, const char *entry, ah_kern
  * on its own (no device needed): writes at most cap bytes of NUL-terminated HIP source to out and the
  * full size to *needed; AH_ERR_COMPILE if the WGSL is outside the subset the reference emits. */
 int ah_translate_wgsl(const char *wgsl, char *out, int64_t cap, int64_t *needed);
+/* Template selection for a rendered WGSL kernel (host only, no device): when the kernel is a plain
+ * contraction REDUCE(ADD, MUL(load, load)) of three f32 buffers whose load and store indices are affine
+ * with zero offset (the scheduler's unsimplified index chains evaluated, codegen/lower.go:98-550 as
+ * rendered by codegen/wgsl.go:36-238), writes the "tmpl:gemm;..." key ah_module_get runs in its place
+ * (the MFMA contraction template) to buf; otherwise writes "". No counterpart in the reference, whose
+ * backend renders every kernel: it exposes the selection ah_module_get and ah_run make (set
+ * AH_WGSL_TEMPLATES=0 to turn it off). */
+int ah_wgsl_template_key(const char *wgsl, char *buf, int32_t cap);
 int ah_launch(ah_device *dev, ah_kernel *k, const uint32_t grid[3], const uint32_t block[3],
               void *const *ptrs, int32_t n_ptrs, const int32_t *scalars, int32_t n_scalars);
 

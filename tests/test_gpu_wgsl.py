@@ -27,3 +27,29 @@ def test_wgsl_kernel_runs_and_matches(dev, name):
         np.testing.assert_array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
     else:
         np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb,b_first", [(96, 80, 64, False, True, False), (257, 130, 77, True, False, True),
+                                                 (512, 384, 256, False, False, False)])
+def test_selected_contraction_matches_rendering(dev, monkeypatch, M, N, K, ta, tb, b_first):
+    """A rendered contraction runs the MFMA template (selected from its WGSL, tests/test_wgsl_select.py);
+    its output matches a float64 product at the f32 reduction bar (1e-5 here) and the rendered kernel's
+    own output (selection off) to summation order."""
+    from anneal_amd import _lib as L
+    from anneal_amd.backend import Device
+    src, ws, wc = W.matmul_wgsl(M, N, K, ta=ta, tb=tb, b_first=b_first)
+    assert L.wgsl_template_key(src).startswith("tmpl:gemm")
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N) if tb else (N, K)).astype(np.float32)
+    want = (A.T if ta else A).astype(np.float64) @ (B if tb else B.T).astype(np.float64)
+    bufs = [Buffer(30, M * N, [M * N]), Buffer(1, A.size, [A.size]), Buffer(2, B.size, [B.size])]
+    item = ExecItem(src, bufs, local_size=ws, workgroup_count=wc)
+    got = Executor(dev).run([item], {1: A.ravel(), 2: B.ravel()})[30].reshape(M, N)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() / scale < 1e-5
+    monkeypatch.setenv("AH_WGSL_TEMPLATES", "0")
+    with Device(0) as d2:    # a fresh device: its module cache renders the WGSL
+        ref = Executor(d2).run([item], {1: A.ravel(), 2: B.ravel()})[30].reshape(M, N)
+    assert np.abs(ref - want).max() / scale < 1e-5
+    assert np.abs(got - ref).max() / scale < 1e-5

@@ -1,0 +1,44 @@
+"""Template selection for rendered WGSL (host side): a kernel that is a plain contraction of three f32
+buffers is recognised from its evaluated index expressions and runs the MFMA contraction template
+(tmpl:gemm) instead of its rendering; everything else keeps the rendering. The GPU side of the same
+kernels is tests/test_gpu_wgsl.py."""
+import pytest
+
+import wgsl_kernels as W
+from anneal_amd import _lib as L
+
+
+def test_reference_matmul_known_answer_is_selected():
+    # webgpu_test.go:224-253's [2,3] @ [3,2]: A [M,K] K-contiguous, B [K,N] (tb=1)
+    assert L.wgsl_template_key(W.kernels()["matmul_known_answer"][0]) == \
+        "tmpl:gemm;dtype=f32;epi=store;ta=0;tb=1;M=2;N=2;K=3"
+
+
+@pytest.mark.parametrize("ta,tb,b_first", [(False, True, False), (True, True, False), (False, False, True),
+                                           (True, False, True)])
+def test_layouts_and_load_order(ta, tb, b_first):
+    M, N, K = 96, 80, 64
+    src, _, _ = W.matmul_wgsl(M, N, K, ta=ta, tb=tb, b_first=b_first)
+    want = f"tmpl:gemm;dtype=f32;epi=store;ta={int(ta)};tb={int(tb)};M={M};N={N};K={K}"
+    assert L.wgsl_template_key(src) == want      # the load order does not change the binding roles
+
+
+@pytest.mark.parametrize("name", ["exp2_elementwise", "max_tie_mask", "symbolic_batch", "f16_accumulate",
+                                  "vec4_accumulators", "group_reduce_lds", "diag_fma_probe"])
+def test_other_kernels_keep_their_rendering(name):
+    ks = W.kernels()
+    if name not in ks:
+        pytest.skip(f"no kernel {name}")
+    assert L.wgsl_template_key(ks[name][0]) == ""
+
+
+def test_offset_index_is_not_a_contraction():
+    src, _, _ = W.matmul_wgsl(16, 16, 16, offset=1)
+    assert L.wgsl_template_key(src) == ""
+
+
+def test_swapped_bindings_select_swap_ab():
+    # B bound first (data1 holds B): the same contraction with the operand PARAMs swapped
+    src, _, _ = W.matmul_wgsl(32, 48, 16)
+    src = src.replace("data1[", "dataX[").replace("data2[", "data1[").replace("dataX[", "data2[")
+    assert L.wgsl_template_key(src) == "tmpl:gemm;dtype=f32;epi=store;ta=0;tb=1;M=32;N=48;K=16;swap_ab=1"

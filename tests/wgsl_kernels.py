@@ -238,3 +238,38 @@ fn main(@builtin(global_invocation_id) gid: vec3<u32>) {
     want = (((accs[0] + accs[1]).astype(np.float32) + accs[2]).astype(np.float32) + accs[3]).astype(np.float32)
     ks["diag_fma_probe"] = (probe, [(80, 256, F32), (1, 1, F32)], (256, 1, 1), (1, 1, 1), {1: inp}, want, None)
     return ks
+
+
+def matmul_wgsl(M, N, K, ta=False, tb=True, b_first=False, offset=0):
+    """A contraction as the reference's codegen renders it (codegen/lower.go REDUCE(ADD, MUL(INDEX, INDEX))
+    with the unsimplified index chains of schedule/index.go): out[m, n] = sum_k A(m, k) * B(k, n), A read
+    from data1 ([M,K], or [K,M] with ta), B from data2 ([K,N] with tb, else [N,K]); with b_first the B load
+    is emitted first. offset shifts A's index (no longer a zero-offset contraction). Returns (wgsl,
+    bufs, local_size, workgroup_count) for the shapes of ExecItem."""
+    ws = (64, 1, 1)
+    wc = ((M * N + 63) // 64, 1, 1)
+    if ta:   # A(m, k) at k*M + m, through a chain over the flat [K, M] view
+        ia = f"((((r2 * {M}) + r0) / {M}) % {K}) * {M} + (((r2 * {M}) + r0) % {M})"
+    else:
+        ia = f"((((r0 * {K}) + r2) / {K}) % {M}) * {K} + (((r0 * {K}) + r2) % {K})"
+    if offset:
+        ia = f"({ia}) + {offset}"
+    if tb:   # B(k, n) at k*N + n
+        ib = f"((((r2 * {N}) + r1) / {N}) % {K}) * {N} + (((r2 * {N}) + r1) % {N})"
+    else:
+        ib = f"((((r1 * {K}) + r2) / {K}) % {N}) * {K} + (((r1 * {K}) + r2) % {K})"
+    loads = [f"    let t9: f32 = data1[{ia}];", f"    let t12: f32 = data2[{ib}];"]
+    if b_first:
+        loads.reverse()
+    src = header(["f32", "f32", "f32"], ws, wc) + main_open(ws, wc) + [
+        f"  let r0: i32 = i32((flat_gid_x / {N}u) % {M}u);",
+        f"  if (r0 >= {M}) {{ return; }}",
+        f"  let r1: i32 = i32(flat_gid_x % {N}u);",
+        f"  if (r1 >= {N}) {{ return; }}",
+        "  var acc0: f32 = 0.0;",
+        f"  for (var r2: i32 = 0; r2 < {K}; r2++) {{"] + loads + [
+        "    acc0 = acc0 + (t9 * t12);",
+        "  }",
+        f"  data0[((r0 * {N}) + r1)] = acc0;",
+        "}"]
+    return "\n".join(src), ws, wc
