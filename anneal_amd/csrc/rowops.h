@@ -52,8 +52,8 @@ long chain_workspace_floats(int R, int Cc);
 // the device `ordinal` (the current device at the call).
 long chain_scratch_floats();
 hipError_t chain_scratch_init(int ordinal, float **out);
-// Config 5 with each 16-column strip of X held on chip (one pass over HBM): for R = 8192 and Cc a
-// multiple of 16. lossp: Cc/16 floats; counter: one int, zero before the call and left zero.
+// Config 5 with each 16-column strip of X held on chip (one pass over HBM): for R = 4096 or 8192 and
+// Cc a multiple of 16. lossp: Cc/16 floats; counter: one int, zero before the call and left zero.
 bool chain_resident_fits(int R, int Cc);
 hipError_t chain_resident(const float *X, const float *g, int R, int Cc, float *lossp, int *counter, float *dX, float *dg,
                           float *loss, hipStream_t s);

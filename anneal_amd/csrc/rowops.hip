@@ -318,8 +318,8 @@ __global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, 
 
 // ── config 5 in one pass over HBM: strips of X held on chip ─────────────────────
 // Every softmax / RMS row of the chain is one column of X, and dg, the loss terms and dX of a column
-// need only that column. So one workgroup per CU takes a strip of 16 columns x R rows (R = 8192:
-// 512 KiB), keeps all of it on chip (kResRegs float4 per thread in VGPRs, kResLds in LDS through
+// need only that column. So one workgroup per CU takes a strip of 16 columns x R rows (R = 4096 or
+// 8192: up to 512 KiB), keeps all of it on chip (kResRegs float4 per thread in VGPRs, kResLds in LDS through
 // LDS-DMA), and runs the whole chain on it: the exact column max, then sum e, sum e^2 and the tie
 // count against that max (no rescaling), the per-column scalars of chain_finalize, dg, and dX written
 // once from the on-chip copy. HBM sees X read once and dX written once; the three-kernel chain reads X
@@ -429,11 +429,17 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         }
     };
     // 3. sum e, sum e^2 and ties against the exact max
+    // exp(x - m) as exp2(fma(x, 1/ln2, -m/ln2)): one VALU op fewer per element than subtract-then-scale
+    // (the argument is rounded once instead of twice); an element equal to m gets exp2 of the rounding
+    // residue of m/ln2, within an ulp of 1
+    float mk[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) mk[u] = -(m[u] * AH_INV_LN2);
     float se[4] = {}, sq[4] = {}, tc[4] = {};
     each([&](int, const floatx4 &x) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const float e = fast_exp2((x[u] - m[u]) * AH_INV_LN2);
+            const float e = fast_exp2(__builtin_fmaf(x[u], AH_INV_LN2, mk[u]));
             se[u] += e;
             sq[u] += e * e;
             tc[u] += x[u] == m[u] ? 1.0f : 0.0f;
@@ -495,15 +501,22 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float y = x[u];
-            const float e = fast_exp2((y - m[u]) * AH_INV_LN2);
+            const float e = fast_exp2(__builtin_fmaf(y, AH_INV_LN2, mk[u]));
             const float S = e * rs[u];
             const float t2 = gsq[u] * S;
             const float gS = (gr[u] + t2) + t2;
             const float ge = gS * rs[u] + gs[u];
-            const float gzs = ((ge * e) * AH_LN2) * AH_INV_LN2;
+            const float gzs = (ge * e) * (AH_LN2 * AH_INV_LN2);   // the Exp rule's ln2 and 1/ln2 as one factor
             o[u] = gzs + (y == m[u] ? sh[u] : 0.0f);
         }
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, o), dr, voff, i * rstepB, 0);
+        // Wait states after the 16-byte store before anything may rewrite its data registers. Without
+        // them the compiler placed a VALU write to the store's first data VGPR two instructions later,
+        // behind a v_readlane of a spilled SGPR, and that dword of some lanes was stored already
+        // overwritten (observed: element 0 of the float4 in lanes 12-15 of a wave).
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 4" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     });
     // 6. loss: this strip's 16 terms in column order, then the strips in order by the last to arrive
     __syncthreads();
@@ -530,19 +543,21 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
     }
 }
 
-// Row counts with an instantiated strip program: R = 8192 (64 float4 slots per thread). An R = 4096
-// instantiation (32 slots, all in VGPRs) returned zero for one element of each float4 in lanes 12-15 of
-// every wave when tested, for a reason not found, so it is not built; other shapes take the three-kernel
-// chain.
+// Row counts with an instantiated strip program: R = 8192 (64 float4 slots per thread: 45 in VGPRs, 19 in
+// LDS) and R = 4096 (32, all in VGPRs); other shapes take the three-kernel chain.
 bool chain_resident_fits(int R, int Cc) {
-    return R == 128 * 64 && Cc >= kResCols && Cc % kResCols == 0 && (long)R * Cc * 4 < (1L << 31);
+    return (R == 128 * 64 || R == 128 * 32) && Cc >= kResCols && Cc % kResCols == 0 && (long)R * Cc * 4 < (1L << 31);
 }
 
 hipError_t chain_resident(const float *X, const float *g, int R, int Cc, float *lossp, int *counter, float *dX, float *dg,
                           float *loss, hipStream_t s) {
     if (!chain_resident_fits(R, Cc)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(chain_resident_kernel<64>, dim3(Cc / kResCols), dim3(kResThreads), 0, s, X, R, Cc, g, dX, dg, lossp,
-                       counter, loss);
+    if (R == 128 * 64)
+        hipLaunchKernelGGL(chain_resident_kernel<64>, dim3(Cc / kResCols), dim3(kResThreads), 0, s, X, R, Cc, g, dX, dg,
+                           lossp, counter, loss);
+    else
+        hipLaunchKernelGGL(chain_resident_kernel<32>, dim3(Cc / kResCols), dim3(kResThreads), 0, s, X, R, Cc, g, dX, dg,
+                           lossp, counter, loss);
     return hipGetLastError();
 }
 

@@ -135,7 +135,8 @@ def test_softmax_ce_kernel(dev, B, C):
     assert abs(dloss.read()[0] - wl) <= 1e-5 * max(1.0, abs(wl))
 
 
-# (8192, 64) and (8192, 528): the column-strip kernel that holds X on chip; the others: the three-kernel chain
+# (4096, 256), (8192, 64) and (8192, 528): the column-strip kernel that holds X on chip; the others: the
+# three-kernel chain
 @pytest.mark.parametrize("R,Cc", [(64, 32), (257, 260), (1024, 512), (4096, 256), (8192, 64), (8192, 528)])
 def test_chain_kernel_vs_oracle(dev, R, Cc):
     X = RNG.standard_normal((R, Cc)).astype(np.float32)
