@@ -43,6 +43,11 @@ struct G16Split {
             const int e = (c % 4) * 4;
             const floatx4 v = {a[e], a[e + 1], a[e + 2], a[e + 3]};
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, own + c * NT * 16, 0, SC1);
+            // wait states before the store's data registers may be rewritten (the compiler once placed
+            // such a VALU write two instructions behind a 16-byte store, and it reached the memory)
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 4" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's partial has landed
         __syncthreads();
