@@ -429,17 +429,11 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         }
     };
     // 3. sum e, sum e^2 and ties against the exact max
-    // exp(x - m) as exp2(fma(x, 1/ln2, -m/ln2)): one VALU op fewer per element than subtract-then-scale
-    // (the argument is rounded once instead of twice); an element equal to m gets exp2 of the rounding
-    // residue of m/ln2, within an ulp of 1
-    float mk[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) mk[u] = -(m[u] * AH_INV_LN2);
     float se[4] = {}, sq[4] = {}, tc[4] = {};
     each([&](int, const floatx4 &x) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const float e = fast_exp2(__builtin_fmaf(x[u], AH_INV_LN2, mk[u]));
+            const float e = fast_exp2((x[u] - m[u]) * AH_INV_LN2);
             se[u] += e;
             sq[u] += e * e;
             tc[u] += x[u] == m[u] ? 1.0f : 0.0f;
@@ -496,20 +490,25 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         for (int u = 0; u < 4; u++) { rs[u] = a[u]; gr[u] = b[u]; gsq[u] = c2[u]; gs[u] = d[u]; sh[u] = e[u]; }
     }
     // 5. dX from the held strip
+    // The stores' row offset is a running value advanced through an empty asm after each slot, so only
+    // the current one is live (all 64 kept from the loads overflow the SGPRs into VGPR lanes).
+    int soff = 0;
     each([&](int i, const floatx4 &x) {
         floatx4 o;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float y = x[u];
-            const float e = fast_exp2(__builtin_fmaf(y, AH_INV_LN2, mk[u]));
+            const float e = fast_exp2((y - m[u]) * AH_INV_LN2);
             const float S = e * rs[u];
             const float t2 = gsq[u] * S;
             const float gS = (gr[u] + t2) + t2;
             const float ge = gS * rs[u] + gs[u];
-            const float gzs = (ge * e) * (AH_LN2 * AH_INV_LN2);   // the Exp rule's ln2 and 1/ln2 as one factor
+            const float gzs = ((ge * e) * AH_LN2) * AH_INV_LN2;
             o[u] = gzs + (y == m[u] ? sh[u] : 0.0f);
         }
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, o), dr, voff, i * rstepB, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, o), dr, voff, soff, 0);
+        soff += rstepB;
+        asm volatile("" : "+s"(soff));
         // Wait states after the 16-byte store before anything may rewrite its data registers. Without
         // them the compiler placed a VALU write to the store's first data VGPR two instructions later,
         // behind a v_readlane of a spilled SGPR, and that dword of some lanes was stored already
