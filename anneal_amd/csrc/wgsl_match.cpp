@@ -17,7 +17,8 @@
 // arithmetic) at every point of each axis and at sampled points of the whole index space, and must be
 // affine there with zero offset. The coefficients then give the contraction: C [M,N] row-major, A read
 // K-contiguous ([M,K]) or MN-contiguous ([K,M]), B likewise, which is "tmpl:gemm" (templates.cpp) with
-// ta/tb and, when the first-bound input is B, swap_ab=1. Anything else is left to the WGSL renderer.
+// ta/tb and, when the first-bound input is B, swap_ab=1. Anything else (and any axis of more than 2^16
+// points) is left to the WGSL renderer.
 #include <ctype.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -230,8 +231,9 @@ bool wgsl_match_contraction(const std::string &src, std::string *key) {
     std::string acc;
     {
         const std::string &s = L[i++];
-        if (!starts(s, "var acc") || s.substr(s.find(':')) != ": f32 = 0.0;") return false;
-        acc = trim(s.substr(4, s.find(':') - 4));
+        const size_t colon = s.find(':');
+        if (!starts(s, "var acc") || colon == std::string::npos || s.substr(colon) != ": f32 = 0.0;") return false;
+        acc = trim(s.substr(4, colon - 4));
     }
     std::string kv;
     int64_t K = 0;
@@ -275,6 +277,9 @@ bool wgsl_match_contraction(const std::string &src, std::string *key) {
     // with the other axes at 0 (their only value)
     const std::string vn[3] = {live[0]->name, live[1]->name, kv};
     const int64_t range[3] = {live[0]->range, live[1]->range, K};
+    // every point of each axis is evaluated below: axes beyond 2^16 points are left to the rendering
+    for (int a = 0; a < 3; a++)
+        if (range[a] > (1 << 16)) return false;
     for (const Axis &a : axes)
         if (a.name == kv) return false;
     int64_t ca[3], cb[3], cc[3];

@@ -42,3 +42,20 @@ def test_swapped_bindings_select_swap_ab():
     src, _, _ = W.matmul_wgsl(32, 48, 16)
     src = src.replace("data1[", "dataX[").replace("data2[", "data1[").replace("dataX[", "data2[")
     assert L.wgsl_template_key(src) == "tmpl:gemm;dtype=f32;epi=store;ta=0;tb=1;M=32;N=48;K=16;swap_ab=1"
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda s: s.replace("var acc0: f32 = 0.0;", "var acc0 = 0.0;"),            # no type: not the emitted form
+    lambda s: s.replace("acc0 = acc0 + (t9 * t12);", "acc0 = acc0 + (t9 + t12);"),
+    lambda s: s.replace("data0[((r0 * 2) + r1)] = acc0;", "data0[((r0 * 2) + r1)] = (acc0 * 2.0);"),
+    lambda s: s.replace("let t9: f32 = data1[", "let t9: f32 = data1[((("),   # unbalanced parentheses
+    lambda s: s[: len(s) // 2],                                                  # truncated
+    lambda s: "",
+])
+def test_malformed_or_other_forms_are_not_selected(mutate):
+    assert L.wgsl_template_key(mutate(W.kernels()["matmul_known_answer"][0])) == ""
+
+
+def test_huge_axis_is_left_to_the_rendering():
+    src, _, _ = W.matmul_wgsl(16, 16, 1 << 20)
+    assert L.wgsl_template_key(src) == ""
