@@ -12,7 +12,9 @@
 //     accI = accI + (tX * tY);
 //   }
 //   data0[<index>] = accI;
-// with three f32 bindings and no symbolic parameters. The index expressions are not parsed for
+// with three f32 bindings and no symbolic parameters, or with a fourth, data3, holding a bias b[n] that
+// is added to accI before the store (let tB: f32 = data3[<index>]; then (accI + tB) or (tB + accI),
+// as a let or in the store): the Linear forward epilogue, "tmpl:gemm;epi=bias", the same f32 add. The index expressions are not parsed for
 // structure: they are evaluated (the scheduler's unsimplified chains of / and % included, as integer
 // arithmetic) at every point of each axis and at sampled points of the whole index space, and must be
 // affine there with zero offset. The coefficients then give the contraction: C [M,N] row-major, A read
@@ -202,7 +204,7 @@ bool wgsl_match_contraction(const std::string &src, std::string *key) {
         if (L[i].find(want) == std::string::npos) return false;
         nb++;
     }
-    if (nb != 3 || i == L.size()) return false;
+    if ((nb != 3 && nb != 4) || i == L.size()) return false;
     // the fixed preamble ends with "let gid_x = ..."
     for (; i < L.size() && !starts(L[i], "let gid_x ="); i++)
         if (L[i].find("var<workgroup>") != std::string::npos) return false;
@@ -226,8 +228,8 @@ bool wgsl_match_contraction(const std::string &src, std::string *key) {
         }
         axes.push_back(ax);
     }
-    // accumulator, loop, two loads, the multiply-add, loop end, store, function end
-    if (i + 8 != L.size()) return false;
+    // accumulator, loop, two loads, the multiply-add, loop end, [bias], store, function end
+    if (i + 8 > L.size()) return false;
     std::string acc;
     {
         const std::string &s = L[i++];
@@ -258,16 +260,44 @@ bool wgsl_match_contraction(const std::string &src, std::string *key) {
         i++;
     }
     if (L[i++] != "}") return false;
+    // optional bias epilogue (Linear forward, acc + b[n], codegen/wgsl.go:270 renders the add as
+    // "(a + b)"): a load of data3, then the sum as a let or inline in the store
+    std::string bname, bidx, sname;
+    while (i + 2 < L.size()) {
+        std::string bn, bt, be, bi;
+        int bb = -1;
+        if (!parse_let(L[i], &bn, &bt, &be) || bt != "f32") return false;
+        if (bname.empty() && parse_load(be, &bb, &bi) && bb == 3) {
+            bname = bn;
+            bidx = bi;
+        } else if (!bname.empty() && sname.empty() && (be == "(" + acc + " + " + bname + ")" || be == "(" + bname + " + " + acc + ")")) {
+            sname = bn;
+        } else {
+            return false;
+        }
+        i++;
+    }
+    if (L.size() - i != 2) return false;
     std::string cidx;
     {
         const std::string &s = L[i++];
-        const std::string tail = "] = " + acc + ";";
-        if (!starts(s, "data0[") || s.size() < tail.size() || s.compare(s.size() - tail.size(), tail.size(), tail) != 0)
-            return false;
-        cidx = s.substr(6, s.size() - 6 - tail.size());
+        std::vector<std::string> vals;   // what the store may write
+        if (bname.empty()) vals = {acc};
+        else if (!sname.empty()) vals = {sname};
+        else vals = {"(" + acc + " + " + bname + ")", "(" + bname + " + " + acc + ")"};
+        bool ok = false;
+        for (const std::string &v : vals) {
+            const std::string tail = "] = " + v + ";";
+            if (starts(s, "data0[") && s.size() > tail.size() + 6 && s.compare(s.size() - tail.size(), tail.size(), tail) == 0) {
+                cidx = s.substr(6, s.size() - 6 - tail.size());
+                ok = true;
+            }
+        }
+        if (!ok) return false;
     }
     if (L[i] != "}") return false;
     if (!((buf[0] == 1 && buf[1] == 2) || (buf[0] == 2 && buf[1] == 1))) return false;
+    if ((nb == 4) != !bname.empty()) return false;   // data3 is bound exactly when it is the bias
     // two output axes with more than one point (others are size 1 and must not move any index)
     std::vector<const Axis *> live;
     for (const Axis &a : axes)
@@ -314,10 +344,14 @@ bool wgsl_match_contraction(const std::string &src, std::string *key) {
     if (B[2] == 1 && B[in] == K) tb = 0;
     else if (B[in] == 1 && B[2] == N) tb = 1;
     else return false;
+    if (!bname.empty()) {   // the bias index must be n itself
+        int64_t cbias[3];
+        if (!affine(bidx, vn, range, cbias) || cbias[in] != 1 || cbias[im] != 0 || cbias[2] != 0) return false;
+    }
     const bool swap = buf[ia] == 2;
     char k[160];
-    snprintf(k, sizeof k, "tmpl:gemm;dtype=f32;epi=store;ta=%d;tb=%d;M=%lld;N=%lld;K=%lld%s", ta, tb, (long long)M,
-             (long long)N, (long long)K, swap ? ";swap_ab=1" : "");
+    snprintf(k, sizeof k, "tmpl:gemm;dtype=f32;epi=%s;ta=%d;tb=%d;M=%lld;N=%lld;K=%lld%s", bname.empty() ? "store" : "bias",
+             ta, tb, (long long)M, (long long)N, (long long)K, swap ? ";swap_ab=1" : "");
     *key = k;
     return true;
 }

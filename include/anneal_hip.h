@@ -79,8 +79,9 @@ int ah_module_get(ah_device *dev, const char *source, const char *entry, ah_kern
  * on its own (no device needed): writes at most cap bytes of NUL-terminated HIP source to out and the
  * full size to *needed; AH_ERR_COMPILE if the WGSL is outside the subset the reference emits. */
 int ah_translate_wgsl(const char *wgsl, char *out, int64_t cap, int64_t *needed);
-/* Template selection for a rendered WGSL kernel (host only, no device): when the kernel is a plain
- * contraction REDUCE(ADD, MUL(load, load)) of three f32 buffers whose load and store indices are affine
+/* Template selection for a rendered WGSL kernel (host only, no device): when the kernel is a contraction
+ * REDUCE(ADD, MUL(load, load)) of f32 buffers, stored as-is or plus a column bias (data3[n]: the Linear
+ * forward), whose load and store indices are affine
  * with zero offset (the scheduler's unsimplified index chains evaluated, codegen/lower.go:98-550 as
  * rendered by codegen/wgsl.go:36-238), writes the "tmpl:gemm;..." key ah_module_get runs in its place
  * (the MFMA contraction template) to buf; otherwise writes "". No counterpart in the reference, whose

@@ -53,3 +53,27 @@ def test_selected_contraction_matches_rendering(dev, monkeypatch, M, N, K, ta, t
         ref = Executor(d2).run([item], {1: A.ravel(), 2: B.ravel()})[30].reshape(M, N)
     assert np.abs(ref - want).max() / scale < 1e-5
     assert np.abs(got - ref).max() / scale < 1e-5
+
+
+@pytest.mark.parametrize("form", ["let", "inline"])
+def test_selected_bias_contraction_matches_rendering(dev, monkeypatch, form):
+    """The Linear forward with its bias (acc + b[n]) selected as tmpl:gemm epi=bias matches float64 and
+    the rendered kernel."""
+    from anneal_amd.backend import Device
+    M, N, K = 200, 136, 96
+    src, ws, wc = W.matmul_wgsl(M, N, K, bias=form)
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    want = A.astype(np.float64) @ B.astype(np.float64) + b
+    bufs = [Buffer(30, M * N, [M * N]), Buffer(1, A.size, [A.size]), Buffer(2, B.size, [B.size]), Buffer(3, N, [N])]
+    item = ExecItem(src, bufs, local_size=ws, workgroup_count=wc)
+    inp = {1: A.ravel(), 2: B.ravel(), 3: b}
+    got = Executor(dev).run([item], inp)[30].reshape(M, N)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() / scale < 1e-5
+    monkeypatch.setenv("AH_WGSL_TEMPLATES", "0")
+    with Device(0) as d2:
+        ref = Executor(d2).run([item], inp)[30].reshape(M, N)
+    assert np.abs(got - ref).max() / scale < 1e-5

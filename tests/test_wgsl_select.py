@@ -59,3 +59,14 @@ def test_malformed_or_other_forms_are_not_selected(mutate):
 def test_huge_axis_is_left_to_the_rendering():
     src, _, _ = W.matmul_wgsl(16, 16, 1 << 20)
     assert L.wgsl_template_key(src) == ""
+
+
+@pytest.mark.parametrize("form", ["let", "inline", "let_rev"])
+def test_bias_epilogue_is_selected(form):
+    src, _, _ = W.matmul_wgsl(64, 48, 32, bias=form)
+    assert L.wgsl_template_key(src) == "tmpl:gemm;dtype=f32;epi=bias;ta=0;tb=1;M=64;N=48;K=32"
+
+
+def test_bias_over_rows_is_not_a_column_bias():
+    src, _, _ = W.matmul_wgsl(64, 48, 32, bias="rows")
+    assert L.wgsl_template_key(src) == ""

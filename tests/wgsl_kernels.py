@@ -240,12 +240,14 @@ fn main(@builtin(global_invocation_id) gid: vec3<u32>) {
     return ks
 
 
-def matmul_wgsl(M, N, K, ta=False, tb=True, b_first=False, offset=0):
+def matmul_wgsl(M, N, K, ta=False, tb=True, b_first=False, offset=0, bias=None):
     """A contraction as the reference's codegen renders it (codegen/lower.go REDUCE(ADD, MUL(INDEX, INDEX))
     with the unsimplified index chains of schedule/index.go): out[m, n] = sum_k A(m, k) * B(k, n), A read
     from data1 ([M,K], or [K,M] with ta), B from data2 ([K,N] with tb, else [N,K]); with b_first the B load
-    is emitted first. offset shifts A's index (no longer a zero-offset contraction). Returns (wgsl,
-    bufs, local_size, workgroup_count) for the shapes of ExecItem."""
+    is emitted first. offset shifts A's index (no longer a zero-offset contraction). bias adds data3[n]
+    after the loop (Linear's forward epilogue, the add rendered "(a + b)" by codegen/wgsl.go:270):
+    "let" (a let of the sum), "inline" (the sum in the store), "let_rev" (bias first), "rows" (data3[m],
+    not a bias of the columns). Returns (wgsl, local_size, workgroup_count) for ExecItem."""
     ws = (64, 1, 1)
     wc = ((M * N + 63) // 64, 1, 1)
     if ta:   # A(m, k) at k*M + m, through a chain over the flat [K, M] view
@@ -261,7 +263,17 @@ def matmul_wgsl(M, N, K, ta=False, tb=True, b_first=False, offset=0):
     loads = [f"    let t9: f32 = data1[{ia}];", f"    let t12: f32 = data2[{ib}];"]
     if b_first:
         loads.reverse()
-    src = header(["f32", "f32", "f32"], ws, wc) + main_open(ws, wc) + [
+    post, store = [], "acc0"
+    if bias:
+        bi = f"(((r0 * {N}) + r1) / {N}) % {M}" if bias == "rows" else f"(((r0 * {N}) + r1) % {N})"
+        post = [f"  let t14: f32 = data3[{bi}];"]
+        add = "(t14 + acc0)" if bias == "let_rev" else "(acc0 + t14)"
+        if bias == "inline":
+            store = add
+        else:
+            post.append(f"  let t15: f32 = {add};")
+            store = "t15"
+    src = header(["f32", "f32", "f32"] + (["f32"] if bias else []), ws, wc) + main_open(ws, wc) + [
         f"  let r0: i32 = i32((flat_gid_x / {N}u) % {M}u);",
         f"  if (r0 >= {M}) {{ return; }}",
         f"  let r1: i32 = i32(flat_gid_x % {N}u);",
@@ -269,7 +281,7 @@ def matmul_wgsl(M, N, K, ta=False, tb=True, b_first=False, offset=0):
         "  var acc0: f32 = 0.0;",
         f"  for (var r2: i32 = 0; r2 < {K}; r2++) {{"] + loads + [
         "    acc0 = acc0 + (t9 * t12);",
-        "  }",
-        f"  data0[((r0 * {N}) + r1)] = acc0;",
+        "  }"] + post + [
+        f"  data0[((r0 * {N}) + r1)] = {store};",
         "}"]
     return "\n".join(src), ws, wc
