@@ -505,6 +505,19 @@ struct Mlp3Trainer : ah_trainer {
         launch_idx = 0;
         return rc;
     }
+    // Partial-row stride of a column-sum epilogue: its waves start at row multiples of their tile height
+    // (BM / WVM) and each stores the sum of its rows into row (first row / 32); with k-groups each group
+    // finishes 32 rows. variant: the variant it runs with (0: the tuned or default choice).
+    int colsum_stride(const GemmDesc &g, int variant) const {
+        int v = variant;
+        if (v == 0) {
+            auto it = dev->gemm_variant.find(tune_key(g));
+            v = it != dev->gemm_variant.end() ? it->second : gemm16_default_variant(g);
+        }
+        G16Params p;
+        if (!gemm16_variant_params(v, &p) || p.kg > 1) return 1;
+        return std::max(1, p.bm / p.wvm / 32);
+    }
     // Paired launches: for each pair, whole steps are timed with the two contractions launched apart
     // and paired with each pair variant (interleaved, three rounds, the best mean of 8 steps each), on
     // hash-filled parameters and data; the fastest is kept. The choice is cached under the pair's key
@@ -621,9 +634,14 @@ struct Mlp3Trainer : ah_trainer {
         }
         TailArgs ta{};
         const int R = rblocks();
-        ta.seg[0] = {b3, b3h, db3p(), sg ? gb3 : nullptr, D3, bs, R, D3};
-        ta.seg[1] = {b2, b2h, db2p(), sg ? gb2 : nullptr, D2, bs, R, D2};
-        ta.seg[2] = {b1, b1h, db1p(), sg ? gb1 : nullptr, D1, bs, R, D1};
+        // Each bias gradient's partial rows: one per 32-row block a wave of its producer starts (see
+        // colsum_stride), stored (not accumulated) on every step, so the tail reads just those rows and
+        // leaves them as they are.
+        const int s3 = colsum_stride(gemm(2, false), 0), s2 = colsum_stride(gemm(3, false), 0);
+        const int s1 = colsum_stride(gemm(5, false), pair_v[0]);
+        ta.seg[0] = {b3, b3h, db3p(), sg ? gb3 : nullptr, D3, bs, (R + s3 - 1) / s3, (long)D3 * s3, 1};
+        ta.seg[1] = {b2, b2h, db2p(), sg ? gb2 : nullptr, D2, bs, (R + s2 - 1) / s2, (long)D2 * s2, 1};
+        ta.seg[2] = {b1, b1h, db1p(), sg ? gb1 : nullptr, D1, bs, (R + s1 - 1) / s1, (long)D1 * s1, 1};
         ta.nseg = 3; ta.lr = lr; ta.loss_mode = 1; ta.lossacc = lossp(); ta.loss_parts = R * lblocks();
         ta.loss_scale = sc; ta.loss_out = loss; ta.loss_sum = sg ? lsum : nullptr;
         LAUNCH("tail", step_tail(ta, s));

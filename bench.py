@@ -44,9 +44,12 @@ def config_workload(cfg: int):
         f = lambda m, n, k: ("flop16", 2.0 * m * n * k)  # noqa: E731
         ks = [("fc1", *f(B, D1, D0)), ("fc2", *f(B, D2, D1)), ("fc3_mse", *f(B, D3, D2)), ("dH2", *f(B, D2, D3)),
               ("dW3", *f(D3, D2, B)), ("dH1", *f(B, D1, D2)), ("dW2", *f(D2, D1, B)), ("dW1", *f(D1, D0, B)),
-              # the tail's distinct bytes: R = B/32 partial rows of the three bias gradients and the
-              # R x D3/32 loss partials, each read and re-zeroed, then f32 bias read + write and f16 write
-              ("tail", "bytes", 8 * (B // 32) * (D1 + D2 + D3 + D3 // 32) + 10 * (D1 + D2 + D3))]
+              # the tail's distinct bytes: the partial rows of the bias gradients that the step's
+              # contractions write (every second of R = B/32 for db1 and db2 from the 64-row waves of
+              # the 256x256 tiles, all R for db3 from fc3's k-group tiles), read once; the R x D3/32 loss
+              # partials read and re-zeroed; then f32 bias read + write and f16 write
+              ("tail", "bytes", 4 * (B // 64) * (D1 + D2) + 4 * (B // 32) * D3 + 8 * (B // 32) * (D3 // 32)
+               + 10 * (D1 + D2 + D3))]
         meta = {"workload": "config3_f16_mlp_1024-4096-4096-1024_b4096_mse_sgd", "batch": B,
                 "flop_per_step": sum(a for _, k, a in ks if k.startswith("flop")), "dtype": "f16"}
         return L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], 1e-3, B, p, ks, meta
