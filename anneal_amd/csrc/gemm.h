@@ -51,7 +51,9 @@ struct GemmDesc {
     int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
     int variant;      // f16 kernel variant (0 = auto; table Var<V> in gemm16_kernel.h), the tuning hook
     int kgroups;      // f32 tiled kernel: wave sets splitting K (0 = auto, else 1 / 2 / 4 as the tile admits;
-                      // a fixed value also turns off the split of K across workgroups)
+                      // a fixed value also turns off the automatic split of K across workgroups)
+    int splits;       // f32 tiled kernel: workgroups splitting K per tile (0 = auto, 1 = none, else 2..16;
+                      // needs the split-K workspace below, without which there is no split)
     // Deterministic partial sums instead of atomics (0 = atomic accumulation into colsum[N] / lossacc[0]):
     // with colsum_ld > 0 each wave stores the column sums of its rows, which start at a multiple of 32,
     // to colsum[(row / 32) * colsum_ld + n]; with loss_ld > 0 each wave stores its MSE partial to
@@ -59,9 +61,9 @@ struct GemmDesc {
     // wave writes are left as they are, so the reader sums every entry and re-zeroes it.
     int colsum_ld;
     int loss_ld;
-    // Split-K workspace of the f32 tiled kernel (shapes with too few tiles for the CUs and a long K): one
-    // arrival counter and one ready counter per tile, zero between launches (the finishing workgroup
-    // resets them), then f32 partial tiles, sk_cap floats. Null: no split. Filled in by the dispatcher.
+    // Split-K workspace of the f32 tiled kernel (shapes with too few tiles for the CUs and a long K): two
+    // ints per tile, the first its arrival counter, zero between launches (the finishing workgroup
+    // resets it), then f32 partial tiles, sk_cap floats. Null: no split. Filled in by the dispatcher.
     int *sk_sync;
     float *sk_part;
     long sk_cap;

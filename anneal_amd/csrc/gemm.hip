@@ -300,60 +300,63 @@ __global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
             }
     }
     if (nsplit > 1) {
-        // Split-K finish. Each workgroup but the last to arrive stores group 0's accumulators as its
-        // split's partial (element-major, thread-minor: coalesced) with device-scope stores, which are
-        // coherent across the XCDs' L2s; the last (an arrival counter picks it, so no workgroup waits on
-        // one that has not started) folds the splits in split order, its own from registers, so the sum
-        // does not depend on the arrival order, and runs the epilogue.
-        constexpr int NE = FM * FN * 16;
+        // Split-K finish. Every split stores group 0's accumulators as its partial with 16-byte buffer
+        // stores and the sc1 cache policy (written through, so coherent across the XCDs' L2s), waits
+        // for them, and then takes a ticket from the tile's arrival counter; the split that draws the
+        // last ticket reads the others' partials the same way (sc1 loads miss in L2), adds all of them
+        // in split order (its own from registers, so the sum does not depend on the arrival order),
+        // resets the counter for the next launch and runs the epilogue. No workgroup waits on another.
+        // Partial layout: 16-byte chunk c of thread t at byte 16 * (c * kThreads + t) of its split.
+        constexpr int NC = FM * FN * 4;               // 16-byte chunks per thread
+        constexpr int PART = NC * kThreads * 16;      // bytes per split
+        constexpr int SC1 = 16;                       // cache policy bit sc1
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
         const int tile = tm * tiles_n + tn;
-        int *const sync = d.sk_sync + 2 * tile;
-        __shared__ int arrival;
-        if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        float *const part = d.sk_part + (long)tile * nsplit * (NE * kThreads) + tid;
-        if (arrival < nsplit - 1) {
-            if (kg == 0) {
-                float *const mine = part + (long)split * (NE * kThreads);
+        int *const count = d.sk_sync + 2 * tile;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            d.sk_part + (long)tile * nsplit * (PART / 4), (short)0, nsplit * PART, 0x00020000);
+        __shared__ int ticket;
+        if (kg == 0) {
 #pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++)
-                            __hip_atomic_store(mine + ((i * FN + j) * 16 + r) * kThreads, acc[i][j][r], __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's stores have completed
+            for (int c = 0; c < NC; c++) {
+                const floatx16 &a = acc[c / (FN * 4)][(c / 4) % FN];
+                const int e = (c % 4) * 4;
+                const floatx4 v = {a[e], a[e + 1], a[e + 2], a[e + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, split * PART + (c * kThreads + tid) * 16, 0, SC1);
+                // wait states before the store's data registers may be rewritten (the compiler has
+                // placed such a VALU write two instructions behind a 16-byte store, and it reached memory)
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("s_nop 4" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __syncthreads();
-            if (threadIdx.x == 0) __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's partial has landed
         }
-        // the partners have arrived, so they are running; the wait is bounded all the same
-        if (threadIdx.x == 0)
-            for (int spin = 0; spin < (1 << 22); spin++) {
-                if (__hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nsplit - 1) break;
-                __builtin_amdgcn_s_sleep(2);
-            }
         __syncthreads();
-        if (kg > 0) return;
+        if (threadIdx.x == 0) ticket = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (ticket != nsplit - 1 || kg > 0) return;
+        // every other split stored its partial before taking its ticket; add them in split order, one
+        // 32x32 block (4 chunks per split in flight) at a time
 #pragma unroll
-        for (int i = 0; i < FM; i++)
+        for (int bl = 0; bl < FM * FN; bl++) {
+            floatx16 &a = acc[bl / FN][bl % FN];
+            floatx4 sum[4];
+            for (int q = 0; q < nsplit; q++) {
+                floatx4 v[4];
 #pragma unroll
-            for (int j = 0; j < FN; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float *src = part + ((i * FN + j) * 16 + r) * kThreads;
-                    float v = split == 0 ? acc[i][j][r] : __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    for (int q = 1; q < nsplit; q++)
-                        v += q == split ? acc[i][j][r]
-                                        : __hip_atomic_load(src + (long)q * (NE * kThreads), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    acc[i][j][r] = v;
+                for (int u = 0; u < 4; u++) {
+                    if (q == split) v[u] = (floatx4){a[4 * u], a[4 * u + 1], a[4 * u + 2], a[4 * u + 3]};
+                    else v[u] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, q * PART + ((bl * 4 + u) * kThreads + tid) * 16, 0, SC1));
                 }
-        if (threadIdx.x == 0) {   // ready for the next launch
-            __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int u = 0; u < 4; u++) sum[u] = q == 0 ? v[u] : sum[u] + v[u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int x = 0; x < 4; x++) a[4 * u + x] = sum[u][x];
         }
+        if (threadIdx.x == 0) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
     }
     if (kg > 0) return;
     epilogue_tile<EPI, T, FM, FN>(d, acc, m0 + wm0, n0 + wn0, lane);
@@ -364,25 +367,25 @@ static hipError_t launch_t(const GemmDesc &d, hipStream_t s) {
     const int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
     constexpr int VEC = 16 / sizeof(T), BK = 8 * VEC;
     const int nk = (d.K + BK - 1) / BK;
-    // k-groups: each of a tile's register-staged K iterations waits on its global loads, so long K
-    // loops over few waves are latency bound. Add wave sets (each taking a share of K) while there
-    // are at most 4 workgroups' worth per CU and every group keeps at least 4 chunks
-    // (LDS: 64-tile 4 groups 128 KiB, 128-tile 2 groups 128 KiB).
-    int kg = 1;
+    // Each k-group of a tile (4 waves) runs a register-staged K loop whose iterations wait on their
+    // global loads, so short-output, long-K contractions are latency bound on few waves. The automatic
+    // choice gives such shapes more wave sets on each tile: k-groups (within one workgroup, up to the
+    // tile's LDS budget: 64-tile 4 groups, 128-tile 2) and then splits of K across workgroups (partials
+    // folded by the last split to arrive), doubling either while the tile's wave sets stay within 1024
+    // (four per CU) and each set keeps at least 2 K chunks.
+    int kg = 1, split = 1;
+    const bool ws = d.sk_sync && d.sk_part && tiles <= kSplitKMaxTiles;
     if (d.kgroups > 0 && gemm32_kgroups_ok(BM, d.kgroups)) {
-        kg = d.kgroups;   // fixed by the caller (a BEAM candidate)
-    } else if (BM <= 128) {
-        const int maxkg = BM == 64 ? 4 : 2;
-        while (kg < maxkg && tiles * kg <= 1024 && nk >= 8 * kg) kg *= 2;   // at least 4 chunks per group
+        kg = d.kgroups;   // fixed by the caller (a tuner candidate)
+    } else {
+        const int maxkg = BM == 64 ? 4 : BM == 128 ? 2 : 1;
+        while (kg < maxkg && (long)tiles * kg * 2 <= 1024 && nk >= 2 * kg * 2) kg *= 2;
     }
-    // Split-K across workgroups only where the tiles (times their k-groups) leave most CUs idle and each
-    // group still runs a long K loop (16 chunks or more): the partials' device-scope round trip and the
-    // last workgroup's wait cost a few microseconds, which only a long loop pays back. Up to 16 splits,
-    // about 512 workgroups, at least 4 chunks per group.
-    int split = 1;
-    if (d.sk_sync && d.sk_part && d.kgroups == 0 && tiles <= kSplitKMaxTiles && (long)tiles * kg <= 128 &&
-        nk >= 16 * kg) {
-        while (split < 16 && (long)tiles * kg * split * 2 <= 512 && nk >= 4 * kg * split * 2 &&
+    if (ws && d.splits > 1) {
+        split = d.splits > 16 ? 16 : d.splits;   // fixed by the caller (a tuner candidate)
+        while (split > 1 && (long)tiles * split * BM * BM > d.sk_cap) split >>= 1;
+    } else if (ws && d.splits == 0 && d.kgroups == 0) {
+        while (split < 16 && (long)tiles * kg * split * 2 <= 1024 && nk >= 2 * kg * split * 2 &&
                (long)tiles * split * 2 * BM * BM <= d.sk_cap)
             split *= 2;
     }
