@@ -177,6 +177,8 @@ int template_gemm(const Params &P, TemplateKernel *t) {
         return set_error(AH_ERR_INVALID, "tmpl gemm: tile %d", base.tile);
     if (base.kgroups != 0 && !(base.tile != 0 && gemm32_kgroups_ok(base.tile, base.kgroups)))
         return set_error(AH_ERR_INVALID, "tmpl gemm: kg=%d needs a tile that admits it", base.kgroups);
+    base.splits = (int)P.integer("splits", 0);
+    if (base.splits < 0 || base.splits > 16) return set_error(AH_ERR_INVALID, "tmpl gemm: splits=%d (0..16)", base.splits);
     const bool swap_ab = P.integer("swap_ab", 0) != 0;
     const int nbuf = (base.epi == EPI_STORE || grad) ? 3 : base.epi == EPI_MSE ? 6 : 4;
     if (base.epi == EPI_MSE) t->side = {{5, true}};

@@ -294,3 +294,44 @@ def test_gemm_tune_disk_cache(dev, tmp_path):
         dev.gemm_tune_cache(str(bad), False)
     for b in (dA, dB, dC):
         b.free()
+
+
+@pytest.mark.parametrize("splits", [0, 1, 2, 4, 8, 16])
+@pytest.mark.parametrize("epi", ["store", "bias_relu", "mask", "grad"])
+def test_gemm_f32_split_k(dev, epi, splits):
+    """The f32 tiled kernel with K split across workgroups (splits=s fixes the count, 0 lets the shape
+    choose: 4 k-groups x 8 splits here): partials folded in split order by the last split to arrive, so
+    every launch gives the same bits, and each launch leaves the tiles' arrival counters at zero for the
+    next (checked by a second launch on other inputs)."""
+    from anneal_amd.executor import Buffer, ExecItem, Executor
+    M, N, K, ta, tb = (256, 512, 2048, 0, 0) if epi != "grad" else (512, 256, 2048, 1, 1)
+    key = f"tmpl:gemm;dtype=f32;epi={epi};ta={ta};tb={tb};M={M};N={N};K={K};tile=64;splits={splits}"
+    if splits == 0:
+        key = f"tmpl:gemm;dtype=f32;epi={epi};ta={ta};tb={tb};M={M};N={N};K={K}"
+    bufs = [Buffer(10, M * N, [M, N], L.AH_F32), Buffer(1, M * K, [K, M] if ta else [M, K], L.AH_F32),
+            Buffer(2, N * K, [K, N] if tb else [N, K], L.AH_F32)]
+    if epi in ("bias_relu", "mask"):
+        bufs.append(Buffer(3, N if epi == "bias_relu" else M * N, [N] if epi == "bias_relu" else [M, N], L.AH_F32))
+    ex = Executor(dev)
+    prev = None
+    for rep in range(2):
+        rng = np.random.default_rng(1000 + rep)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K)).astype(np.float32)
+        ins = {1: store_operand(A, ta).ravel(), 2: store_operand(B, tb).ravel()}
+        ref = A.astype(np.float64) @ B.astype(np.float64).T
+        if epi == "bias_relu":
+            bias = rng.standard_normal(N).astype(np.float32)
+            ins[3] = bias
+            ref = np.maximum(ref + bias, 0)
+        elif epi == "mask":
+            H = rng.standard_normal((M, N)).astype(np.float32)
+            H = np.where(H < 0, np.float32(-0.0), H).astype(np.float32)
+            ins[3] = H.ravel()
+            ref = np.where(np.signbit(H) & (H == 0), 0.0, ref)
+        got = ex.run([ExecItem(key, bufs)], ins)[10].reshape(M, N)
+        assert O.relerr(got, ref) < 1e-5, (epi, splits, rep)
+        again = ex.run([ExecItem(key, bufs)], ins)[10].reshape(M, N)
+        np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
+        assert prev is None or not np.array_equal(prev, got)
+        prev = got
