@@ -185,6 +185,7 @@ static GemmDesc gdesc(int dtype, int epi, int ta, int tb, int M, int N, int K, c
 struct MlpCeTrainer : ah_trainer {
     int Bmax, D, H, C;
     float *x, *W1, *b1, *W2, *b2, *H1, *Z2, *dZ2, *dZ1, *rowloss, *acc, *loss, *gW1, *gb1, *gW2, *gb2;
+    float *dbpart = nullptr;   // softmax_ce_cols' partial rows of the output bias gradient (C <= kSoftmaxColsMaxC)
     int32_t *lab;
     bool fused = false;   // the three-kernel step of mlpce.h
     int init() {
@@ -197,6 +198,7 @@ struct MlpCeTrainer : ah_trainer {
         rc |= alloc(&dZ1, (size_t)Bmax * H); rc |= alloc(&rowloss, Bmax); rc |= alloc(&acc, H + C);
         rc |= alloc(&loss, 1); rc |= alloc(&gW1, (size_t)H * D); rc |= alloc(&gb1, H);
         rc |= alloc(&gW2, (size_t)C * H); rc |= alloc(&gb2, C);
+        if (C <= kSoftmaxColsMaxC) rc |= alloc(&dbpart, (size_t)softmax_ce_cols_blocks(Bmax) * C);
         fused = mlpce_fused_ok(Bmax, D, H, C);
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * (H + C)));
@@ -246,8 +248,12 @@ struct MlpCeTrainer : ah_trainer {
         GemmDesc g2 = gdesc(GEMM_F32, EPI_BIAS, 0, 0, B, C, H, H1, H, W2, H, Z2, C);
         g2.bias = b2;
         LAUNCH("fc2", gemm_run(dev, g2, s));
-        LAUNCH("softmax_ce", softmax_ce(Z2, lab, B, C, a, dZ2, rowloss, s));
-        LAUNCH("db2", colsum_add(dZ2, B, C, C, db2, s));
+        if (dbpart) {
+            LAUNCH("softmax_ce", softmax_ce_cols(Z2, lab, B, C, a, dZ2, rowloss, dbpart, s));
+        } else {
+            LAUNCH("softmax_ce", softmax_ce(Z2, lab, B, C, a, dZ2, rowloss, s));
+            LAUNCH("db2", colsum_add(dZ2, B, C, C, db2, s));
+        }
         GemmDesc g3 = gdesc(GEMM_F32, EPI_MASK, 0, 1, B, H, C, dZ2, C, W2, H, dZ1, H);
         g3.aux = H1; g3.ldaux = H; g3.colsum = db1;
         LAUNCH("dH1", gemm_run(dev, g3, s));
@@ -259,6 +265,12 @@ struct MlpCeTrainer : ah_trainer {
         LAUNCH("dW1", gemm_run(dev, g5, s));
         TailArgs ta{};
         ta.seg[0] = {b2, nullptr, db2, sg ? gb2 : nullptr, C, 1.0f};
+        if (dbpart) {   // the bias gradient as softmax_ce_cols' partial rows, rewritten every step
+            ta.seg[0].acc = dbpart;
+            ta.seg[0].acc_rows = softmax_ce_cols_blocks(B);
+            ta.seg[0].acc_ld = C;
+            ta.seg[0].keep = 1;
+        }
         ta.seg[1] = {b1, nullptr, db1, sg ? gb1 : nullptr, H, 1.0f};
         ta.nseg = 2; ta.lr = lr; ta.loss_mode = 2; ta.loss_scale = a; ta.rowloss = rowloss; ta.nrow = B; ta.loss_out = loss;
         LAUNCH("tail", step_tail(ta, s));

@@ -16,6 +16,13 @@ hipError_t cast_f32_f16(const float *src, half_t *dst, long n, hipStream_t s);
 hipError_t sgd_update(float *p, const float *g, long n, float lr, float scale, half_t *p16, float *gout,
                       hipStream_t s);
 hipError_t colsum_add(const float *G, int M, int N, long ld, float *out, hipStream_t s);
+// softmax_ce plus the column sums of dz as partial rows part[softmax_ce_cols_blocks(B)][C] (each row
+// rewritten by every call; their row-order sum is the output bias gradient). C <= kSoftmaxColsMaxC.
+constexpr int kSoftmaxColsMaxC = 1024;
+constexpr int kSoftmaxColsMaxBlocks = 256;
+int softmax_ce_cols_blocks(int B);
+hipError_t softmax_ce_cols(const float *z, const int32_t *labels, int B, int C, float a, float *dz, float *rowloss,
+                           float *part, hipStream_t s);
 hipError_t softmax_ce(const float *z, const int32_t *labels, int B, int C, float a, float *dz, float *rowloss,
                       hipStream_t s);
 hipError_t sum_scale(const float *v, int n, float a, float *out, hipStream_t s);

@@ -89,6 +89,30 @@ __global__ __launch_bounds__(256) void softmax_ce_kernel(const float *z, const i
     if (lane == 0) rowloss[row] = rl;
 }
 
+// Softmax-CE with the logit gradient's column sums (the output bias gradient) fused in: each wave
+// takes rows blockIdx.x * 4 + wave, then every 4 * gridDim.x rows further, holding each row in
+// registers, and keeps the column sums of its rows' dz in registers; the block's four waves add theirs
+// in wave order into partial row blockIdx.x of part[gridDim.x][C] (summed in row order by the step's
+// tail), so the result does not depend on timing.
+template <int VPR>
+__global__ __launch_bounds__(256) void softmax_ce_cols_kernel(const float *z, const int32_t *labels, int B, int C,
+                                                               float a, float *dz, float *rowloss, float *part) {
+    __shared__ float red[4][64 * VPR];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float col[VPR];
+#pragma unroll
+    for (int j = 0; j < VPR; j++) col[j] = 0.0f;
+    for (int row = blockIdx.x * 4 + wave; row < B; row += gridDim.x * 4) {
+        const float rl = softmax_ce_row_regs<VPR>(z + (long)row * C, labels[row], C, a, dz + (long)row * C, lane, col);
+        if (lane == 0) rowloss[row] = rl;
+    }
+#pragma unroll
+    for (int j = 0; j < VPR; j++) red[wave][lane + 64 * j] = col[j];
+    __syncthreads();
+    for (int c = threadIdx.x; c < C; c += 256)
+        part[(long)blockIdx.x * C + c] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
+}
+
 // out[0] = (Sum_i v[i]) * a   (single block, fixed-order tree)
 __global__ __launch_bounds__(256) void sum_scale_kernel(const float *v, int n, float a, float *out) {
     __shared__ float red[256];
@@ -718,6 +742,22 @@ hipError_t softmax_ce(const float *z, const int32_t *labels, int B, int C, float
                       hipStream_t s) {
     if (B <= 0) return hipSuccess;
     hipLaunchKernelGGL(softmax_ce_kernel, dim3((B + 3) / 4), dim3(256), 0, s, z, labels, B, C, a, dz, rowloss);
+    return hipGetLastError();
+}
+int softmax_ce_cols_blocks(int B) {
+    const int b = (B + 3) / 4;
+    return b < kSoftmaxColsMaxBlocks ? (b < 1 ? 1 : b) : kSoftmaxColsMaxBlocks;
+}
+hipError_t softmax_ce_cols(const float *z, const int32_t *labels, int B, int C, float a, float *dz, float *rowloss,
+                           float *part, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    const dim3 grid(softmax_ce_cols_blocks(B)), block(256);
+    if (C <= 64) hipLaunchKernelGGL(softmax_ce_cols_kernel<1>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
+    else if (C <= 128) hipLaunchKernelGGL(softmax_ce_cols_kernel<2>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
+    else if (C <= 256) hipLaunchKernelGGL(softmax_ce_cols_kernel<4>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
+    else if (C <= 512) hipLaunchKernelGGL(softmax_ce_cols_kernel<8>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
+    else if (C <= kSoftmaxColsMaxC) hipLaunchKernelGGL(softmax_ce_cols_kernel<16>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 hipError_t sum_scale(const float *v, int n, float a, float *out, hipStream_t s) {

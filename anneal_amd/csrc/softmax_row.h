@@ -50,4 +50,60 @@ __device__ __forceinline__ float softmax_ce_row(const float *zr, int lab, int C,
     return rl;
 }
 
+// softmax_ce_row with the row held in registers: VPR values per lane (C <= 64 * VPR), lane l holding
+// columns l, l + 64, ... in order, so every per-lane sum adds the same terms in the same order as
+// softmax_ce_row and each result has the same bits. Writes the row's dz and adds it to col[j] (the
+// running column sums of the rows this wave handles); returns the row's log-probability of its label.
+template <int VPR>
+__device__ __forceinline__ float softmax_ce_row_regs(const float *zr, int lab, int C, float a, float *dz, int lane,
+                                                     float (&col)[VPR]) {
+#pragma clang fp contract(off)
+    float v[VPR], e[VPR];
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < VPR; j++) {
+        const int c = lane + 64 * j;
+        v[j] = c < C ? zr[c] : -FLT_MAX;
+        m = fmaxf(m, v[j]);
+    }
+    m = wave_max(m);
+    float tie = 0.0f, s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPR; j++) {
+        e[j] = exp2f((v[j] - m) * AH_INV_LN2);
+        if (lane + 64 * j < C) {
+            tie += (v[j] == m) ? 1.0f : 0.0f;
+            s += e[j];
+        }
+    }
+    tie = wave_sum(tie);
+    s = wave_sum(s);
+    float ls = log2f(s) * AH_LN2;
+    const float rl = (lab >= 0 && lab < C) ? ((zr[lab] - m) - ls) : 0.0f;
+    float gls = (lab >= 0 && lab < C) ? -a : 0.0f;
+    float glog2 = gls * AH_LN2;
+    float gs = glog2 * (1.0f / (s * AH_LN2));
+    float gm = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPR; j++) {
+        const int c = lane + 64 * j;
+        float glogp = (c == lab) ? a : 0.0f;
+        e[j] = glogp + ((gs * e[j]) * AH_LN2) * AH_INV_LN2;   // the row's gzs
+        if (c < C) gm += -e[j];
+    }
+    gm = wave_sum(gm);
+    float share = gm * (1.0f / tie);
+#pragma unroll
+    for (int j = 0; j < VPR; j++) {
+        const int c = lane + 64 * j;
+        if (c < C) {
+            float d = e[j];
+            if (v[j] == m) d += share;
+            dz[c] = d;
+            col[j] += d;
+        }
+    }
+    return rl;
+}
+
 }  // namespace ah
