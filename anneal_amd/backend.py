@@ -93,14 +93,15 @@ class Device:
         L.check(self.lib.ah_gemm(self.h, C.byref(d)))
 
     def gemm_tune(self, iterations: int = 3, **kw):
-        """Times every f16 variant of the contraction and caches the fastest; returns (variant, mean us)."""
+        """Times every f16 variant (or f32 configuration) of the contraction and caches the fastest;
+        returns (variant or configuration index, mean us)."""
         d = self._gemm_desc(**kw)
         v, us = C.c_int32(), C.c_double()
         L.check(self.lib.ah_gemm_tune(self.h, C.byref(d), iterations, C.byref(v), C.byref(us)))
         return v.value, us.value
 
     def gemm_tune_cache(self, path: str, save: bool) -> None:
-        """Saves the tuned f16 variant choices to path, or merges a saved file into this device's cache."""
+        """Saves the tuned f16 variants and f32 configurations to path, or merges a saved file into this device's cache."""
         L.check(self.lib.ah_gemm_tune_cache(self.h, str(path).encode(), 1 if save else 0))
 
     def softmax_ce(self, z: DeviceBuffer, labels: DeviceBuffer, B: int, Cn: int, dz: DeviceBuffer,

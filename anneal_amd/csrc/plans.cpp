@@ -12,6 +12,8 @@
 
 #include <algorithm>
 #include <map>
+#include <set>
+#include <vector>
 
 #include "ah_internal.h"
 #include "conv.h"
@@ -46,6 +48,8 @@ struct ah_trainer {
     virtual int set(int slot, const void *host, int64_t n) = 0;
     virtual int get(int slot, void *host, int64_t n) = 0;
     virtual int enqueue(int64_t batch, int flags) = 0;
+    // Work before a batch's first step, outside any capture (tuning); called before every step.
+    virtual int prepare(int64_t) { return AH_OK; }
     virtual int max_batch() const { return (int)dims[0]; }
 
     template <class T>
@@ -117,12 +121,42 @@ static std::string tune_key(const GemmDesc &g) {
     return b;
 }
 
-// Launch with the tuned variant when the caller left the choice open, and with the device's split-K
-// workspace (used by the f32 tiled kernel for shapes with few tiles and a long K).
+// Configurations of the f32 tiled kernel the tuner times: (tile, k-groups, splits), 0 meaning the
+// shape's automatic choice of that parameter; entry 0 leaves all three to the shape. A fixed k-group
+// count with splits 0 runs without a split of K across workgroups.
+struct F32Cfg {
+    int tile, kg, splits;
+};
+static const std::vector<F32Cfg> &f32_cfgs() {
+    static const std::vector<F32Cfg> v = [] {
+        std::vector<F32Cfg> c{{0, 0, 0}};
+        for (int tile : {64, 128})
+            for (int kg : {0, 1, 2, 4}) {
+                if (kg && !gemm32_kgroups_ok(tile, kg)) continue;
+                for (int sp : {0, 1, 2, 4, 8, 16}) {
+                    if (kg && sp == 0) continue;   // the same launch as splits 1
+                    c.push_back({tile, kg, sp});
+                }
+            }
+        return c;
+    }();
+    return v;
+}
+
+// Launch with the tuned variant (f16) or configuration (f32) when the caller left the choice open, and
+// with the device's split-K workspace (used by the f32 tiled kernel for shapes with few tiles and a
+// long K).
 static hipError_t gemm_run(ah_device *dev, GemmDesc g, hipStream_t s) {
     if (g.variant == 0 && g.dtype == GEMM_F16) {
         auto it = dev->gemm_variant.find(tune_key(g));
         if (it != dev->gemm_variant.end()) g.variant = it->second;
+    }
+    if (g.dtype == GEMM_F32 && g.tile == 0 && g.kgroups == 0 && g.splits == 0) {
+        auto it = dev->gemm_variant.find(tune_key(g));
+        if (it != dev->gemm_variant.end() && it->second > 0 && it->second < (int)f32_cfgs().size()) {
+            const F32Cfg &c = f32_cfgs()[it->second];
+            g.tile = c.tile; g.kgroups = c.kg; g.splits = c.splits;
+        }
     }
     if (dev->splitk_ws) {
         const size_t sync_bytes = (size_t)kSplitKMaxTiles * 2 * sizeof(int);
@@ -138,8 +172,10 @@ hipError_t ah::gemm_dispatch(ah_device *dev, const GemmDesc &g) { return gemm_ru
 // Times every f16 variant of g (as given: its epilogue runs on whatever outputs g names) and caches
 // the fastest for g's shape. Two passes over the variants, each variant's time the lower of its two
 // means of `iters` launches, so one disturbed measurement does not decide the choice.
+static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us);
 static int tune_gemm(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us) {
-    if (g.dtype != GEMM_F16) return set_error(AH_ERR_UNSUPPORTED, "gemm tuning covers the f16 kernels");
+    if (g.dtype == GEMM_F32) return tune_gemm_f32(dev, g, iters, best, best_us);
+    if (g.dtype != GEMM_F16) return set_error(AH_ERR_UNSUPPORTED, "gemm tuning covers the f16 and f32 kernels");
     if (iters <= 0) return set_error(AH_ERR_INVALID, "gemm tuning: iterations must be > 0");
     hipEvent_t e0, e1;
     AH_HIP(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence));   // timing only
@@ -165,6 +201,49 @@ static int tune_gemm(ah_device *dev, GemmDesc g, int iters, int *best, double *b
     int bv = 1;
     for (int v = 2; v <= kGemm16Variants; v++)
         if (t[v] < t[bv]) bv = v;
+    dev->gemm_variant[tune_key(g)] = bv;
+    if (best) *best = bv;
+    if (best_us) *best_us = t[bv] * 1000.0 / iters;
+    return AH_OK;
+}
+
+// The f32 counterpart: times every configuration of f32_cfgs() the same way (two passes, the lower of
+// each configuration's two means) and caches the fastest one's index for g's shape (0: the automatic
+// choice). Configurations add K in different orders, so results differ at the rounding level.
+static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us) {
+    if (iters <= 0) return set_error(AH_ERR_INVALID, "gemm tuning: iterations must be > 0");
+    const std::vector<F32Cfg> &cfgs = f32_cfgs();
+    if (dev->splitk_ws) {
+        const size_t sync_bytes = (size_t)kSplitKMaxTiles * 2 * sizeof(int);
+        g.sk_sync = (int *)dev->splitk_ws;
+        g.sk_part = (float *)((char *)dev->splitk_ws + sync_bytes);
+        g.sk_cap = kSplitKPartFloats;
+    }
+    hipEvent_t e0, e1;
+    AH_HIP(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence));   // timing only
+    AH_HIP(hipEventCreateWithFlags(&e1, hipEventDisableSystemFence));
+    std::vector<float> t(cfgs.size(), 0.0f);
+    hipError_t err = hipSuccess;
+    for (int pass = 0; pass < 2 && err == hipSuccess; pass++) {
+        for (size_t v = 0; v < cfgs.size() && err == hipSuccess; v++) {
+            g.tile = cfgs[v].tile; g.kgroups = cfgs[v].kg; g.splits = cfgs[v].splits;
+            err = gemm_launch(g, dev->stream);
+            if (err == hipSuccess) err = hipEventRecord(e0, dev->stream);
+            for (int i = 0; i < iters && err == hipSuccess; i++) err = gemm_launch(g, dev->stream);
+            if (err == hipSuccess) err = hipEventRecord(e1, dev->stream);
+            if (err == hipSuccess) err = hipEventSynchronize(e1);
+            float ms = 0.0f;
+            if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+            if (err == hipSuccess && (pass == 0 || ms < t[v])) t[v] = ms;
+        }
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (err != hipSuccess) return fail_hip(err, "gemm tuning (f32)");
+    int bv = 0;
+    for (size_t v = 1; v < cfgs.size(); v++)
+        if (t[v] < t[bv]) bv = (int)v;
+    g.tile = g.kgroups = g.splits = 0;
     dev->gemm_variant[tune_key(g)] = bv;
     if (best) *best = bv;
     if (best_us) *best_us = t[bv] * 1000.0 / iters;
@@ -218,6 +297,31 @@ struct MlpCeTrainer : ah_trainer {
         if (slot < 0 || slot > 10) return set_error(AH_ERR_INVALID, "MLP_CE: bad slot %d", slot);
         if (n > t[slot].n) return set_error(AH_ERR_INVALID, "MLP_CE: slot %d too small", slot);
         return copy_out(dev, h, t[slot].p, (size_t)n * 4);
+    }
+    // Before a batch's first GEMM-based step: tune each f32 contraction's (tile, k-groups, splits) for
+    // shapes the device has not tuned. Each runs with its own epilogue into buffers the step rewrites
+    // (the weight updates into the gradient outputs, with lr 0); the bias-gradient accumulator it
+    // touches is re-zeroed.
+    std::set<int> tuned;
+    int prepare(int64_t batch) override {
+        const int B = (int)batch;
+        if (fused || mlp_small_ok(B, D, H, C) || tuned.count(B)) return AH_OK;
+        GemmDesc g[5] = {gdesc(GEMM_F32, EPI_BIAS_RELU, 0, 0, B, H, D, x, D, W1, D, H1, H),
+                         gdesc(GEMM_F32, EPI_BIAS, 0, 0, B, C, H, H1, H, W2, H, Z2, C),
+                         gdesc(GEMM_F32, EPI_MASK, 0, 1, B, H, C, dZ2, C, W2, H, dZ1, H),
+                         gdesc(GEMM_F32, EPI_SGD, 1, 1, C, H, B, dZ2, C, H1, H, nullptr, H),
+                         gdesc(GEMM_F32, EPI_SGD, 1, 1, H, D, B, dZ1, H, x, D, nullptr, D)};
+        g[0].bias = b1;
+        g[1].bias = b2;
+        g[2].aux = H1; g[2].ldaux = H; g[2].colsum = acc;
+        g[3].W32 = gW2; g[3].lr = 0.0f;
+        g[4].W32 = gW1; g[4].lr = 0.0f;
+        for (GemmDesc &d : g)
+            if (!dev->gemm_variant.count(tune_key(d)))
+                if (int rc = tune_gemm(dev, d, 3, nullptr, nullptr)) return rc;
+        AH_HIP(hipMemsetAsync(acc, 0, sizeof(float) * (H + C), dev->stream));
+        tuned.insert(B);
+        return AH_OK;
     }
     int enqueue(int64_t batch, int flags) override {
         const int B = (int)batch;
@@ -839,6 +943,7 @@ int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags) {
     if (!t) return set_error(AH_ERR_INVALID, "ah_trainer_step: null trainer");
     if (batch <= 0 || batch > t->max_batch())
         return set_error(AH_ERR_INVALID, "ah_trainer_step: batch %lld outside [1, %d]", (long long)batch, t->max_batch());
+    if (int rc = t->prepare(batch)) return rc;
     if (flags & AH_STEP_GRAPH) {
         // one graph per (batch, gradient-output choice): the two capture different kernels' arguments
         const int64_t key = batch * 2 + ((flags & AH_STEP_STORE_GRADS) ? 1 : 0);
@@ -966,8 +1071,11 @@ int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save) {
         }
         char key[128];
         int v = 0;
-        const bool pair = sscanf(line, "%127s %d", key, &v) == 2 && strncmp(key, "pair", 4) == 0;
-        const bool ok = pair ? (v == 0 || v == 27 || v == 30) : v >= 1 && v <= kGemm16Variants;
+        const bool parsed = sscanf(line, "%127s %d", key, &v) == 2;
+        const bool pair = parsed && strncmp(key, "pair", 4) == 0;
+        const bool f32 = parsed && strncmp(key, "0/", 2) == 0;   // tune_key: dtype first
+        const bool ok = pair ? (v == 0 || v == 27 || v == 30)
+                        : f32 ? v >= 0 && v < (int)f32_cfgs().size() : v >= 1 && v <= kGemm16Variants;
         if (sscanf(line, "%127s %d", key, &v) != 2 || !ok) {
             rc = set_error(AH_ERR_INVALID, "gemm tune cache %s: bad line %d", path, lineno);
             break;
@@ -982,12 +1090,12 @@ int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save) {
 
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us) {
     if (!dev || !d) return set_error(AH_ERR_INVALID, "ah_gemm_tune: null argument");
-    if (d->dtype != AH_F16) return set_error(AH_ERR_UNSUPPORTED, "ah_gemm_tune: f16 contractions only");
+    if (d->dtype != AH_F16 && d->dtype != AH_F32) return set_error(AH_ERR_UNSUPPORTED, "ah_gemm_tune: f16 and f32 contractions only");
     if (d->M <= 0 || d->N <= 0 || d->K <= 0 || !d->A || !d->B) return set_error(AH_ERR_INVALID, "ah_gemm_tune: bad shape/pointer");
     if (d->epi == AH_EPI_SGD ? !d->W32 : !d->C) return set_error(AH_ERR_INVALID, "ah_gemm_tune: missing output");
     GemmDesc g;
     memset(&g, 0, sizeof g);
-    g.dtype = GEMM_F16;
+    g.dtype = d->dtype == AH_F16 ? GEMM_F16 : GEMM_F32;
     g.epi = d->epi; g.ta = d->ta; g.tb = d->tb; g.M = d->M; g.N = d->N; g.K = d->K;
     g.A = d->A; g.B = d->B; g.lda = d->lda; g.ldb = d->ldb; g.C = d->C; g.ldc = d->ldc; g.bias = d->bias;
     g.aux = d->aux; g.ldaux = d->ldaux; g.scale = d->scale; g.colsum = d->colsum; g.W32 = d->W32; g.W16 = d->W16;

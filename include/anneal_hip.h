@@ -211,7 +211,13 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * (the epilogue runs 2 * (iterations + 1) times per variant). Variants without k-groups differ only in
  * tiling and scheduling and accumulate each output over k in the same order (bit-identical results);
  * the k-group variants 10, 11, 15, 25, 28 and 31 add two k-halves, which rounds differently in f32 (relative
- * 1e-6 level). */
+ * 1e-6 level). For an f32 contraction (dtype AH_F32) the candidates are the f32 kernel's (tile, k-groups,
+ * splits of K across workgroups) configurations, 38 of them, and *best_variant is the winner's index:
+ * 0 is the shape's automatic choice, then tile 64 and 128 each with k-groups auto / 1 / 2 / 4 (as the
+ * tile admits) and splits auto / 1 / 2 / 4 / 8 / 16 in that nesting order (a fixed k-group count takes
+ * no automatic split, so splits auto is listed only with k-groups auto). Later f32 launches of the shape
+ * with tile, k-groups and splits all automatic use it. Configurations add K in different orders, so
+ * their results differ at the rounding level. */
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us);
 /* BEAM's disk cache (codegen/beam.go:118-169): save (save != 0) the device's tuned choices to path, one
  * "dtype/ta/tb/M/N/K variant" line each under a header naming the gfx arch, or merge a saved file into

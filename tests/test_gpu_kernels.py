@@ -335,3 +335,32 @@ def test_gemm_f32_split_k(dev, epi, splits):
         np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
         assert prev is None or not np.array_equal(prev, got)
         prev = got
+
+
+def test_gemm_f32_tune_and_cache(dev, tmp_path):
+    """The tuner over the f32 kernel's (tile, k-groups, splits) configurations: it returns an index into
+    the 38-entry table, later automatic launches of the shape use the winner (against float64), and the
+    choice survives the disk cache, where an index past the table is rejected."""
+    M, N, K = 256, 512, 2048
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    B = RNG.standard_normal((N, K)).astype(np.float32)
+    dA, dB = dev.buffer(A), dev.buffer(B)
+    dC = dev.buffer(M * N, L.AH_F32)
+    common = dict(dtype=L.AH_F32, epi=L.EPI_STORE, ta=0, tb=0, M=M, N=N, K=K, A=dA, B=dB, lda=K, ldb=K, C_out=dC,
+                  ldc=N)
+    best, us = dev.gemm_tune(iterations=2, **common)
+    assert 0 <= best < 38 and us > 0
+    dev.gemm(**common)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    assert O.relerr(dC.read().reshape(M, N), ref) < 1e-5
+    path = tmp_path / "tune32.txt"
+    dev.gemm_tune_cache(str(path), True)
+    lines = path.read_text().splitlines()
+    assert f"0/0/0/{M}/{N}/{K} {best}" in lines
+    dev.gemm_tune_cache(str(path), False)
+    bad = tmp_path / "bad32.txt"
+    bad.write_text(lines[0] + f"\n0/0/0/{M}/{N}/{K} 38\n")
+    with pytest.raises(L.AnnealHipError, match="bad line"):
+        dev.gemm_tune_cache(str(bad), False)
+    for b in (dA, dB, dC):
+        b.free()
