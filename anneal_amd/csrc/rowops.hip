@@ -102,8 +102,18 @@ __global__ __launch_bounds__(256) void softmax_ce_cols_kernel(const float *z, co
     float col[VPR];
 #pragma unroll
     for (int j = 0; j < VPR; j++) col[j] = 0.0f;
-    for (int row = blockIdx.x * 4 + wave; row < B; row += gridDim.x * 4) {
-        const float rl = softmax_ce_row_regs<VPR>(z + (long)row * C, labels[row], C, a, dz + (long)row * C, lane, col);
+    // the next row's loads are issued before this row's arithmetic, so a wave with several rows keeps
+    // one row's loads in flight
+    const int step = gridDim.x * 4;
+    int row = blockIdx.x * 4 + wave;
+    float nv[VPR];
+    if (row < B) softmax_ce_row_load<VPR>(z + (long)row * C, C, lane, nv);
+    for (; row < B; row += step) {
+        float v[VPR];
+#pragma unroll
+        for (int j = 0; j < VPR; j++) v[j] = nv[j];
+        if (row + step < B) softmax_ce_row_load<VPR>(z + (long)(row + step) * C, C, lane, nv);
+        const float rl = softmax_ce_row_regs<VPR>(v, z + (long)row * C, labels[row], C, a, dz + (long)row * C, lane, col);
         if (lane == 0) rowloss[row] = rl;
     }
 #pragma unroll
@@ -596,7 +606,10 @@ __device__ __forceinline__ float block_sum_512(float v, float *red) {   // fixed
 
 __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
     static_assert(kTailCols * kTailChunks == 512, "tail block is 512 threads");
-    if (blockIdx.x == 0) {
+    // The loss has a block of its own (the last), so its reduction runs beside the parameters' instead
+    // of ahead of one block's share of them.
+    const int ncol = gridDim.x - (t.loss_mode != 0 ? 1 : 0);
+    if ((int)blockIdx.x == ncol) {
         __shared__ float red[8];
         if (t.loss_mode == 1 && t.loss_parts > 0) {
             // per-wave partials, summed in a fixed order, then the f16(acc) narrowing (lower.go:712)
@@ -633,6 +646,7 @@ __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
             acc = block_sum_512(acc, red);
             if (threadIdx.x == 0) t.loss_out[0] = acc * t.loss_scale;
         }
+        return;
     }
     // kTailCols consecutive elements per block pass, so a half-wave reads 128 contiguous bytes of a
     // partial row; the rows of a partial-row accumulator are split into kTailChunks chunks (up to 16
@@ -642,7 +656,7 @@ __global__ __launch_bounds__(512) void tail_kernel(TailArgs t) {
     for (int s = 0; s < t.nseg; s++) total += t.seg[s].n;
     __shared__ float part[kTailChunks][kTailCols];
     const int e = threadIdx.x % kTailCols, q = threadIdx.x / kTailCols;
-    for (long base = (long)blockIdx.x * kTailCols; base < total; base += (long)gridDim.x * kTailCols) {
+    for (long base = (long)blockIdx.x * kTailCols; base < total; base += (long)ncol * kTailCols) {
         const long i = base + e;
         long k = i;
         int s = 0;
@@ -699,6 +713,7 @@ hipError_t step_tail(const TailArgs &t, hipStream_t s) {
     long total = 0;
     for (int i = 0; i < t.nseg; i++) total += t.seg[i].n;
     int blocks = (int)std::min<long>(std::max<long>((total + kTailCols - 1) / kTailCols, 1), 2048);
+    if (t.loss_mode != 0) blocks++;   // the loss block
     hipLaunchKernelGGL(tail_kernel, dim3(blocks), dim3(kTailCols * kTailChunks), 0, s, t);
     return hipGetLastError();
 }

@@ -50,22 +50,27 @@ __device__ __forceinline__ float softmax_ce_row(const float *zr, int lab, int C,
     return rl;
 }
 
-// softmax_ce_row with the row held in registers: VPR values per lane (C <= 64 * VPR), lane l holding
-// columns l, l + 64, ... in order, so every per-lane sum adds the same terms in the same order as
+// softmax_ce_row with the row held in registers: VPR values per lane (C <= 64 * VPR, loaded by
+// softmax_ce_row_load; columns past C hold -FLT_MAX), lane l holding columns l, l + 64, ... in order, so every per-lane sum adds the same terms in the same order as
 // softmax_ce_row and each result has the same bits. Writes the row's dz and adds it to col[j] (the
 // running column sums of the rows this wave handles); returns the row's log-probability of its label.
+// v: the row's values as softmax_ce_row_load leaves them.
 template <int VPR>
-__device__ __forceinline__ float softmax_ce_row_regs(const float *zr, int lab, int C, float a, float *dz, int lane,
-                                                     float (&col)[VPR]) {
-#pragma clang fp contract(off)
-    float v[VPR], e[VPR];
-    float m = -FLT_MAX;
+__device__ __forceinline__ void softmax_ce_row_load(const float *zr, int C, int lane, float (&v)[VPR]) {
 #pragma unroll
     for (int j = 0; j < VPR; j++) {
         const int c = lane + 64 * j;
         v[j] = c < C ? zr[c] : -FLT_MAX;
-        m = fmaxf(m, v[j]);
     }
+}
+template <int VPR>
+__device__ __forceinline__ float softmax_ce_row_regs(const float (&v)[VPR], const float *zr, int lab, int C, float a,
+                                                     float *dz, int lane, float (&col)[VPR]) {
+#pragma clang fp contract(off)
+    float e[VPR];
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < VPR; j++) m = fmaxf(m, v[j]);
     m = wave_max(m);
     float tie = 0.0f, s = 0.0f;
 #pragma unroll

@@ -34,7 +34,7 @@ TRAFFIC_BYTES = {(3, "dW2"): 268.6e6 + 100.7e6, (5, "chain_resident"): 135.2e6 +
                  (5, "chain_stats"): 134.3e6 + 4.2e6}
 
 
-def config_workload(cfg: int):
+def config_workload(cfg: int, batch4: int = 4096):
     """Returns (trainer kind, dims, lr, batch, inputs dict, kernels [(name, kind, amount)], meta)."""
     from anneal_amd import _lib as L
     from anneal_amd import data
@@ -63,10 +63,10 @@ def config_workload(cfg: int):
                 "bytes_per_step": 8.0 * R * Cc + 8 * Cc, "dtype": "f32"}
         return L.TRAIN_CHAIN, [R, Cc], 0.0, R, p, ks, meta
     if cfg in (1, 4):
-        B, D, H, C = (64, 784, 128, 10) if cfg == 1 else (4096, 512, 2048, 512)
+        B, D, H, C = (64, 784, 128, 10) if cfg == 1 else (batch4, 512, 2048, 512)
         p = data.mlp_ce_inputs(B, D, H, C, **({} if cfg == 1 else {"x_lo": -1.0, "x_hi": 1.0}))
         ks = mlp_ce_kernels(B, D, H, C)
-        wl = "config1_mlp_784-128-10_b64_f32" if cfg == 1 else "config4_dynmlp_512-2048-512_f32_N4096"
+        wl = "config1_mlp_784-128-10_b64_f32" if cfg == 1 else f"config4_dynmlp_512-2048-512_f32_N{B}"
         meta = {"workload": wl, "batch": B, "dtype": "f32",
                 "flop_per_step": sum(a for _, k, a in ks if k.startswith("flop"))}
         return L.TRAIN_MLP_CE, [B, D, H, C], 0.01, B, p, ks, meta
@@ -347,6 +347,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=4096, help="config 4's batch N (1 to 4096)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true", help="skip the steps/s of the other configs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -366,7 +367,9 @@ def main():
         sys.exit(2)
 
     from anneal_amd.backend import Device, Trainer
-    kind, dims, lr, batch, p, kernels, meta = config_workload(args.config)
+    if not 1 <= args.batch <= 4096:
+        raise SystemExit("bench: --batch is 1 to 4096")
+    kind, dims, lr, batch, p, kernels, meta = config_workload(args.config, args.batch)
     dev = Device(0)
     caps = dev.caps()
     t = Trainer(dev, kind, dims, lr)
