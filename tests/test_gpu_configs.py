@@ -77,6 +77,29 @@ def test_mlp_three_kernel_step_ragged(dev, shape):
     check_mlp(out, p, 0.01)
 
 
+@pytest.mark.parametrize("shape", [(300, 299, 200, 300, 10), (128, 97, 100, 130, 700), (64, 33, 896, 256, 1000),
+                                   (40, 37, 64, 96, 1030)])
+def test_mlp_gemm_step_ragged(dev, shape):
+    """The GEMM-based MLP step off config 4's shape: ragged tiles of the f32 contractions (with the
+    configurations the trainer tunes for them), softmax-CE with the bias-gradient partial rows at
+    C = 10 / 700 / 1000 (1, 11 and 16 values per lane, columns past C masked), and past C = 1024 the
+    separate column-sum launch; each against the oracle."""
+    Bmax, B, D, H, C = shape
+    p = data.mlp_ce_inputs(B, D, H, C, seed=13)
+    t = Trainer(dev, L.TRAIN_MLP_CE, [Bmax, D, H, C], 0.01)
+    names = t.kernel_names(B)
+    assert "softmax_ce" in names and (("db2" in names) == (C > 1024)), names
+    for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+        t.set(k, p[k])
+    t.step(B, store_grads=True)
+    out = {"loss": t.get("loss", 1)[0]}
+    for k, n in (("dW1", H * D), ("db1", H), ("dW2", C * H), ("db2", C), ("W1", H * D), ("b1", H),
+                 ("W2", C * H), ("b2", C)):
+        out[k] = t.get(k, n)
+    t.close()
+    check_mlp(out, p, 0.01)
+
+
 @pytest.mark.parametrize("N", [2, 8, 9])
 def test_config4_small_batch_paths(dev, N):
     """Batches up to 8 take the four-kernel small-batch step, 9 the GEMM step; both against the oracle."""

@@ -364,3 +364,24 @@ def test_gemm_f32_tune_and_cache(dev, tmp_path):
         dev.gemm_tune_cache(str(bad), False)
     for b in (dA, dB, dC):
         b.free()
+
+
+@pytest.mark.parametrize("cfg", [(64, 0, 4), (64, 4, 2), (128, 2, 8), (128, 0, 16), (64, 1, 3)])
+def test_gemm_f32_split_k_ragged(dev, cfg):
+    """Split-K on ragged tiles (M, N and K not multiples of the tile or the 32-wide k chunk), with fixed
+    or automatic k-groups; splits=3 runs three splits (groups past K load zeros)."""
+    from anneal_amd.executor import Buffer, ExecItem, Executor
+    tile, kg, splits = cfg
+    M, N, K = 200, 300, 1000
+    key = f"tmpl:gemm;dtype=f32;epi=bias_relu;ta=1;tb=0;M={M};N={N};K={K};tile={tile};splits={splits}"
+    if kg:
+        key += f";kg={kg}"
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    bufs = [Buffer(10, M * N, [M, N], L.AH_F32), Buffer(1, M * K, [K, M], L.AH_F32), Buffer(2, N * K, [N, K], L.AH_F32),
+            Buffer(3, N, [N], L.AH_F32)]
+    got = Executor(dev).run([ExecItem(key, bufs)], {1: store_operand(A, 1).ravel(), 2: B.ravel(), 3: bias})[10]
+    ref = np.maximum(A.astype(np.float64) @ B.astype(np.float64).T + bias, 0)
+    assert O.relerr(got.reshape(M, N), ref) < 1e-5
