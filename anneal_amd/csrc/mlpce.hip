@@ -211,15 +211,18 @@ __global__ __launch_bounds__(kMlpThreads) void mlpce_grad_kernel(const float *__
 // one streaming pass over W1 and W2.
 
 constexpr int kSmallB = 8, kSmallMaxC = 512;
+constexpr int kSmallUnits = 8;    // hidden units per workgroup of the dH kernel
+constexpr int kGradRows = 4;      // weight rows per thread of the small-batch gradient kernel
 
-// out[n][j] = in[n] . W[j] + b[j] (ReLU, sign-tagged, when RELU): 8 samples x 8 rows per workgroup,
-// 16 lanes per output with 16-byte loads, 8 in flight per operand and lane. K % 4 == 0.
-template <bool RELU>
-__global__ __launch_bounds__(kMlpThreads) void mlp_lin_kernel(const float *__restrict__ in, const float *__restrict__ W,
-                                                              const float *__restrict__ b, int B, int K, int J,
-                                                              float *__restrict__ out) {
+// out[n][j] = in[n] . W[j] + b[j] (ReLU, sign-tagged, when RELU): 8 samples x JT rows per workgroup,
+// 16 lanes per output with 16-byte loads, 8 in flight per operand and lane. K % 4 == 0. A long K takes
+// fewer rows per workgroup (JT = 2), so more CUs read W: a CU keeps only so many misses in flight.
+template <bool RELU, int JT>
+__global__ __launch_bounds__(128 * JT) void mlp_lin_kernel(const float *__restrict__ in, const float *__restrict__ W,
+                                                           const float *__restrict__ b, int B, int K, int J,
+                                                           float *__restrict__ out) {
     const int tid = threadIdx.x, o = tid / 16, ks = tid % 16;
-    const int n = blockIdx.x * 8 + o / 8, j = blockIdx.y * 8 + o % 8;
+    const int n = blockIdx.x * 8 + o / JT, j = blockIdx.y * JT + o % JT;
     const bool live = n < B && j < J;
     const float *ar = in + (long)(live ? n : 0) * K, *wr = W + (long)(live ? j : 0) * K;
     float acc = 0.0f;
@@ -244,9 +247,13 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_lin_kernel(const float *__res
     }
 }
 
-// Softmax-CE of every sample (each workgroup; workgroup 0 writes dz and rowloss), then dH for the 64
-// hidden units [64 * blockIdx.x, +64): wave w sums its share of the classes for every sample (all its
-// W2 loads in flight at once), the waves' sums are added in wave order, and the ReLU mask applied.
+// Softmax-CE of every sample (each workgroup; workgroup 0 writes dz and rowloss), then dH for the
+// kSmallUnits (U) hidden units [U * blockIdx.x, +U): wave w takes a share of the classes, its lane
+// (j, s) the classes c0 + s, c0 + s + 64 / U, ... of that share for hidden unit j (64 / U rows of 4U
+// bytes per load; all of a lane's W2 loads in flight at once), the lanes of a unit are added by
+// shuffles, the waves' sums in wave order, and the ReLU mask applied. Few units per workgroup spread
+// W2's reads over H / U workgroups: a CU keeps only so many misses in flight, so the read rate grows
+// with the CUs reading.
 __global__ __launch_bounds__(kMlpThreads) void mlp_small_dh_kernel(const int32_t *__restrict__ lab,
                                                                    const float *__restrict__ Z,
                                                                    const float *__restrict__ Hg,
@@ -254,16 +261,32 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_small_dh_kernel(const int32_t
                                                                    float a, float *__restrict__ dz,
                                                                    float *__restrict__ dH,
                                                                    float *__restrict__ rowloss) {
-    constexpr int NW = kMlpThreads / 64, CW = kSmallMaxC / NW;   // classes per wave, at most
+    constexpr int NW = kMlpThreads / 64, SUBS = 64 / kSmallUnits;   // waves; lanes per hidden unit
+    constexpr int CW = kSmallMaxC / NW / SUBS;                       // classes per lane, at most
     __shared__ float dzs[kSmallB * kSmallMaxC];
     __shared__ float zr[NW * kSmallB * 64];   // the logits, then the per-wave sums
     float *zs = zr;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, j = blockIdx.x * 64 + lane;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, jl = lane % kSmallUnits, sub = lane / kSmallUnits;
+    const int j = blockIdx.x * kSmallUnits + jl;
     const int cw = (C + NW - 1) / NW, c0 = w * cw, c1 = min(C, c0 + cw);
-    float wv[CW];   // this lane's column of W2 over the wave's classes
+    float wv[CW];   // W2[c][j] for this lane's classes c = c0 + sub + SUBS * q
 #pragma unroll
-    for (int q = 0; q < CW; q++) wv[q] = (c0 + q < c1 && j < H) ? W2[(long)(c0 + q) * H + j] : 0.0f;
-    for (int i = tid; i < B * C; i += kMlpThreads) zs[i] = Z[i];
+    for (int q = 0; q < CW; q++) {
+        const int c = c0 + sub + SUBS * q;
+        wv[q] = (c < c1 && j < H) ? W2[(long)c * H + j] : 0.0f;
+    }
+    // this thread's activation for the ReLU mask at the end (thread n * U + u: sample n, unit u)
+    const int mn = tid / kSmallUnits, mj = blockIdx.x * kSmallUnits + tid % kSmallUnits;
+    const bool mlive = tid < B * kSmallUnits && mj < H;
+    const float hact = mlive ? Hg[(long)mn * H + mj] : 0.0f;
+    // the logits into LDS, every thread's loads in flight together
+    static_assert(kSmallB * kSmallMaxC <= 4 * kMlpThreads, "logit staging is 4 values per thread");
+    float zl[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) zl[u] = tid + u * kMlpThreads < B * C ? Z[tid + u * kMlpThreads] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (tid + u * kMlpThreads < B * C) zs[tid + u * kMlpThreads] = zl[u];
     __syncthreads();
     for (int n = w; n < B; n += NW) {
         const float r = softmax_ce_row(zs + n * C, lab[n], C, a, dzs + n * C, lane);
@@ -278,42 +301,56 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_small_dh_kernel(const int32_t
         acc[n] = 0.0f;
         if (n < B)
 #pragma unroll
-            for (int q = 0; q < CW; q++)
-                if (c0 + q < c1) acc[n] += dzs[n * C + c0 + q] * wv[q];
-    }
+            for (int q = 0; q < CW; q++) {
+                const int c = c0 + sub + SUBS * q;
+                if (c < c1) acc[n] += dzs[n * C + c] * wv[q];
+            }
 #pragma unroll
-    for (int n = 0; n < kSmallB; n++) zr[(w * kSmallB + n) * 64 + lane] = acc[n];
+        for (int o = kSmallUnits; o < 64; o <<= 1) acc[n] += __shfl_xor(acc[n], o);
+    }
+    if (sub == 0)
+#pragma unroll
+        for (int n = 0; n < kSmallB; n++) zr[(w * kSmallB + n) * kSmallUnits + jl] = acc[n];
     __syncthreads();
-    if (tid < B * 64) {
-        const int n = tid / 64, jj = blockIdx.x * 64 + lane;
+    if (mlive) {
+        const int u = tid % kSmallUnits;
         float g = 0.0f;
-        for (int q = 0; q < NW; q++) g += zr[(q * kSmallB + n) * 64 + lane];
-        if (jj < H) dH[(long)n * H + jj] = relu_dead(Hg[(long)n * H + jj]) ? 0.0f : g;
+        for (int q = 0; q < NW; q++) g += zr[(q * kSmallB + mn) * kSmallUnits + u];
+        dH[(long)mn * H + mj] = relu_dead(hact) ? 0.0f : g;
     }
 }
 
-// dW1 = dH^T x and dW2 = dz^T H over the batch, with SGD, one float4 of W1 or W2 per thread; the last
-// workgroup takes b1, b2 and the loss.
+// dW1 = dH^T x and dW2 = dz^T H over the batch, with SGD, one float4 column chunk of kGradRows rows of W1
+// or W2 per thread; the workgroups after those take the biases (one per thread) and the loss.
 __global__ __launch_bounds__(256) void mlp_small_grad_kernel(const float *__restrict__ x, const float *__restrict__ Hg,
                                                              const float *__restrict__ dz, const float *__restrict__ dH,
                                                              const float *__restrict__ rowloss, int B, int D, int H,
                                                              int C, MlpSgd S) {
-    const long n1 = (long)H * D / 4, n2 = (long)C * H / 4;
+    // Weight units: kGradRows rows x one float4 column chunk (W1: rows j of H, chunks of D; W2: rows c of
+    // C, chunks of H), so each activation chunk loaded serves kGradRows rows. H % 4 == 0 (mlp_small_ok),
+    // so W1's rows divide; W2's last unit may hold fewer than kGradRows rows.
+    const long n1 = (long)(H / kGradRows) * (D / 4), n2 = (long)((C + kGradRows - 1) / kGradRows) * (H / 4);
+    const long nwb = (n1 + n2 + 255) / 256;   // workgroups for the weights; then (H + C) / 256 for the biases
     const long u = (long)blockIdx.x * 256 + threadIdx.x;
-    if (blockIdx.x == gridDim.x - 1) {   // biases and the loss
-        for (int j = threadIdx.x; j < H; j += 256) {
+    if (blockIdx.x >= nwb) {   // one bias per thread (b1 then b2), its batch's terms loaded together; the loss
+        const int t = (int)(blockIdx.x - nwb) * 256 + threadIdx.x;
+        if (t < H + C) {
+            const bool hid = t < H;
+            const float *src = hid ? dH + t : dz + (t - H);
+            const long ld = hid ? H : C;
+            float d[kSmallB];
+#pragma unroll
+            for (int n = 0; n < kSmallB; n++) d[n] = n < B ? src[n * ld] : 0.0f;
             float g = 0.0f;
-            for (int n = 0; n < B; n++) g += dH[(long)n * H + j];
-            if (S.gb1) S.gb1[j] = g;
-            S.b1[j] = S.b1[j] - S.lr * g;
+#pragma unroll
+            for (int n = 0; n < kSmallB; n++)
+                if (n < B) g += d[n];
+            float *bp = hid ? S.b1 + t : S.b2 + (t - H);
+            float *gb = hid ? S.gb1 : S.gb2;
+            if (gb) gb[hid ? t : t - H] = g;
+            *bp = *bp - S.lr * g;
         }
-        for (int c = threadIdx.x; c < C; c += 256) {
-            float g = 0.0f;
-            for (int n = 0; n < B; n++) g += dz[(long)n * C + c];
-            if (S.gb2) S.gb2[c] = g;
-            S.b2[c] = S.b2[c] - S.lr * g;
-        }
-        if (threadIdx.x < 64) {
+        if (blockIdx.x == nwb && threadIdx.x < 64) {
             float l = 0.0f;
             for (int n = threadIdx.x; n < B; n += 64) l += rowloss[n];
             l = wave_sum(l);
@@ -321,37 +358,41 @@ __global__ __launch_bounds__(256) void mlp_small_grad_kernel(const float *__rest
         }
         return;
     }
-    float s[kSmallB];
-    floatx4 v[kSmallB];
+    const float *act, *adj;
     float *Wp, *gp;
-    long e;
-    if (u < n1) {   // W1[j][i .. i+3]: dH[n][j] * x[n][i .. i+3]
-        e = 4 * u;
-        const int j = (int)(e / D), i = (int)(e % D);
-#pragma unroll
-        for (int n = 0; n < kSmallB; n++) {
-            s[n] = n < B ? dH[(long)n * H + j] : 0.0f;
-            v[n] = n < B ? *(const floatx4 *)(x + (long)n * D + i) : (floatx4){};
-        }
-        Wp = S.W1; gp = S.gW1;
-    } else if (u < n1 + n2) {   // W2[c][j .. j+3]: dz[n][c] * H[n][j .. j+3]
-        e = 4 * (u - n1);
-        const int c = (int)(e / H), j = (int)(e % H);
-#pragma unroll
-        for (int n = 0; n < kSmallB; n++) {
-            s[n] = n < B ? dz[(long)n * C + c] : 0.0f;
-            v[n] = n < B ? *(const floatx4 *)(Hg + (long)n * H + j) : (floatx4){};
-        }
-        Wp = S.W2; gp = S.gW2;
+    int row0, nrows, i, len, ald, jld;
+    if (u < n1) {   // W1[j][i .. i+3] += over n: dH[n][j] * x[n][i .. i+3]
+        const int per = D / 4, v = (int)u;
+        row0 = kGradRows * (v / per); i = 4 * (v % per);
+        nrows = H; len = D; act = x; ald = D; adj = dH; jld = H; Wp = S.W1; gp = S.gW1;
+    } else if (u < n1 + n2) {   // W2[c][j .. j+3] += over n: dz[n][c] * H[n][j .. j+3]
+        const int per = H / 4, v = (int)(u - n1);
+        row0 = kGradRows * (v / per); i = 4 * (v % per);
+        nrows = C; len = H; act = Hg; ald = H; adj = dz; jld = C; Wp = S.W2; gp = S.gW2;
     } else {
         return;
     }
-    const floatx4 wold = *(const floatx4 *)(Wp + e);
-    floatx4 g = {};
+    floatx4 v[kSmallB], wold[kGradRows];
+    float sc[kGradRows][kSmallB];
 #pragma unroll
-    for (int n = 0; n < kSmallB; n++) g += s[n] * v[n];
-    if (gp) *(floatx4 *)(gp + e) = g;
-    *(floatx4 *)(Wp + e) = wold - S.lr * g;
+    for (int n = 0; n < kSmallB; n++) v[n] = n < B ? *(const floatx4 *)(act + (long)n * ald + i) : (floatx4){};
+#pragma unroll
+    for (int r = 0; r < kGradRows; r++) {
+        const bool ok = row0 + r < nrows;
+        wold[r] = ok ? *(const floatx4 *)(Wp + (long)(row0 + r) * len + i) : (floatx4){};
+#pragma unroll
+        for (int n = 0; n < kSmallB; n++) sc[r][n] = ok && n < B ? adj[(long)n * jld + row0 + r] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < kGradRows; r++) {
+        if (row0 + r >= nrows) break;
+        floatx4 g = {};
+#pragma unroll
+        for (int n = 0; n < kSmallB; n++) g += sc[r][n] * v[n];
+        const long e = (long)(row0 + r) * len + i;
+        if (gp) *(floatx4 *)(gp + e) = g;
+        *(floatx4 *)(Wp + e) = wold[r] - S.lr * g;
+    }
 }
 
 bool mlp_small_ok(int B, int D, int H, int C) {
@@ -363,20 +404,29 @@ hipError_t mlp_small_step(const float *x, const int32_t *lab, int B, int D, int 
     if (!mlp_small_ok(B, D, H, C)) return hipErrorInvalidValue;
     switch (part) {
         case 0:
-            hipLaunchKernelGGL(mlp_lin_kernel<true>, dim3((B + 7) / 8, (H + 7) / 8), dim3(kMlpThreads), 0, s, x, S.W1,
-                               S.b1, B, D, H, Hbuf);
+            if (D >= 1024)
+                hipLaunchKernelGGL((mlp_lin_kernel<true, 2>), dim3((B + 7) / 8, (H + 1) / 2), dim3(256), 0, s, x, S.W1,
+                                   S.b1, B, D, H, Hbuf);
+            else
+                hipLaunchKernelGGL((mlp_lin_kernel<true, 8>), dim3((B + 7) / 8, (H + 7) / 8), dim3(1024), 0, s, x, S.W1,
+                                   S.b1, B, D, H, Hbuf);
             break;
         case 1:
-            hipLaunchKernelGGL(mlp_lin_kernel<false>, dim3((B + 7) / 8, (C + 7) / 8), dim3(kMlpThreads), 0, s, Hbuf,
-                               S.W2, S.b2, B, H, C, Z);
+            if (H >= 1024)
+                hipLaunchKernelGGL((mlp_lin_kernel<false, 2>), dim3((B + 7) / 8, (C + 1) / 2), dim3(256), 0, s, Hbuf,
+                                   S.W2, S.b2, B, H, C, Z);
+            else
+                hipLaunchKernelGGL((mlp_lin_kernel<false, 8>), dim3((B + 7) / 8, (C + 7) / 8), dim3(1024), 0, s, Hbuf,
+                                   S.W2, S.b2, B, H, C, Z);
             break;
         case 2:
-            hipLaunchKernelGGL(mlp_small_dh_kernel, dim3((H + 63) / 64), dim3(kMlpThreads), 0, s, lab, Z, Hbuf, S.W2, B,
+            hipLaunchKernelGGL(mlp_small_dh_kernel, dim3((H + kSmallUnits - 1) / kSmallUnits), dim3(kMlpThreads), 0, s, lab, Z, Hbuf, S.W2, B,
                                H, C, a, dz, dH, rowloss);
             break;
         default: {
-            const long n4 = ((long)H * D + (long)C * H) / 4;
-            hipLaunchKernelGGL(mlp_small_grad_kernel, dim3((unsigned)((n4 + 255) / 256) + 1), dim3(256), 0, s, x, Hbuf,
+            const long units = (long)(H / kGradRows) * (D / 4) + (long)((C + kGradRows - 1) / kGradRows) * (H / 4);
+            const unsigned nb = (unsigned)((H + C + 255) / 256);
+            hipLaunchKernelGGL(mlp_small_grad_kernel, dim3((unsigned)((units + 255) / 256) + nb), dim3(256), 0, s, x, Hbuf,
                                dz, dH, rowloss, B, D, H, C, S);
         }
     }
