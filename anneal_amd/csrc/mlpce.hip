@@ -279,6 +279,8 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_small_dh_kernel(const int32_t
     const int mn = tid / kSmallUnits, mj = blockIdx.x * kSmallUnits + tid % kSmallUnits;
     const bool mlive = tid < B * kSmallUnits && mj < H;
     const float hact = mlive ? Hg[(long)mn * H + mj] : 0.0f;
+    static_assert(kMlpThreads / 64 >= kSmallB, "one wave per sample's softmax-CE");
+    const int mylab = w < B ? lab[w] : 0;   // wave w's sample's label, loaded with everything else
     // the logits into LDS, every thread's loads in flight together
     static_assert(kSmallB * kSmallMaxC <= 4 * kMlpThreads, "logit staging is 4 values per thread");
     float zl[4];
@@ -288,9 +290,9 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_small_dh_kernel(const int32_t
     for (int u = 0; u < 4; u++)
         if (tid + u * kMlpThreads < B * C) zs[tid + u * kMlpThreads] = zl[u];
     __syncthreads();
-    for (int n = w; n < B; n += NW) {
-        const float r = softmax_ce_row(zs + n * C, lab[n], C, a, dzs + n * C, lane);
-        if (blockIdx.x == 0 && lane == 0) rowloss[n] = r;
+    if (w < B) {
+        const float r = softmax_ce_row(zs + w * C, mylab, C, a, dzs + w * C, lane);
+        if (blockIdx.x == 0 && lane == 0) rowloss[w] = r;
     }
     __syncthreads();
     if (blockIdx.x == 0)
