@@ -156,52 +156,72 @@ __global__ __launch_bounds__(kMlpThreads) void mlpce_grad_kernel(const float *__
     __shared__ float dzs[kMlpMaxB * kMlpMaxC];
     const int tid = threadIdx.x, i0 = blockIdx.x * kGradCols;
     if (i0 >= D) {   // the extra workgroup: dW2, db2, loss
+        // the parameters it updates and the row losses are loaded with the staged operands, so the
+        // updates need no second round trip to memory
+        constexpr int kW2Per = kMlpMaxC * kMlpMaxH / kMlpThreads;
+        static_assert(kMlpMaxB <= 64 && kMlpMaxC <= kMlpThreads, "one row loss per lane of wave 0");
+        float w2old[kW2Per];
+#pragma unroll
+        for (int u = 0; u < kW2Per; u++) w2old[u] = tid + u * kMlpThreads < C * H ? S.W2[tid + u * kMlpThreads] : 0.0f;
+        const float b2old = tid < C ? S.b2[tid] : 0.0f;
+        const float rl = tid < B ? rowloss[tid] : 0.0f;
         mlp_stage(hs, Hg, B * H);
         for (int i = tid; i < B * C; i += kMlpThreads) dzs[i] = dz[i];
         __syncthreads();
-        for (int o = tid; o < C * H; o += kMlpThreads) {
+#pragma unroll
+        for (int u = 0; u < kW2Per; u++) {
+            const int o = tid + u * kMlpThreads;
+            if (o >= C * H) break;
             const int c = o / H, j = o % H;
             float g = 0.0f;
             for (int n = 0; n < B; n++) g += dzs[n * C + c] * hs[n * H + j];
             if (S.gW2) S.gW2[o] = g;
-            S.W2[o] = S.W2[o] - S.lr * g;
+            S.W2[o] = w2old[u] - S.lr * g;
         }
         if (tid < C) {
             float g = 0.0f;
             for (int n = 0; n < B; n++) g += dzs[n * C + tid];
             if (S.gb2) S.gb2[tid] = g;
-            S.b2[tid] = S.b2[tid] - S.lr * g;
+            S.b2[tid] = b2old - S.lr * g;
         }
         if (tid < 64) {
-            float l = 0.0f;
-            for (int n = tid; n < B; n += 64) l += rowloss[n];
-            l = wave_sum(l);
+            const float l = wave_sum(rl);
             if (tid == 0) S.loss[0] = l * S.loss_scale;
         }
         return;
     }
     const int ni = min(kGradCols, D - i0);
+    // this thread's W1 entries (and workgroup 0's biases) loaded with the staged operands
+    constexpr int kW1Per = kMlpMaxH * kGradCols / kMlpThreads;
+    static_assert(kMlpMaxH <= kMlpThreads, "one hidden bias per thread");
+    float w1old[kW1Per];
+#pragma unroll
+    for (int u = 0; u < kW1Per; u++) {
+        const int o = tid + u * kMlpThreads, j = o / kGradCols, q = o % kGradCols;
+        w1old[u] = j < H && q < ni ? S.W1[(long)j * D + i0 + q] : 0.0f;
+    }
+    const float b1old = blockIdx.x == 0 && tid < H ? S.b1[tid] : 0.0f;
     mlp_stage(hs, dH, B * H);
     for (int i = tid; i < B * kGradCols; i += kMlpThreads) {
         const int n = i / kGradCols, q = i % kGradCols;
         xt[i] = q < ni ? x[(long)n * D + i0 + q] : 0.0f;
     }
     __syncthreads();
-    if (blockIdx.x == 0)
-        for (int j = tid; j < H; j += kMlpThreads) {   // db1
-            float g = 0.0f;
-            for (int n = 0; n < B; n++) g += hs[n * H + j];
-            if (S.gb1) S.gb1[j] = g;
-            S.b1[j] = S.b1[j] - S.lr * g;
-        }
-    for (int o = tid; o < H * kGradCols; o += kMlpThreads) {   // W1[j][i0 + q]
-        const int j = o / kGradCols, q = o % kGradCols;
-        if (q >= ni) continue;
+    if (blockIdx.x == 0 && tid < H) {   // db1
+        float g = 0.0f;
+        for (int n = 0; n < B; n++) g += hs[n * H + tid];
+        if (S.gb1) S.gb1[tid] = g;
+        S.b1[tid] = b1old - S.lr * g;
+    }
+#pragma unroll
+    for (int u = 0; u < kW1Per; u++) {   // W1[j][i0 + q]
+        const int o = tid + u * kMlpThreads, j = o / kGradCols, q = o % kGradCols;
+        if (j >= H || q >= ni) continue;
         float g = 0.0f;
         for (int n = 0; n < B; n++) g += hs[n * H + j] * xt[n * kGradCols + q];
         const long wi = (long)j * D + i0 + q;
         if (S.gW1) S.gW1[wi] = g;
-        S.W1[wi] = S.W1[wi] - S.lr * g;
+        S.W1[wi] = w1old[u] - S.lr * g;
     }
 }
 
