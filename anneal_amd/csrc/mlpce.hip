@@ -310,8 +310,11 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_small_dh_kernel(const int32_t
     for (int u = 0; u < 4; u++)
         if (tid + u * kMlpThreads < B * C) zs[tid + u * kMlpThreads] = zl[u];
     __syncthreads();
-    if (w < B) {
-        const float r = softmax_ce_row(zs + w * C, mylab, C, a, dzs + w * C, lane);
+    if (w < B) {   // the row from LDS into registers once (the same sums, in the same order, as softmax_ce_row)
+        constexpr int VPR = kSmallMaxC / 64;
+        float v[VPR], unused[VPR] = {};
+        softmax_ce_row_load<VPR>(zs + w * C, C, lane, v);
+        const float r = softmax_ce_row_regs<VPR>(v, zs + w * C, mylab, C, a, dzs + w * C, lane, unused);
         if (blockIdx.x == 0 && lane == 0) rowloss[w] = r;
     }
     __syncthreads();
