@@ -234,11 +234,13 @@ def other_configs(dev, skip: int) -> dict:
         dev.sync()
         return steps / (time.perf_counter() - t0)
 
-    def entry(t, batch, kernels, steps=50):
+    def entry(t, batch, kernels, steps=50, cfg=None):
         # eager launches and hipGraph replay both timed; a step of a few short kernels is bound by the
         # host's launch rate, where eager launches can beat a graph launch
         eager, graph = rate(t, batch, steps, False), rate(t, batch, steps, True)
         roof, rows = kernel_table(t, batch, kernels)
+        if cfg is not None and (cfg, roof["kernel"]) in TRAFFIC_BYTES:
+            roof["traffic"] = TRAFFIC_BYTES[(cfg, roof["kernel"])]   # measured HBM bytes per launch
         return {"steps_per_s": max(eager, graph), "eager_steps_per_s": eager, "graph_steps_per_s": graph,
                 "roofline": roof, "kernels": rows}
 
@@ -270,7 +272,7 @@ def other_configs(dev, skip: int) -> dict:
         t = Trainer(dev, kind, dims, lr)
         for k, v in p.items():
             t.set(k, v)
-        out["config5_chain_8192x4096_f32"] = entry(t, batch, ks)
+        out["config5_chain_8192x4096_f32"] = entry(t, batch, ks, cfg=5)
         t.close()
     if skip != 3:
         kind, dims, lr, batch, p, ks, _ = config_workload(3)
