@@ -462,21 +462,30 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
             f(kResRegs + j, x);
         }
     };
-    // 3. sum e, sum e^2 and ties against the exact max
+    // 3. sum e, sum e^2 and ties against the exact max. Each slot then keeps its e in place of x,
+    // negated where the element ties its column's max (e is exactly 1 there, and every other e is
+    // +0 or positive), so the backward pass needs neither the exp nor the max again.
     float se[4] = {}, sq[4] = {}, tc[4] = {};
-    each([&](int, const floatx4 &x) {
+    auto stat = [&](floatx4 x) -> floatx4 {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float e = fast_exp2((x[u] - m[u]) * AH_INV_LN2);
+            const bool tie = x[u] == m[u];
             se[u] += e;
             sq[u] += e * e;
-            tc[u] += x[u] == m[u] ? 1.0f : 0.0f;
+            tc[u] += tie ? 1.0f : 0.0f;
+            x[u] = tie ? -e : e;
         }
         // materialise all three sums after every slot: left free, the compiler runs the e sums over
         // all slots first and the e^2 sums after them, keeping every slot's e live in between
         asm volatile("" : "+v"(se[0]), "+v"(se[1]), "+v"(se[2]), "+v"(se[3]), "+v"(sq[0]), "+v"(sq[1]), "+v"(sq[2]),
-                     "+v"(sq[3]), "+v"(tc[0]), "+v"(tc[1]), "+v"(tc[2]), "+v"(tc[3]));
-    });
+                     "+v"(sq[3]), "+v"(tc[0]), "+v"(tc[1]), "+v"(tc[2]), "+v"(tc[3]), "+v"(x));
+        return x;
+    };
+#pragma unroll
+    for (int i = 0; i < kResRegs; i++) v[i] = stat(v[i]);
+#pragma unroll 2
+    for (int j = 0; j < kResLds; j++) held[j][tid] = stat(*(volatile floatx4 *)&held[j][tid]);
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         se[u] = res_tree_sum(se[u]);
@@ -506,22 +515,22 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         const float gRs = (gi * r) * s_ + 2.0f * gsq_ * (r_s * q_);
         const float gs_ = ((-gRs) * r_s) * r_s;
         const float gm = -(AH_LN2 * AH_INV_LN2) * (r_s * gRs + gs_ * s_);
-        coef[0][tid] = r_s;
-        coef[1][tid] = gi * r;
-        coef[2][tid] = gsq_;
-        coef[3][tid] = gs_;
+        // dX = e * (gr * r_s + gs) + e^2 * (2 gsq r_s^2), plus the tie share where x is the max: the
+        // per-element backward of S = e * r_s through sum e and sum S^2, with its per-column factors
+        // gathered (the reference's op order rounds them per element; the difference is at f32 rounding)
+        coef[0][tid] = (gi * r) * r_s + gs_;
+        coef[1][tid] = 2.0f * gsq_ * (r_s * r_s);
         coef[4][tid] = gm * (1.0f / t_);
         coef[5][tid] = gi * (r * sumS);
         dg[c] = r * sumS;
     }
     __syncthreads();
-    float rs[4], gr[4], gsq[4], gs[4], sh[4];
+    float ca[4], cb[4], sh[4];
     {
         const floatx4 a = *(const floatx4 *)&coef[0][4 * q], b = *(const floatx4 *)&coef[1][4 * q],
-                      c2 = *(const floatx4 *)&coef[2][4 * q], d = *(const floatx4 *)&coef[3][4 * q],
                       e = *(const floatx4 *)&coef[4][4 * q];
 #pragma unroll
-        for (int u = 0; u < 4; u++) { rs[u] = a[u]; gr[u] = b[u]; gsq[u] = c2[u]; gs[u] = d[u]; sh[u] = e[u]; }
+        for (int u = 0; u < 4; u++) { ca[u] = a[u]; cb[u] = b[u]; sh[u] = e[u]; }
     }
     // 5. dX from the held strip
     // The stores' row offset is a running value advanced through an empty asm after each slot, so only
@@ -531,14 +540,10 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         floatx4 o;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const float y = x[u];
-            const float e = fast_exp2((y - m[u]) * AH_INV_LN2);
-            const float S = e * rs[u];
-            const float t2 = gsq[u] * S;
-            const float gS = (gr[u] + t2) + t2;
-            const float ge = gS * rs[u] + gs[u];
-            const float gzs = ((ge * e) * AH_LN2) * AH_INV_LN2;
-            o[u] = gzs + (y == m[u] ? sh[u] : 0.0f);
+            const float y = x[u];   // e, negated at the column's max
+            const float e = fabsf(y);
+            const float gzs = (ca[u] + cb[u] * e) * e;
+            o[u] = gzs + (y < 0.0f ? sh[u] : 0.0f);
         }
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, o), dr, voff, soff, 0);
         soff += rstepB;

@@ -29,7 +29,7 @@ PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
 # HBM bytes per launch of the dominant kernels, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
 # scaled by a plain copy of known size (read factor 2.0, write factor 1.0): profiles/hbm_traffic_pmc.md,
 # profiles/chain_resident_config5.md.
-TRAFFIC_BYTES = {(3, "dW2"): 268.6e6 + 100.7e6, (5, "chain_resident"): 135.2e6 + 140.3e6,
+TRAFFIC_BYTES = {(3, "dW2"): 268.6e6 + 100.7e6, (5, "chain_resident"): 134.8e6 + 143.0e6,
                  (5, "chain_grad"): 134.4e6 + 134.4e6,
                  (5, "chain_stats"): 134.3e6 + 4.2e6}
 
