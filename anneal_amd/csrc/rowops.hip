@@ -396,7 +396,6 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
     int strip = blockIdx.x;
     if ((nstrips & 7) == 0) strip = (strip & 7) * (nstrips >> 3) + (strip >> 3);   // neighbouring strips share an XCD
     const int q = tid & 3, rl = tid >> 2;
-    const int col = strip * kResCols + 4 * q;
     // Buffer accesses from the strip's first column: the lane's offset in one VGPR, the slot's row
     // offset (wave-uniform) in the scalar offset, so the 64 slots cost no address registers. The
     // caller guarantees R * Cc * 4 < 2^31.
