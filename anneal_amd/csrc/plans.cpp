@@ -298,14 +298,18 @@ struct MlpCeTrainer : ah_trainer {
         if (n > t[slot].n) return set_error(AH_ERR_INVALID, "MLP_CE: slot %d too small", slot);
         return copy_out(dev, h, t[slot].p, (size_t)n * 4);
     }
-    // Before a batch's first GEMM-based step: tune each f32 contraction's (tile, k-groups, splits) for
-    // shapes the device has not tuned. Each runs with its own epilogue into buffers the step rewrites
-    // (the weight updates into the gradient outputs, with lr 0); the bias-gradient accumulator it
-    // touches is re-zeroed.
+    // Before a batch's first GEMM-based step outside a capture: tune each f32 contraction's (tile,
+    // k-groups, splits) for shapes the device has not tuned. Each runs with its own epilogue into
+    // buffers the step rewrites (the weight updates into the gradient outputs, with lr 0); the
+    // bias-gradient accumulator it touches is re-zeroed.
     std::set<int> tuned;
     int prepare(int64_t batch) override {
         const int B = (int)batch;
         if (fused || mlp_small_ok(B, D, H, C) || tuned.count(B)) return AH_OK;
+        // a caller capturing the device stream gets the automatic choices (timing would end its capture)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        AH_HIP(hipStreamIsCapturing(dev->stream, &cs));
+        if (cs != hipStreamCaptureStatusNone) return AH_OK;
         GemmDesc g[5] = {gdesc(GEMM_F32, EPI_BIAS_RELU, 0, 0, B, H, D, x, D, W1, D, H1, H),
                          gdesc(GEMM_F32, EPI_BIAS, 0, 0, B, C, H, H1, H, W2, H, Z2, C),
                          gdesc(GEMM_F32, EPI_MASK, 0, 1, B, H, C, dZ2, C, W2, H, dZ1, H),

@@ -424,3 +424,28 @@ def test_config3_trainer_starts_zeroed_after_in_step_tuning(dev):
     for k, n in (("W1", D1 * D0), ("b3", D3), ("db1", D1), ("db3", D3)):
         assert not np.any(t.get(k, n)), k
     t.close()
+
+
+def test_config4_first_step_captured_by_caller(dev):
+    """A caller that captures the device stream around a batch's first GEMM-based step: the trainer skips
+    its contraction timing there (automatic choices), and the replayed graph computes the step."""
+    import ctypes as C
+    N = 256
+    p = data.mlp_ce_inputs(N, 512, 2048, 512, x_lo=-1.0, x_hi=1.0, seed=21)
+    t = Trainer(dev, L.TRAIN_MLP_CE, [4096, 512, 2048, 512], 0.01)
+    for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+        t.set(k, p[k])
+    lib = dev.lib
+    assert lib.ah_graph_begin(dev.h) == 0
+    t.step(N, store_grads=True)
+    g = C.c_void_p()
+    assert lib.ah_graph_end(dev.h, C.byref(g)) == 0
+    assert lib.ah_graph_replay(dev.h, g) == 0
+    dev.sync()
+    lib.ah_graph_destroy(g)
+    out = {"loss": t.get("loss", 1)[0]}
+    for k, n in (("dW1", 2048 * 512), ("db1", 2048), ("dW2", 512 * 2048), ("db2", 512), ("W1", 2048 * 512),
+                 ("b1", 2048), ("W2", 512 * 2048), ("b2", 512)):
+        out[k] = t.get(k, n)
+    t.close()
+    check_mlp(out, p, 0.01)
