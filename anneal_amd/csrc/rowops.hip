@@ -464,11 +464,13 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
     // 3. sum e, sum e^2 and ties against the exact max. Each slot then keeps its e in place of x,
     // negated where the element ties its column's max (e is exactly 1 there, and every other e is
     // +0 or positive), so the backward pass needs neither the exp nor the max again.
-    float se[4] = {}, sq[4] = {}, tc[4] = {};
+    float se[4] = {}, sq[4] = {}, tc[4] = {}, mc[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) mc[u] = m[u] * AH_INV_LN2;
     auto stat = [&](floatx4 x) -> floatx4 {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const float e = fast_exp2((x[u] - m[u]) * AH_INV_LN2);
+            const float e = fast_exp2(__builtin_fmaf(x[u], AH_INV_LN2, -mc[u]));
             const bool tie = x[u] == m[u];
             se[u] += e;
             sq[u] += e * e;
