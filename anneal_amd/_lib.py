@@ -135,6 +135,7 @@ SIGNATURES = {
     "ah_trainer_set": (C.c_int, [_P, C.c_int32, _P, C.c_int64]),
     "ah_trainer_get": (C.c_int, [_P, C.c_int32, _P, C.c_int64]),
     "ah_trainer_step": (C.c_int, [_P, C.c_int64, C.c_int32]),
+    "ah_trainer_steps": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32]),
     "ah_trainer_probe": (C.c_int, [_P, C.c_int32]),
     "ah_trainer_probe_read": (C.c_int, [_P, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "ah_trainer_kernel_count": (C.c_int, [_P, C.c_int64, C.POINTER(C.c_int32)]),

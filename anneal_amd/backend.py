@@ -135,7 +135,7 @@ class Trainer:
         L.TRAIN_CONVNET: ["x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb", "loss", "dcw1", "dcb1", "dcw2",
                           "dcb2", "dfw", "dfb"],
         L.TRAIN_MLP3_F16: ["x", "t", "W1", "b1", "W2", "b2", "W3", "b3", "loss", "dW1", "db1", "dW2", "db2", "dW3",
-                           "db3", "loss_sum"],
+                           "db3", "loss_sum", "H1", "H2", "d"],
         L.TRAIN_CHAIN: ["X", "g", "loss", "dX", "dg"],
     }
 
@@ -161,6 +161,11 @@ class Trainer:
     def step(self, batch: int, store_grads: bool = False, graph: bool = False) -> None:
         flags = (L.STEP_STORE_GRADS if store_grads else 0) | (L.STEP_GRAPH if graph else 0)
         L.check(self.dev.lib.ah_trainer_step(self.h, int(batch), flags))
+
+    def steps(self, batch: int, n: int, store_grads: bool = False, graph: bool = False) -> None:
+        """n consecutive steps; with graph=True as hipGraph launches of up to 16 steps each."""
+        flags = (L.STEP_STORE_GRADS if store_grads else 0) | (L.STEP_GRAPH if graph else 0)
+        L.check(self.dev.lib.ah_trainer_steps(self.h, int(batch), flags, int(n)))
 
     def probe(self, kernel_index: int) -> None:
         L.check(self.dev.lib.ah_trainer_probe(self.h, kernel_index))

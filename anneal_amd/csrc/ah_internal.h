@@ -35,6 +35,9 @@ struct TemplateKernel {
     // bytes of device workspace the kernel needs for a symbolic binding (null: none); the workspace is the
     // template's own, grown by template_prepare (or on first use) and freed with the template
     std::function<int64_t(int64_t symval)> workspace;
+    // bytes each PARAM must hold for a binding (entry j: PARAM j; 0: not read or written), from the key's
+    // shape; the executor checks the bound buffers against it before anything is launched
+    std::function<std::vector<int64_t>(int64_t symval)> bytes;
     void *ws = nullptr;
     int64_t ws_bytes = 0;
     std::function<int(ah_device *, TemplateKernel *self, void *const *ptrs, int32_t n_ptrs, const int32_t *scalars,

@@ -36,6 +36,9 @@
 #include "gemm.h"
 
 namespace ah {
+// Longest opt sequence a search keeps (ah_beam_result.opts holds 8).
+constexpr int kMaxBeamOpts = 8;
+
 namespace {
 
 uint64_t fnv64(const std::string &s) {
@@ -346,7 +349,7 @@ int ah_beam_search(ah_device *d, const ah_exec_item *item, int32_t width, int32_
         auto it = g_cache.find(sk);
         if (it != g_cache.end()) {
             res->from_cache = 1;
-            res->n_opts = (int32_t)std::min<size_t>(it->second.opts.size(), 8);
+            res->n_opts = (int32_t)std::min<size_t>(it->second.opts.size(), kMaxBeamOpts);
             for (int i = 0; i < res->n_opts; i++) res->opts[i] = it->second.opts[i];
         }
     }
@@ -363,6 +366,9 @@ int ah_beam_search(ah_device *d, const ah_exec_item *item, int32_t width, int32_
     if (int rc = run_single(d, *item, key.c_str(), in, &ref)) return rc;
     Cand best{{}, ki.knobs, base_us};
     std::vector<Cand> cur{best};
+    // a winning sequence holds at most kMaxBeamOpts opts: what ah_beam_result reports and what the cache
+    // file's loader accepts
+    depth = std::min(depth, kMaxBeamOpts);
     for (int dep = 0; dep < depth; dep++) {
         std::vector<Cand> next;
         for (const Cand &c : cur) {
@@ -385,7 +391,7 @@ int ah_beam_search(ah_device *d, const ah_exec_item *item, int32_t width, int32_
         cur = next;
     }
     res->min_us = best.us;
-    res->n_opts = (int32_t)std::min<size_t>(best.opts.size(), 8);
+    res->n_opts = (int32_t)std::min<size_t>(best.opts.size(), kMaxBeamOpts);
     for (int i = 0; i < res->n_opts; i++) res->opts[i] = best.opts[i];
     std::lock_guard<std::mutex> g(g_cache_mu);
     g_cache[sk] = CacheEntry{best.opts, fnv64(best.opts.empty() ? key : emit_key(ki, best.knobs))};
@@ -447,7 +453,7 @@ int ah_beam_cache(const char *path, int32_t save) {
         if (line[0] == '#' || line[0] == '\n') continue;
         unsigned long long sk = 0, h = 0;
         int n = 0, off = 0;
-        if (sscanf(line, "%llx %llx %d%n", &sk, &h, &n, &off) != 3 || n < 0 || n > 8) { rc = set_error(AH_ERR_INVALID, "beam cache %s: bad line %d", path, lineno); break; }
+        if (sscanf(line, "%llx %llx %d%n", &sk, &h, &n, &off) != 3 || n < 0 || n > kMaxBeamOpts) { rc = set_error(AH_ERR_INVALID, "beam cache %s: bad line %d", path, lineno); break; }
         CacheEntry e;
         e.src_hash = h;
         const char *p = line + off;

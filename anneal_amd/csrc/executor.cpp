@@ -239,7 +239,25 @@ int plan_run(ah_plan *p, const ah_input *inputs, int32_t n_inputs, int64_t n, bo
     *n_outputs = 0;
     if (p->items.empty()) return AH_OK;
     if (int rc = plan_alloc(p, n)) return rc;
-    // Template workspaces for this binding; a workspace that moves invalidates captured graphs.
+    // Template workspaces for this binding; a workspace that moves invalidates captured graphs. First,
+    // every buffer a template reads or writes must hold what its key's shape needs: the hand-written
+    // kernels index by the key's M, N, K (and the like), not by the buffer sizes.
+    for (size_t i = 0; i < p->items.size(); i++) {
+        const ah_plan::Item &it = p->items[i];
+        TemplateKernel *t = it.k->tmpl;
+        if (!t || !t->bytes) continue;
+        const std::vector<int64_t> want = t->bytes(symbolic ? n : 0);
+        if (want.size() > it.bufs.size())
+            return set_error(AH_ERR_INVALID, "ah_run: kernel %zu (%s) takes %zu buffers, got %zu", i, t->name.c_str(),
+                             want.size(), it.bufs.size());
+        for (size_t j = 0; j < want.size(); j++) {
+            const ah_plan::Mem &m = p->mem[it.bufs[j].uop];
+            const int64_t have = m.slot >= 0 ? std::max<int64_t>(m.elems(n), 1) * 4 : m.elems(n) * dtype_bytes(m.dtype);
+            if (want[j] > have)
+                return set_error(AH_ERR_INVALID, "ah_run: kernel %zu (%s): PARAM %zu (uop %u) holds %lld bytes, the key's "
+                                 "shape needs %lld", i, t->name.c_str(), j, it.bufs[j].uop, (long long)have, (long long)want[j]);
+        }
+    }
     for (size_t i = 0; i < p->items.size(); i++) {
         TemplateKernel *t = p->items[i].k->tmpl;
         if (!t) continue;
@@ -394,6 +412,15 @@ int ah_benchmark(ah_device *d, const ah_exec_item *item, int32_t warmup, int32_t
     int rc = ah_module_get(d, item->source, "kernel", &k);
     if (rc) return rc;
     if (k->tmpl && (rc = template_prepare(k->tmpl, 0))) return rc;
+    if (k->tmpl && k->tmpl->bytes) {   // buffers sized below what the key's shape needs: refuse before launching
+        const std::vector<int64_t> want = k->tmpl->bytes(0);
+        if ((int32_t)want.size() > item->n_bufs)
+            return set_error(AH_ERR_INVALID, "benchmark: %s takes %zu buffers, got %d", k->tmpl->name.c_str(), want.size(), item->n_bufs);
+        for (size_t j = 0; j < want.size(); j++)
+            if (want[j] > std::max<int64_t>(item->bufs[j].size, 1) * dtype_bytes(item->bufs[j].dtype))
+                return set_error(AH_ERR_INVALID, "benchmark: %s: PARAM %zu is smaller than the key's shape needs",
+                                 k->tmpl->name.c_str(), j);
+    }
     std::vector<void *> ptrs;
     auto release = [&]() { for (void *p : ptrs) hipFree(p); };
     for (int j = 0; j < item->n_bufs; j++) {

@@ -48,6 +48,13 @@ struct GemmDesc {
     void *W16;        // EPI_SGD f16 copy, optional
     float *gout;      // EPI_SGD gradient output [M,N] (row stride ldc), optional
     float *lossacc;   // EPI_MSE scalar accumulator
+    // Two-plane adjoint (f16 kernels): with A2 set the contraction runs over K twice, the second pass
+    // reading A2 (same layout and lda as A) against the same B: C = epi(sum_k (A + A2)(m,k) B(n,k)). An f32
+    // operand carried as hi = f16(a), lo = f16(a - hi) keeps ~22 bits of it through f16 MFMAs.
+    const void *A2;
+    // EPI_MASK of an f16 contraction: with C2 set, the f32 value v is stored as C = f16(v) and
+    // C2 = f16(v - f16(v)) (the two planes a following two-plane contraction reads)
+    void *C2;
     int tile;         // 0 = auto, else 64 / 128 / 256 (square tiles)
     int variant;      // f16 kernel variant (0 = auto; table Var<V> in gemm16_kernel.h), the tuning hook
     int kgroups;      // f32 tiled kernel: wave sets splitting K (0 = auto, else 1 / 2 / 4 as the tile admits;

@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kThreads * KG) void gemm_kernel(GemmDesc d) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's partial has landed
         }
         __syncthreads();
-        if (threadIdx.x == 0) ticket = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) ticket = ticket_take(count);
         __syncthreads();
         if (ticket != nsplit - 1 || kg > 0) return;
         // every other split stored its partial before taking its ticket; add them in split order, one
@@ -512,8 +512,10 @@ hipError_t gemm_launch(const GemmDesc &d, hipStream_t s) {
     if (d.dtype == GEMM_F16) {
         hipError_t e = hipSuccess;
         if (gemm16_try_launch(d, s, &e)) return e;
+        if (d.A2) return hipErrorInvalidValue;   // two-plane contractions run on the direct-to-LDS kernels only
         return launch_layout<half_t>(d, s);
     }
+    if (d.A2 || d.C2) return hipErrorInvalidValue;
     if (d.dtype == GEMM_F32) return launch_layout<float>(d, s);
     return hipErrorInvalidValue;
 }

@@ -77,6 +77,7 @@ bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err) {
     if (d.K % (64 * variant_kgroups(v))) return false;   // k-groups contract whole stages
     bool ok = (d.ta ? operand_ok<1>(d.A, d.lda, d.M) : operand_ok<0>(d.A, d.lda, d.M)) &&
               (d.tb ? operand_ok<1>(d.B, d.ldb, d.N) : operand_ok<0>(d.B, d.ldb, d.N));
+    if (ok && d.A2) ok = d.ta ? operand_ok<1>(d.A2, d.lda, d.M) : operand_ok<0>(d.A2, d.lda, d.M);
     if (!ok) return false;
     *err = kVariants[v](d, s);
     return true;
@@ -89,7 +90,7 @@ namespace {
 // The vector (LDS-staged) epilogue's conditions with every tile whole.
 bool pair_operand_ok(const GemmDesc &d, int bm) {
     using namespace g16;
-    if (d.dtype != GEMM_F16 || d.M % bm || d.N % bm || d.K % 64 || d.ldc % 4 || d.ldaux % 4) return false;
+    if (d.dtype != GEMM_F16 || d.M % bm || d.N % bm || d.K % 64 || d.ldc % 4 || d.ldaux % 4 || d.A2 || d.C2) return false;
     const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
                         (uintptr_t)d.W16 | (uintptr_t)d.gout;
     if (a & 15) return false;

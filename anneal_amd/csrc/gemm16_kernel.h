@@ -213,7 +213,7 @@ __device__ __forceinline__ void g16_tile_origin(int L, int tiles_m, int tiles_n,
 // One output tile at (m0, n0) over k in [kbase, kbase + klen), then fold.run (single k-group) and
 // the epilogue. smem holds G16Smem<...>::SMEM bytes.
 template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG,
-          class Fold>
+          class Fold, bool HL = false>
 __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, int n0, long kbase, int klen,
                                          const Fold &fold) {
     using SM = G16Smem<BM, BN, BK, NS, WVM, WVN, FETCH, KG>;
@@ -242,11 +242,29 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
     fb.init(d.ldb, n0, d.N, wave, lane);
     const char *Ab = (const char *)d.A, *Bb = (const char *)d.B;
     const int nk = klen / BK / KG;
+    // HL (two-plane A, GemmDesc::A2): the stages run over the group's part of K twice, the second time
+    // from A2. Stage offsets k >= nk*BK address A2 and B through bases moved back by one pass, so every
+    // fetch keeps its (base, k) form.
+    const char *Ab2v = nullptr, *Bbv = nullptr;
     {   // this group's part of K starts at kbase + kg * nk * BK
         const long k0 = kbase + (long)kg * nk * BK;
         Ab += TA == 0 ? k0 * 2 : k0 * d.lda * 2;
         Bb += TB == 0 ? k0 * 2 : k0 * d.ldb * 2;
+        if constexpr (HL) {
+            const long span = (long)nk * BK;
+            Ab2v = (const char *)d.A2 + (TA == 0 ? (k0 - span) * 2 : (k0 - span) * d.lda * 2);
+            Bbv = Bb - (TB == 0 ? span * 2 : span * d.ldb * 2);
+        }
     }
+    const int nkt = HL ? 2 * nk : nk;   // stages of the loop
+    auto ab = [&](int k) -> const char * {
+        if constexpr (HL) return k >= nk * BK ? Ab2v : Ab;
+        else return Ab;
+    };
+    auto bb = [&](int k) -> const char * {
+        if constexpr (HL) return k >= nk * BK ? Bbv : Bb;
+        else return Bb;
+    };
 
     floatx16 acc[FM][FN];
 #pragma unroll
@@ -261,21 +279,21 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
     // which the vmcnt accounting of the loop relies on.
     const bool pf_a = __builtin_amdgcn_readfirstlane(wave) < NW / 2;
     auto prefetch = [&](int k0) {
-        if (pf_a) prefetch_stage<BM, TA>(Ab, d.lda, m0, d.M, k0, tid, junk);
-        else prefetch_stage<BN, TB>(Bb, d.ldb, n0, d.N, k0, tid - BM, junk);
+        if (pf_a) prefetch_stage<BM, TA>(ab(k0), d.lda, m0, d.M, k0, tid, junk);
+        else prefetch_stage<BN, TB>(bb(k0), d.ldb, n0, d.N, k0, tid - BM, junk);
     };
 #pragma unroll
     for (int p = 0; p < NS - 1; p++) {
-        const int kp = min(p, nk - 1) * BK;
+        const int kp = min(p, nkt - 1) * BK;
         if constexpr (FETCH >= 3) {
-            fa.issue_asm(Ab, d.lda, kp, gsm_lds + p * STAGE, wave_u);
-            fb.issue_asm(Bb, d.ldb, kp, gsm_lds + p * STAGE + ABYTES, wave_u);
+            fa.issue_asm(ab(kp), d.lda, kp, gsm_lds + p * STAGE, wave_u);
+            fb.issue_asm(bb(kp), d.ldb, kp, gsm_lds + p * STAGE + ABYTES, wave_u);
         } else {
-            fa.issue(Ab, d.lda, kp, gsm + p * STAGE, wave);
-            fb.issue(Bb, d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
+            fa.issue(ab(kp), d.lda, kp, gsm + p * STAGE, wave);
+            fb.issue(bb(kp), d.ldb, kp, gsm + p * STAGE + ABYTES, wave);
         }
     }
-    if constexpr (FETCH == 3) prefetch(min(NS - 1, nk - 1) * BK);
+    if constexpr (FETCH == 3) prefetch(min(NS - 1, nkt - 1) * BK);
     // Waits until stage kt has landed: its own loads are done once at most the younger stages' loads
     // (and, with prefetching, the one younger prefetch line) are still in flight; the barrier then
     // covers every wave's loads, and every wave has finished reading the buffer refilled next.
@@ -290,17 +308,17 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
     // keeping the number of loads in flight, and so the wait counts, the same in every iteration).
     auto issue_grouped = [&](int kt, bool all_modes = false) {
         char *nxt = gsm + ((kt + NS - 1) % NS) * STAGE;
-        const int kn = min(kt + NS - 1, nk - 1) * BK;
+        const int kn = min(kt + NS - 1, nkt - 1) * BK;
         if (FETCH >= 5 && !all_modes) {
             // mode 5 issues these between the MFMAs that follow
         } else if constexpr (FETCH == 2) {
-            fa.issue(Ab, d.lda, kn, nxt, wave);
-            fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
+            fa.issue(ab(kn), d.lda, kn, nxt, wave);
+            fb.issue(bb(kn), d.ldb, kn, nxt + ABYTES, wave);
         } else if constexpr (FETCH >= 3) {
             const uint32_t nxt_lds = gsm_lds + ((kt + NS - 1) % NS) * STAGE;
-            fa.issue_asm(Ab, d.lda, kn, nxt_lds, wave_u);
-            fb.issue_asm(Bb, d.ldb, kn, nxt_lds + ABYTES, wave_u);
-            if constexpr (FETCH == 3) prefetch(min(kt + NS, nk - 1) * BK);
+            fa.issue_asm(ab(kn), d.lda, kn, nxt_lds, wave_u);
+            fb.issue_asm(bb(kn), d.ldb, kn, nxt_lds + ABYTES, wave_u);
+            if constexpr (FETCH == 3) prefetch(min(kt + NS, nkt - 1) * BK);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -313,10 +331,10 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
 #pragma unroll
         for (int j = 0; j < FN; j++) b[0][j] = frag<BN, TB, BK>(gsm + ABYTES, wn0 + j * 32, 0, lane);
     }
-    for (int kt = 0; kt < nk; kt++) {
+    for (int kt = 0; kt < nkt; kt++) {
         const char *sa = gsm + (kt % NS) * STAGE, *sb = sa + ABYTES;
         char *nxt = gsm + ((kt + NS - 1) % NS) * STAGE;   // fetch modes 0 and 1 refill this buffer
-        const int kn = min(kt + NS - 1, nk - 1) * BK;
+        const int kn = min(kt + NS - 1, nkt - 1) * BK;
         if constexpr (!XB) {
             stage_wait();
             if constexpr (FETCH >= 2) issue_grouped(kt);
@@ -335,8 +353,8 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
         constexpr int FPS = (PERSTAGE + KS - 1) / KS;                      // fetches per k-step
         constexpr bool SPREAD = FETCH == 1;
         if constexpr (FETCH == 0) {
-            fa.issue(Ab, d.lda, kn, nxt, wave);
-            fb.issue(Bb, d.ldb, kn, nxt + ABYTES, wave);
+            fa.issue(ab(kn), d.lda, kn, nxt, wave);
+            fb.issue(bb(kn), d.ldb, kn, nxt + ABYTES, wave);
         }
 #pragma unroll
         for (int s = 0; s < KS; s++) {
@@ -367,7 +385,7 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
             constexpr int DPM = NM >= PERSTAGE ? 1 : PERSTAGE / NM;
             static_assert(FETCH < 5 || MPD * PERSTAGE == NM || DPM * NM == PERSTAGE, "DMAs must spread evenly");
             const uint32_t refill_lds = gsm_lds + (kt % NS) * STAGE;
-            const int kr = min(kt + NS, nk - 1) * BK;
+            const int kr = min(kt + NS, nkt - 1) * BK;
 #pragma unroll
             for (int t = 0; t < NM; t++) {
                 acc[t / FN][t % FN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][t / FN], b[c][t % FN], acc[t / FN][t % FN], 0, 0, 0);
@@ -376,16 +394,16 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
 #pragma unroll
                         for (int q = 0; q < DPM; q++) {
                             const int f = (t / MPD) * DPM + q;
-                            if (f < PA) fa.issue_one_asm(f, Ab, d.lda, kr, refill_lds, wave_u);
-                            else fb.issue_one_asm(f - PA, Bb, d.ldb, kr, refill_lds + ABYTES, wave_u);
+                            if (f < PA) fa.issue_one_asm(f, ab(kr), d.lda, kr, refill_lds, wave_u);
+                            else fb.issue_one_asm(f - PA, bb(kr), d.ldb, kr, refill_lds + ABYTES, wave_u);
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
                 if (SPREAD && t % (NM / FPS) == NM / FPS - 1) {
                     const int f = s * FPS + t / (NM / FPS);
-                    if (f < PA) fa.issue_one(f, Ab, d.lda, kn, nxt, wave);
-                    else if (f < PERSTAGE) fb.issue_one(f - PA, Bb, d.ldb, kn, nxt + ABYTES, wave);
+                    if (f < PA) fa.issue_one(f, ab(kn), d.lda, kn, nxt, wave);
+                    else if (f < PERSTAGE) fb.issue_one(f - PA, bb(kn), d.ldb, kn, nxt + ABYTES, wave);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -471,7 +489,8 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
     }
 }
 
-template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG>
+template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG,
+          bool HL = false>
 __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d) {
     __shared__ __attribute__((aligned(1024))) char smem[G16Smem<BM, BN, BK, NS, WVM, WVN, FETCH, KG>::SMEM];
     const int tiles_n = (d.N + BN - 1) / BN;
@@ -481,7 +500,7 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     if ((ntiles & 7) == 0) L = (L & 7) * (ntiles >> 3) + (L >> 3);   // contiguous tile runs per XCD
     int m0, n0;
     g16_tile_origin(L, tiles_m, tiles_n, BM, BN, m0, n0);
-    g16_tile<BM, BN, TA, TB, EPI, VEPI, BK, NS, WVM, WVN, FETCH, XB, KG>(d, smem, m0, n0, 0, d.K, G16NoFold{});
+    g16_tile<BM, BN, TA, TB, EPI, VEPI, BK, NS, WVM, WVN, FETCH, XB, KG, G16NoFold, HL>(d, smem, m0, n0, 0, d.K, G16NoFold{});
 }
 
 template <int T>
@@ -492,15 +511,15 @@ static bool operand_ok(const void *p, long ld, int rows) {
     return (rows % 8) == 0;
 }
 
-template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, bool XB, int KG, int TA, int TB, int EPI>
+template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, bool XB, int KG, int TA, int TB, int EPI, bool HL = false>
 static hipError_t launch(const GemmDesc &d, hipStream_t s) {
     int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
     const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
-                        (uintptr_t)d.W16 | (uintptr_t)d.gout;
+                        (uintptr_t)d.W16 | (uintptr_t)d.gout | (uintptr_t)d.C2;
     const bool vepi = d.M % BM == 0 && d.N % BM == 0 && d.ldc % 4 == 0 && d.ldaux % 4 == 0 && (a & 15) == 0;
     constexpr int NT = 64 * WVM * WVN * KG;
-    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH, XB, KG>), dim3(tiles), dim3(NT), 0, s, d);
-    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS, WVM, WVN, FETCH, XB, KG>), dim3(tiles), dim3(NT), 0, s, d);
+    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH, XB, KG, HL>), dim3(tiles), dim3(NT), 0, s, d);
+    else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS, WVM, WVN, FETCH, XB, KG, HL>), dim3(tiles), dim3(NT), 0, s, d);
     return hipGetLastError();
 }
 
@@ -549,6 +568,18 @@ constexpr int kMaxVariant = 31;
 template <int V, int TA, int TB>
 static hipError_t run_epi(const GemmDesc &d, hipStream_t s) {
     using P = Var<V>;
+    if (d.A2) {
+        // two-plane contractions are instantiated for the adjoint products of the f32-adjoint MLP step:
+        // dX with the ReLU mask (A K-contiguous, B MN-contiguous) and dW with the SGD update (both
+        // MN-contiguous)
+        if constexpr (TA == 0 && TB == 1) {
+            if (d.epi == EPI_MASK) return launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, 0, 1, EPI_MASK, true>(d, s);
+        }
+        if constexpr (TA == 1 && TB == 1) {
+            if (d.epi == EPI_SGD) return launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, 1, 1, EPI_SGD, true>(d, s);
+        }
+        return hipErrorInvalidValue;
+    }
 #define AH_G16_L(E) launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, TA, TB, E>(d, s)
     switch (d.epi) {
         case EPI_STORE: return AH_G16_L(EPI_STORE);

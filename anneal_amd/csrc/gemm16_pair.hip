@@ -51,7 +51,7 @@ struct G16Split {
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's partial has landed
         __syncthreads();
-        if (threadIdx.x == 0) *ticket = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) *ticket = ticket_take(count);
         __syncthreads();
         if (*ticket != nsplit - 1) return false;
         // every other split stored its partial before taking its ticket; add them in split order,

@@ -41,6 +41,7 @@ __device__ __forceinline__ float epi_apply(const GemmDesc &d, int m, int n, floa
     } else if constexpr (EPI == EPI_MASK) {
         const float v = relu_dead(in) ? 0.0f : d.scale * acc;
         C[ci] = (T)v;
+        if (sizeof(T) == 2 && d.C2) ((T *)d.C2)[ci] = (T)(v - (float)(T)v);
         return v;
     } else {  // EPI_SGD
         const float g = d.scale * acc;
@@ -149,6 +150,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
     const float sc = d.scale, lr = d.lr;
     float *const colsum = d.colsum;
     const int colsum_ld = d.colsum_ld;
+    void *const c2 = EPI == EPI_MASK ? d.C2 : nullptr;
     const int c4 = (lane & 15) * 4;
     // every slab's bias columns, loaded before the first slab (one load latency, not one per slab)
     floatx4 biasv[FN / 2];
@@ -224,6 +226,12 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
                         o[e] = (T)v[e];
                     }
                     *(T4 *)((T *)d.C + m * d.ldc + n) = o;
+                    if (sizeof(T) == 2 && c2) {   // the rounding residue as a second f16 plane
+                        T4 lo;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) lo[e] = (T)(v[e] - (float)o[e]);
+                        *(T4 *)((T *)c2 + m * d.ldc + n) = lo;
+                    }
                 } else {  // EPI_SGD
                     const floatx4 g = sc * a;
                     if (d.gout) *(floatx4 *)(d.gout + m * d.ldc + n) = g;

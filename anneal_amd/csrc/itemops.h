@@ -9,6 +9,8 @@ constexpr int kRedRows = 64;   // rows per column-reduce chunk
 
 // Zeroes `bytes` (rounded up to whole 4-byte words) with a kernel, so graph capture records no memset node.
 hipError_t zero_fill(void *p, long bytes, hipStream_t s);
+// *differs (zeroed first) becomes 1 when any of the `words` 32-bit words of a and b differ.
+hipError_t words_differ(const void *a, const void *b, long words, int *differs, hipStream_t s);
 // out[m] = scale * reduce_n G[m, n] (scale not applied to max); G is f32, or f16 when f16 is set, and the
 // reduction runs in f32.
 hipError_t reduce_rows(const void *G, bool f16, int M, int N, int op, float scale, float *out, hipStream_t s);

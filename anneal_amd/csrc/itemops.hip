@@ -21,6 +21,15 @@ __global__ void zero_u32_kernel(uint32_t *p, long n) {
     for (; i < n; i += stride) p[i] = 0u;
 }
 
+// ── word comparison: *differs = 1 when any 32-bit word of a and b differs ──
+__global__ void words_differ_kernel(const uint32_t *a, const uint32_t *b, long n, int *differs) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long stride = (long)gridDim.x * blockDim.x;
+    bool d = false;
+    for (; i < n; i += stride) d |= a[i] != b[i];
+    if (__any(d) && (threadIdx.x & 63) == 0) *differs = 1;   // a plain vector store of the same value
+}
+
 // ── reductions over a row-major [M, N] f32 matrix ──────────────────────────────────────────────────
 __device__ __forceinline__ float red_init(int op) { return op == RED_MAX ? -FLT_MAX : 0.0f; }
 __device__ __forceinline__ float red_step(int op, float acc, float v) {
@@ -205,6 +214,14 @@ hipError_t zero_fill(void *p, long bytes, hipStream_t s) {
     const long words = (bytes + 3) / 4;
     if (words <= 0) return hipSuccess;
     hipLaunchKernelGGL(zero_u32_kernel, dim3(grid_of(words, 256, 4096)), dim3(256), 0, s, (uint32_t *)p, words);
+    return hipGetLastError();
+}
+
+hipError_t words_differ(const void *a, const void *b, long words, int *differs, hipStream_t s) {
+    hipError_t e = zero_fill(differs, 4, s);
+    if (e != hipSuccess || words <= 0) return e;
+    hipLaunchKernelGGL(words_differ_kernel, dim3(grid_of(words, 256, 4096)), dim3(256), 0, s, (const uint32_t *)a,
+                       (const uint32_t *)b, words, differs);
     return hipGetLastError();
 }
 

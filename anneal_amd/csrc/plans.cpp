@@ -20,9 +20,13 @@
 #include "convnet.h"
 #include "mlpce.h"
 #include "gemm.h"
+#include "itemops.h"
 #include "rowops.h"
 
 using namespace ah;
+
+// Steps per hipGraph in ah_trainer_steps (the rest of n runs as one shorter graph).
+constexpr int kMaxGraphSteps = 16;
 
 struct ah_trainer {
     ah_device *dev = nullptr;
@@ -117,7 +121,7 @@ static int copy_in_f16(ah_device *d, half_t *dst, const float *src, size_t n) {
 
 static std::string tune_key(const GemmDesc &g) {
     char b[96];
-    snprintf(b, sizeof b, "%d/%d/%d/%d/%d/%d", g.dtype, g.ta, g.tb, g.M, g.N, g.K);
+    snprintf(b, sizeof b, "%d/%d/%d/%d/%d/%d%s", g.dtype, g.ta, g.tb, g.M, g.N, g.K, g.A2 ? "/2" : "");
     return b;
 }
 
@@ -172,9 +176,9 @@ hipError_t ah::gemm_dispatch(ah_device *dev, const GemmDesc &g) { return gemm_ru
 // Times every f16 variant of g (as given: its epilogue runs on whatever outputs g names) and caches
 // the fastest for g's shape. Two passes over the variants, each variant's time the lower of its two
 // means of `iters` launches, so one disturbed measurement does not decide the choice.
-static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us);
+static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us, bool same_bits);
 static int tune_gemm(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us) {
-    if (g.dtype == GEMM_F32) return tune_gemm_f32(dev, g, iters, best, best_us);
+    if (g.dtype == GEMM_F32) return tune_gemm_f32(dev, g, iters, best, best_us, false);
     if (g.dtype != GEMM_F16) return set_error(AH_ERR_UNSUPPORTED, "gemm tuning covers the f16 and f32 kernels");
     if (iters <= 0) return set_error(AH_ERR_INVALID, "gemm tuning: iterations must be > 0");
     hipEvent_t e0, e1;
@@ -209,8 +213,12 @@ static int tune_gemm(ah_device *dev, GemmDesc g, int iters, int *best, double *b
 
 // The f32 counterpart: times every configuration of f32_cfgs() the same way (two passes, the lower of
 // each configuration's two means) and caches the fastest one's index for g's shape (0: the automatic
-// choice). Configurations add K in different orders, so results differ at the rounding level.
-static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us) {
+// choice). Configurations add K in different orders, so results differ at the rounding level. With
+// same_bits, a configuration is a candidate only when its output is bit-identical to the automatic
+// choice's (BEAM's value guard, codegen/beam.go:410-451), checked on hash-filled operands of g's shape
+// and layout: the choice then changes only the speed, never the result, whichever configuration a
+// noisy timing picks.
+static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, double *best_us, bool same_bits) {
     if (iters <= 0) return set_error(AH_ERR_INVALID, "gemm tuning: iterations must be > 0");
     const std::vector<F32Cfg> &cfgs = f32_cfgs();
     if (dev->splitk_ws) {
@@ -219,6 +227,46 @@ static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, doubl
         g.sk_part = (float *)((char *)dev->splitk_ws + sync_bytes);
         g.sk_cap = kSplitKPartFloats;
     }
+    std::vector<char> admitted(cfgs.size(), 1);
+    if (same_bits) {
+        // the guard runs on hash-filled copies of g's operands (real operands may still be all zero),
+        // writing into scratch: C, or the gradient output of an SGD epilogue
+        GemmDesc q = g;
+        const long na = (long)(g.ta ? g.K : g.M) * g.lda, nb = (long)(g.tb ? g.K : g.N) * g.ldb;
+        const long nc = (long)(g.M - 1) * g.ldc + g.N, nx = g.aux ? (long)(g.M - 1) * g.ldaux + g.N : 0;
+        const long total = na + nb + 3 * nc + nx + (g.bias ? g.N : 0) + 64;
+        float *scr = nullptr;
+        int *flag = nullptr;
+        hipError_t e = hipMalloc(&scr, (size_t)total * 4);
+        if (e == hipSuccess) e = hipMalloc((void **)&flag, sizeof(int));
+        if (e == hipSuccess) e = fill_hash(scr, nullptr, total, 11u, 1.0f, dev->stream);
+        float *p = scr;
+        q.A = p; p += na;
+        q.B = p; p += nb;
+        float *out = p, *ref = p + nc, *w32 = p + 2 * nc;
+        p += 3 * nc;
+        if (g.aux) { q.aux = p; p += nx; }
+        if (g.bias) q.bias = p;
+        q.colsum = nullptr;
+        q.lossacc = nullptr;
+        if (g.epi == EPI_SGD) { q.W32 = w32; q.gout = out; q.C = nullptr; q.W16 = nullptr; }
+        else q.C = out;
+        q.tile = q.kgroups = q.splits = 0;
+        if (e == hipSuccess) e = gemm_launch(q, dev->stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(ref, out, (size_t)nc * 4, hipMemcpyDeviceToDevice, dev->stream);
+        for (size_t v = 1; v < cfgs.size() && e == hipSuccess; v++) {
+            q.tile = cfgs[v].tile; q.kgroups = cfgs[v].kg; q.splits = cfgs[v].splits;
+            e = gemm_launch(q, dev->stream);
+            if (e == hipSuccess) e = words_differ(out, ref, nc, flag, dev->stream);
+            int differs = 1;
+            if (e == hipSuccess) e = hipMemcpyAsync(&differs, flag, sizeof(int), hipMemcpyDeviceToHost, dev->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+            admitted[v] = e == hipSuccess && differs == 0;
+        }
+        if (scr) hipFree(scr);
+        if (flag) hipFree(flag);
+        if (e != hipSuccess) return fail_hip(e, "gemm tuning (f32 bit-identity guard)");
+    }
     hipEvent_t e0, e1;
     AH_HIP(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence));   // timing only
     AH_HIP(hipEventCreateWithFlags(&e1, hipEventDisableSystemFence));
@@ -226,6 +274,7 @@ static int tune_gemm_f32(ah_device *dev, GemmDesc g, int iters, int *best, doubl
     hipError_t err = hipSuccess;
     for (int pass = 0; pass < 2 && err == hipSuccess; pass++) {
         for (size_t v = 0; v < cfgs.size() && err == hipSuccess; v++) {
+            if (!admitted[v]) { t[v] = 1e30f; continue; }
             g.tile = cfgs[v].tile; g.kgroups = cfgs[v].kg; g.splits = cfgs[v].splits;
             err = gemm_launch(g, dev->stream);
             if (err == hipSuccess) err = hipEventRecord(e0, dev->stream);
@@ -265,6 +314,10 @@ struct MlpCeTrainer : ah_trainer {
     int Bmax, D, H, C;
     float *x, *W1, *b1, *W2, *b2, *H1, *Z2, *dZ2, *dZ1, *rowloss, *acc, *loss, *gW1, *gb1, *gW2, *gb2;
     float *dbpart = nullptr;   // softmax_ce_cols' partial rows of the output bias gradient (C <= kSoftmaxColsMaxC)
+    // dH1's column sums (the hidden bias gradient) as one partial row per 32-row block a wave of the
+    // masked contraction starts (GemmDesc::colsum_ld): plain stores summed by the tail in row order and
+    // re-zeroed there, so db1 does not depend on the order in which workgroups finish
+    float *db1part = nullptr;
     int32_t *lab;
     bool fused = false;   // the three-kernel step of mlpce.h
     int init() {
@@ -278,9 +331,11 @@ struct MlpCeTrainer : ah_trainer {
         rc |= alloc(&loss, 1); rc |= alloc(&gW1, (size_t)H * D); rc |= alloc(&gb1, H);
         rc |= alloc(&gW2, (size_t)C * H); rc |= alloc(&gb2, C);
         if (C <= kSoftmaxColsMaxC) rc |= alloc(&dbpart, (size_t)softmax_ce_cols_blocks(Bmax) * C);
+        rc |= alloc(&db1part, (size_t)((Bmax + 31) / 32) * H);
         fused = mlpce_fused_ok(Bmax, D, H, C);
         if (rc) return AH_ERR_HIP;
         AH_HIP(hipMemset(acc, 0, sizeof(float) * (H + C)));
+        AH_HIP(hipMemset(db1part, 0, sizeof(float) * ((Bmax + 31) / 32) * H));
         return AH_OK;
     }
     int set(int slot, const void *h, int64_t n) override {
@@ -306,6 +361,8 @@ struct MlpCeTrainer : ah_trainer {
     int prepare(int64_t batch) override {
         const int B = (int)batch;
         if (fused || mlp_small_ok(B, D, H, C) || tuned.count(B)) return AH_OK;
+        const char *off = getenv("AH_GEMM_TUNE");   // "0": keep the automatic choices
+        if (off && *off == '0') return AH_OK;
         // a caller capturing the device stream gets the automatic choices (timing would end its capture)
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         AH_HIP(hipStreamIsCapturing(dev->stream, &cs));
@@ -317,13 +374,20 @@ struct MlpCeTrainer : ah_trainer {
                          gdesc(GEMM_F32, EPI_SGD, 1, 1, H, D, B, dZ1, H, x, D, nullptr, D)};
         g[0].bias = b1;
         g[1].bias = b2;
-        g[2].aux = H1; g[2].ldaux = H; g[2].colsum = acc;
+        g[2].aux = H1; g[2].ldaux = H; g[2].colsum = db1part; g[2].colsum_ld = H;
         g[3].W32 = gW2; g[3].lr = 0.0f;
         g[4].W32 = gW1; g[4].lr = 0.0f;
+        // Only configurations that add K in the automatic choice's order are candidates, so the step's
+        // results do not depend on which of them timing noise selects (AH_GEMM_TUNE_ANY_ORDER=1 admits
+        // every configuration: faster on some shapes, results then equal only to rounding).
+        const char *any = getenv("AH_GEMM_TUNE_ANY_ORDER");
+        const bool same_bits = !(any && *any == '1');
+        int rc = AH_OK;
         for (GemmDesc &d : g)
-            if (!dev->gemm_variant.count(tune_key(d)))
-                if (int rc = tune_gemm(dev, d, 3, nullptr, nullptr)) return rc;
+            if (rc == AH_OK && !dev->gemm_variant.count(tune_key(d))) rc = tune_gemm_f32(dev, d, 3, nullptr, nullptr, same_bits);
+        if (rc) return rc;
         AH_HIP(hipMemsetAsync(acc, 0, sizeof(float) * (H + C), dev->stream));
+        AH_HIP(hipMemsetAsync(db1part, 0, sizeof(float) * ((Bmax + 31) / 32) * H, dev->stream));
         tuned.insert(B);
         return AH_OK;
     }
@@ -349,7 +413,7 @@ struct MlpCeTrainer : ah_trainer {
             LAUNCH("grad", mlp_small_step(x, lab, B, D, H, C, a, H1, Z2, dZ2, dZ1, rowloss, u, s, 3));
             return AH_OK;
         }
-        float *db1 = acc, *db2 = acc + H;
+        float *db2 = acc + H;
         GemmDesc g1 = gdesc(GEMM_F32, EPI_BIAS_RELU, 0, 0, B, H, D, x, D, W1, D, H1, H);
         g1.bias = b1;
         LAUNCH("fc1", gemm_run(dev, g1, s));
@@ -363,7 +427,7 @@ struct MlpCeTrainer : ah_trainer {
             LAUNCH("db2", colsum_add(dZ2, B, C, C, db2, s));
         }
         GemmDesc g3 = gdesc(GEMM_F32, EPI_MASK, 0, 1, B, H, C, dZ2, C, W2, H, dZ1, H);
-        g3.aux = H1; g3.ldaux = H; g3.colsum = db1;
+        g3.aux = H1; g3.ldaux = H; g3.colsum = db1part; g3.colsum_ld = H;
         LAUNCH("dH1", gemm_run(dev, g3, s));
         GemmDesc g4 = gdesc(GEMM_F32, EPI_SGD, 1, 1, C, H, B, dZ2, C, H1, H, nullptr, H);
         g4.W32 = W2; g4.lr = lr; g4.gout = sg ? gW2 : nullptr;
@@ -379,7 +443,7 @@ struct MlpCeTrainer : ah_trainer {
             ta.seg[0].acc_ld = C;
             ta.seg[0].keep = 1;
         }
-        ta.seg[1] = {b1, nullptr, db1, sg ? gb1 : nullptr, H, 1.0f};
+        ta.seg[1] = {b1, nullptr, db1part, sg ? gb1 : nullptr, H, 1.0f, (B + 31) / 32, (long)H, 0};
         ta.nseg = 2; ta.lr = lr; ta.loss_mode = 2; ta.loss_scale = a; ta.rowloss = rowloss; ta.nrow = B; ta.loss_out = loss;
         LAUNCH("tail", step_tail(ta, s));
         return AH_OK;
@@ -394,6 +458,12 @@ struct MlpCeTrainer : ah_trainer {
 struct Mlp3Trainer : ah_trainer {
     int B, D0, D1, D2, D3;
     half_t *X, *T, *W1h, *W2h, *W3h, *b1h, *b2h, *b3h, *H1, *H2, *Dd, *dZ2, *dZ1;
+    // f32-adjoint mode (dims[5] = 1): the masked adjoints dZ2 and dZ1 are kept as two f16 planes,
+    // hi = f16(v) in dZ2/dZ1 and lo = f16(v - hi) here, and the contractions that read them (dH1, dW2,
+    // dW1) run over both planes (GemmDesc::A2). The products are then the reference's f32-adjoint ones
+    // (tensor/ops.go:74-79, tensor/gradient_ruleset.go:114-122) to about 22 bits of the adjoint.
+    bool exact = false;
+    half_t *dZ2lo = nullptr, *dZ1lo = nullptr;
     float *W1, *W2, *W3, *b1, *b2, *b3, *acc, *loss, *lsum, *gW1, *gW2, *gW3, *gb1, *gb2, *gb3;
     // Paired launches (gemm16_pair.hip): pair 0 runs dW3 split over K beside dH1, pair 1 dW1 split
     // over K beside dW2. pair_v[p] is the variant of pair p (0: the two contractions launch apart),
@@ -406,7 +476,10 @@ struct Mlp3Trainer : ah_trainer {
     int init() {
         B = (int)dims[0]; D0 = (int)dims[1]; D1 = (int)dims[2]; D2 = (int)dims[3]; D3 = (int)dims[4];
         if (B <= 0 || D0 <= 0 || D1 <= 0 || D2 <= 0 || D3 <= 0) return set_error(AH_ERR_INVALID, "MLP3: bad dims");
+        if (dims.size() > 5 && dims[5] != 0 && dims[5] != 1) return set_error(AH_ERR_INVALID, "MLP3: dims[5] (adjoint precision) is 0 or 1");
+        exact = dims.size() > 5 && dims[5] == 1;
         int rc = 0;
+        if (exact) { rc |= alloc(&dZ2lo, (size_t)B * D2); rc |= alloc(&dZ1lo, (size_t)B * D1); }
         rc |= alloc(&X, (size_t)B * D0); rc |= alloc(&T, (size_t)B * D3);
         rc |= alloc(&W1, (size_t)D1 * D0); rc |= alloc(&W1h, (size_t)D1 * D0);
         rc |= alloc(&W2, (size_t)D2 * D1); rc |= alloc(&W2h, (size_t)D2 * D1);
@@ -472,6 +545,12 @@ struct Mlp3Trainer : ah_trainer {
             {W2, (int64_t)D2 * D1}, {b2, D2}, {W3, (int64_t)D3 * D2}, {b3, D3}, {loss, 1},
             {gW1, (int64_t)D1 * D0}, {gb1, D1}, {gW2, (int64_t)D2 * D1}, {gb2, D2}, {gW3, (int64_t)D3 * D2}, {gb3, D3},
             {lsum, 1}};
+        if (slot >= 16 && slot <= 18) {   // the step's f16 activations and loss adjoint, widened to f32
+            const half_t *src = slot == 16 ? H1 : slot == 17 ? H2 : Dd;
+            const int64_t cap = (int64_t)B * (slot == 16 ? D1 : slot == 17 ? D2 : D3);
+            if (n > cap) return set_error(AH_ERR_INVALID, "MLP3: slot %d too small", slot);
+            return ah_download(dev, (float *)h, src, n, AH_F16);
+        }
         if (slot < 2 || slot > 15) return set_error(AH_ERR_INVALID, "MLP3: bad slot %d", slot);
         if (n > t[slot].n) return set_error(AH_ERR_INVALID, "MLP3: slot %d too small", slot);
         return copy_out(dev, h, t[slot].p, (size_t)n * 4);
@@ -494,6 +573,7 @@ struct Mlp3Trainer : ah_trainer {
             case 3:
                 g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D2, D3, Dd, D3, W3h, D2, dZ2, D2);
                 g.aux = H2; g.ldaux = D2; g.colsum = db2; g.colsum_ld = D2;
+                g.C2 = dZ2lo;
                 break;
             case 4:
                 g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D3, D2, B, Dd, D3, H2, D2, nullptr, D2);
@@ -502,14 +582,17 @@ struct Mlp3Trainer : ah_trainer {
             case 5:
                 g = gdesc(GEMM_F16, EPI_MASK, 0, 1, B, D1, D2, dZ2, D2, W2h, D1, dZ1, D1);
                 g.aux = H1; g.ldaux = D1; g.colsum = db1; g.colsum_ld = D1;
+                g.A2 = dZ2lo; g.C2 = dZ1lo;
                 break;
             case 6:
                 g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D2, D1, B, dZ2, D2, H1, D1, nullptr, D1);
                 g.scale = bs; g.W32 = W2; g.W16 = W2h; g.lr = lr; g.gout = sg ? gW2 : nullptr;
+                g.A2 = dZ2lo;
                 break;
             default:
                 g = gdesc(GEMM_F16, EPI_SGD, 1, 1, D1, D0, B, dZ1, D1, X, D0, nullptr, D0);
                 g.scale = bs; g.W32 = W1; g.W16 = W1h; g.lr = lr; g.gout = sg ? gW1 : nullptr;
+                g.A2 = dZ1lo;
                 break;
         }
         return g;
@@ -647,7 +730,7 @@ struct Mlp3Trainer : ah_trainer {
         return "pair" + std::to_string(kPairSplit) + "/" + tune_key(a) + "/" + tune_key(b);
     }
     bool pair_admitted(int q) const {
-        if (!pair_count) return false;
+        if (!pair_count || exact) return false;   // the paired kernels take one-plane operands
         const GemmDesc a = gemm(q == 0 ? 4 : 7, false), b = gemm(q == 0 ? 5 : 6, false);
         auto whole = [](const GemmDesc &g) { return g.M % 256 == 0 && g.N % 256 == 0 && g.K % 256 == 0; };
         return whole(a) && whole(b) && a.K % (64 * kPairSplit) == 0 &&
@@ -914,15 +997,16 @@ int ah_trainer_create(ah_device *dev, int32_t kind, const int64_t *dims, int32_t
     hipSetDevice(dev->ordinal);
     ah_trainer *t = nullptr;
     int rc = AH_OK;
-    auto setup = [&](ah_trainer *tt, int need) {
+    auto setup = [&](ah_trainer *tt, int need, int optional = 0) {
         tt->dev = dev; tt->kind = kind; tt->lr = lr;
-        if (n_dims != need) return set_error(AH_ERR_INVALID, "kind %d needs %d dims, got %d", kind, need, n_dims);
+        if (n_dims < need || n_dims > need + optional)
+            return set_error(AH_ERR_INVALID, "kind %d needs %d dims, got %d", kind, need, n_dims);
         tt->dims.assign(dims, dims + n_dims);
         return AH_OK;
     };
     switch (kind) {
         case AH_TRAIN_MLP_CE: { auto *m = new MlpCeTrainer(); t = m; rc = setup(t, 4); if (!rc) rc = m->init(); break; }
-        case AH_TRAIN_MLP3_F16: { auto *m = new Mlp3Trainer(); t = m; rc = setup(t, 5); if (!rc) rc = m->init(); break; }
+        case AH_TRAIN_MLP3_F16: { auto *m = new Mlp3Trainer(); t = m; rc = setup(t, 5, 1); if (!rc) rc = m->init(); break; }
         case AH_TRAIN_CHAIN: { auto *m = new ChainTrainer(); t = m; rc = setup(t, 2); if (!rc) rc = m->init(); break; }
         case AH_TRAIN_CONVNET: { auto *m = new ConvNetTrainer(); t = m; rc = setup(t, 5); if (!rc) rc = m->init(); break; }
         default: return set_error(AH_ERR_INVALID, "ah_trainer_create: unknown kind %d", kind);
@@ -943,33 +1027,65 @@ int ah_trainer_get(ah_trainer *t, int32_t slot, void *host, int64_t n) {
     return t->get(slot, host, n);
 }
 
+// Replays `steps` consecutive steps as one hipGraph launch. One graph per (batch, gradient-output
+// choice, step count), captured on first use: the gradient outputs change kernels' arguments, and a
+// graph of several steps holds that many copies of the step's kernel sequence. A hipGraphLaunch costs
+// this runtime about 17 us of host time and about 4.5 us of GPU idle time per launch whatever the graph
+// holds (measured on MI355X with 1-6 short kernels per graph), so a graph of k steps pays that once per k.
+static int graph_steps(ah_trainer *t, int64_t batch, int32_t flags, int steps) {
+    const int64_t key = ((batch * 2 + ((flags & AH_STEP_STORE_GRADS) ? 1 : 0)) << 6) | steps;
+    auto it = t->graphs.find(key);
+    if (it == t->graphs.end()) {
+        int saved = t->probe_index;
+        t->probe_index = -1;
+        int rc = ah_graph_begin(t->dev);
+        if (rc) { t->probe_index = saved; return rc; }
+        int rc2 = AH_OK;
+        for (int i = 0; i < steps && rc2 == AH_OK; i++) {
+            t->launch_idx = 0;
+            rc2 = t->enqueue(batch, flags & ~AH_STEP_GRAPH);
+        }
+        ah_graph *g = nullptr;
+        rc = ah_graph_end(t->dev, &g);
+        t->probe_index = saved;
+        if (rc2) { ah_graph_destroy(g); return rc2; }
+        if (rc) return rc;
+        it = t->graphs.emplace(key, g).first;
+    }
+    return ah_graph_replay(t->dev, it->second);
+}
+
 int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags) {
     if (!t) return set_error(AH_ERR_INVALID, "ah_trainer_step: null trainer");
     if (batch <= 0 || batch > t->max_batch())
         return set_error(AH_ERR_INVALID, "ah_trainer_step: batch %lld outside [1, %d]", (long long)batch, t->max_batch());
     if (int rc = t->prepare(batch)) return rc;
-    if (flags & AH_STEP_GRAPH) {
-        // one graph per (batch, gradient-output choice): the two capture different kernels' arguments
-        const int64_t key = batch * 2 + ((flags & AH_STEP_STORE_GRADS) ? 1 : 0);
-        auto it = t->graphs.find(key);
-        if (it == t->graphs.end()) {
-            int saved = t->probe_index;
-            t->probe_index = -1;
-            int rc = ah_graph_begin(t->dev);
-            if (rc) { t->probe_index = saved; return rc; }
-            t->launch_idx = 0;
-            int rc2 = t->enqueue(batch, flags & ~AH_STEP_GRAPH);
-            ah_graph *g = nullptr;
-            rc = ah_graph_end(t->dev, &g);
-            t->probe_index = saved;
-            if (rc2) { ah_graph_destroy(g); return rc2; }
-            if (rc) return rc;
-            it = t->graphs.emplace(key, g).first;
-        }
-        return ah_graph_replay(t->dev, it->second);
-    }
+    if (flags & AH_STEP_GRAPH) return graph_steps(t, batch, flags, 1);
     t->launch_idx = 0;
     return t->enqueue(batch, flags);
+}
+
+int ah_trainer_steps(ah_trainer *t, int64_t batch, int32_t flags, int32_t n) {
+    if (!t) return set_error(AH_ERR_INVALID, "ah_trainer_steps: null trainer");
+    if (n < 0) return set_error(AH_ERR_INVALID, "ah_trainer_steps: n = %d", n);
+    if (batch <= 0 || batch > t->max_batch())
+        return set_error(AH_ERR_INVALID, "ah_trainer_steps: batch %lld outside [1, %d]", (long long)batch, t->max_batch());
+    if (n == 0) return AH_OK;
+    if (int rc = t->prepare(batch)) return rc;
+    if (!(flags & AH_STEP_GRAPH)) {
+        for (int32_t i = 0; i < n; i++) {
+            t->launch_idx = 0;
+            if (int rc = t->enqueue(batch, flags)) return rc;
+        }
+        return AH_OK;
+    }
+    // whole graphs of kMaxGraphSteps steps, then one graph of the remainder
+    for (int32_t done = 0; done < n;) {
+        const int u = std::min<int32_t>(kMaxGraphSteps, n - done);
+        if (int rc = graph_steps(t, batch, flags, u)) return rc;
+        done += u;
+    }
+    return AH_OK;
 }
 
 int ah_trainer_probe(ah_trainer *t, int32_t kernel_index) {

@@ -563,8 +563,7 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         float a = 0.0f;
         for (int c = 0; c < kResCols; c++) a += coef[5][c];
         __hip_atomic_store(lossp + strip, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket = ticket_take_atomic_partials(counter);   // lossp[] is written and read as atomics
     }
     __syncthreads();
     if (ticket != (int)gridDim.x - 1 || wave != 0) return;

@@ -91,6 +91,7 @@ struct Dim {
     long v = -1;
     bool sym = false;
     long at(const int32_t *sc, int32_t ns) const { return sym ? (ns > 0 ? sc[0] : -1) : v; }
+    int64_t with(int64_t symv) const { return sym ? symv : v; }
 };
 
 int get_dim(const Params &p, const char *k, Dim *d, bool allow_sym, bool required = true, long dflt = -1) {
@@ -182,6 +183,19 @@ int template_gemm(const Params &P, TemplateKernel *t) {
     const bool swap_ab = P.integer("swap_ab", 0) != 0;
     const int nbuf = (base.epi == EPI_STORE || grad) ? 3 : base.epi == EPI_MSE ? 6 : 4;
     if (base.epi == EPI_MSE) t->side = {{5, true}};
+    t->bytes = [base, M, N, K, grad, swap_ab](int64_t sv) -> std::vector<int64_t> {
+        const int64_t m = M.with(sv), n = N.with(sv), k = K.with(sv), es = base.dtype == GEMM_F16 ? 2 : 4;
+        const int64_t a = m * k * es, bb = n * k * es;
+        std::vector<int64_t> b = {m * n * ((base.epi == EPI_SGD || grad) ? 4 : es), swap_ab ? bb : a, swap_ab ? a : bb};
+        switch (base.epi) {
+        case EPI_BIAS: case EPI_BIAS_RELU: b.push_back(n * es); break;
+        case EPI_MASK: b.push_back(m * n * es); break;
+        case EPI_MSE: b.push_back(n * es); b.push_back(m * n * es); b.push_back((m + 31) / 32 * ((n + 31) / 32) * 4); break;
+        case EPI_SGD: if (!grad) b.push_back(m * n * 4); break;
+        default: break;
+        }
+        return b;
+    };
     const std::string key = t->key;
     t->run = [base, M, N, K, nbuf, grad, key, swap_ab](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs,
                                          const int32_t *sc, int32_t ns) -> int {
@@ -245,6 +259,10 @@ int template_reduce(const Params &P, TemplateKernel *t) {
     if (dt != "f32" && dt != "f16") return set_error(AH_ERR_UNSUPPORTED, "tmpl reduce: dtype %s", dt.c_str());
     const bool f16 = dt == "f16";
     const std::string key = t->key;
+    t->bytes = [axis, M, N, f16](int64_t sv) -> std::vector<int64_t> {
+        const int64_t m = M.with(sv), n = N.with(sv);
+        return {(axis == 0 ? n : m) * 4, m * n * (f16 ? 2 : 4)};
+    };
     t->workspace = [axis, M, N](int64_t symv) -> int64_t {
         if (axis != 0) return 0;
         const long m = M.sym ? symv : M.v, n = N.sym ? symv : N.v;
@@ -272,6 +290,10 @@ int template_softmax_ce(const Params &P, TemplateKernel *t) {
     GET("B", B, true);
     GET("C", C, false);
     t->side = {{3, false}};
+    t->bytes = [B, C](int64_t sv) -> std::vector<int64_t> {
+        const int64_t b = B.with(sv);
+        return {b * C.v * 4, b * C.v * 4, b * 4, b * 4};
+    };
     const std::string key = t->key;
     t->run = [B, C, key](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, 4)) return rc;
@@ -298,6 +320,11 @@ int template_maxpool(const Params &P, TemplateKernel *t, bool bwd) {
     if (kh.v < 1 || kw.v < 1 || sh.v < 1 || sw.v < 1 || kh.v > H.v || kw.v > W.v)
         return set_error(AH_ERR_INVALID, "tmpl %s: window %ldx%ld stride %ldx%ld on %ldx%ld", P.name.c_str(), kh.v, kw.v,
                          sh.v, sw.v, H.v, W.v);
+    t->bytes = [=](int64_t sv) -> std::vector<int64_t> {
+        const int64_t nc = N.with(sv) * C.v, in = nc * H.v * W.v * 4;
+        const int64_t out = nc * ((H.v - kh.v) / sh.v + 1) * ((W.v - kw.v) / sw.v + 1) * 4;
+        return bwd ? std::vector<int64_t>{in, in, out} : std::vector<int64_t>{out, in};
+    };
     const std::string key = t->key;
     t->run = [=](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, bwd ? 3 : 2)) return rc;
@@ -320,6 +347,10 @@ int template_pool_relu_bwd(const Params &P, TemplateKernel *t) {
     GET("C", C, false);
     GET("H", H, false);
     if (H.v % 2) return set_error(AH_ERR_INVALID, "tmpl pool_relu_bwd: H must be even");
+    t->bytes = [=](int64_t sv) -> std::vector<int64_t> {
+        const int64_t full = N.with(sv) * C.v * H.v * H.v * 4, half = full / 4;
+        return {full, half, full, half};
+    };
     const std::string key = t->key;
     t->run = [=](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, 4)) return rc;
@@ -343,6 +374,17 @@ int template_conv(const Params &P, TemplateKernel *t, ConvKind kind) {
     if (kind == CONV_FWD_POOL && H.v % 2) return set_error(AH_ERR_INVALID, "tmpl conv2d_relu_pool: H must be even");
     const int relu = (int)P.integer("relu", 0);
     if (kind == CONV_FWD_POOL) t->side = {{4, false}};
+    t->bytes = [=](int64_t sv) -> std::vector<int64_t> {
+        const int64_t n = N.with(sv), hh = H.v * H.v, xi = n * Ci.v * hh * 4, yo = n * Co.v * hh * 4;
+        const int64_t w = Co.v * Ci.v * 9 * 4, b = Co.v * 4;
+        switch (kind) {
+        case CONV_FWD: return {yo, xi, w, b};
+        case CONV_FWD_POOL: return {yo / 4, xi, w, b, yo};
+        case CONV_BWD_X: return {xi, yo, w};
+        case CONV_BWD_W: return {w, xi, yo};
+        default: return {b, yo};
+        }
+    };
     if (kind == CONV_BWD_W)
         t->workspace = [N, Ci, Co, H](int64_t symv) -> int64_t {
             const long n = N.sym ? symv : N.v;
@@ -387,6 +429,7 @@ int template_sgd(const Params &P, TemplateKernel *t) {
     Dim n;
     GET("n", n, true);
     const float lr = P.real("lr", 0.0f), scale = P.real("scale", 1.0f);
+    t->bytes = [n](int64_t sv) -> std::vector<int64_t> { const int64_t b = n.with(sv) * 4; return {b, b, b}; };
     const std::string key = t->key;
     t->run = [=](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, 3)) return rc;
@@ -401,6 +444,7 @@ int template_mse_loss(const Params &P, TemplateKernel *t) {
     Dim parts;
     GET("parts", parts, true);
     const float scale = P.real("scale", 1.0f);
+    t->bytes = [parts](int64_t sv) -> std::vector<int64_t> { return {4, parts.with(sv) * 4}; };
     const std::string key = t->key;
     t->run = [=](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, 2)) return rc;
@@ -417,6 +461,10 @@ int template_chain(const Params &P, TemplateKernel *t) {
     GET("Cc", Cc, false);
     if (R.v <= 0 || Cc.v <= 0 || Cc.v % 4) return set_error(AH_ERR_INVALID, "tmpl chain: Cc must be a positive multiple of 4");
     t->side = {{3, false}, {4, false}};
+    t->bytes = [R, Cc](int64_t) -> std::vector<int64_t> {
+        const int64_t x = R.v * Cc.v * 4;
+        return {x, x, Cc.v * 4, Cc.v * 4, 4};
+    };
     t->workspace = [R, Cc](int64_t) -> int64_t { return chain_workspace_floats((int)R.v, (int)Cc.v) * 4; };
     const std::string key = t->key;
     t->run = [=](ah_device *d, TemplateKernel *self, void *const *ptrs, int32_t n_ptrs, const int32_t *, int32_t) -> int {

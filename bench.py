@@ -29,6 +29,10 @@ PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
 # HBM bytes per launch of the dominant kernels, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
 # scaled by a plain copy of known size (read factor 2.0, write factor 1.0): profiles/hbm_traffic_pmc.md,
 # profiles/chain_resident_config5.md.
+# The CPU baseline is the oracle (a C restatement of the reference's step, OpenMP over the host cores);
+# the reference's own WebGPU path needs Go and a software Vulkan adapter, neither of which is on the box.
+CPU_LABEL = "CPU restatement \u2014 not the reference binary"
+
 TRAFFIC_BYTES = {(3, "dW2"): 268.6e6 + 100.7e6, (5, "chain_resident"): 134.8e6 + 143.0e6,
                  (5, "chain_grad"): 134.4e6 + 134.4e6,
                  (5, "chain_stats"): 134.3e6 + 4.2e6}
@@ -95,17 +99,19 @@ def cpu_baseline(cfg: int, inputs: dict):
         dt = time.perf_counter() - t0
         full = dt * (4096 / Bs)
         return {"value": 1.0 / full, "unit": "train steps/s", "cores": threads, "kind": "port",
-                "sample": f"one oracle step at batch {Bs} of 4096 (full layer widths), {dt:.1f} s, "
+                "label": CPU_LABEL, "sample": f"one oracle step at batch {Bs} of 4096 (full layer widths), {dt:.1f} s, "
                           f"scaled x{4096 // Bs} to a full step"}
     if cfg == 4:
-        Bs = 512
+        B = len(inputs["labels"])
+        Bs = min(512, B)
         q = dict(inputs)
         q["x"], q["labels"] = inputs["x"][:Bs], inputs["labels"][:Bs]
         t0 = time.perf_counter()
         O.mlp_ce_step(q, 0.01)
         dt = time.perf_counter() - t0
-        return {"value": 1.0 / (dt * 4096 / Bs), "unit": "train steps/s", "cores": threads, "kind": "port",
-                "sample": f"one oracle step at batch {Bs} of 4096, {dt:.1f} s, scaled x{4096 // Bs} to a full step"}
+        return {"value": Bs / (dt * B), "unit": "train steps/s", "cores": threads, "kind": "port",
+                "label": CPU_LABEL,
+                "sample": f"one oracle step at batch {Bs} of {B}, {dt:.1f} s, scaled x{B / Bs:g} to a full step"}
     if cfg in (1, 2):
         n, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < 10.0:
@@ -116,7 +122,7 @@ def cpu_baseline(cfg: int, inputs: dict):
             n += 1
         dt = time.perf_counter() - t0
         return {"value": n / dt, "unit": "train steps/s", "cores": threads, "kind": "port",
-                "sample": f"{n} full oracle steps in {dt:.1f} s"}
+                "label": CPU_LABEL, "sample": f"{n} full oracle steps in {dt:.1f} s"}
     if cfg == 5:
         n, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < 10.0:
@@ -124,7 +130,7 @@ def cpu_baseline(cfg: int, inputs: dict):
             n += 1
         dt = time.perf_counter() - t0
         return {"value": n / dt, "unit": "train steps/s", "cores": threads, "kind": "port",
-                "sample": f"{n} full oracle steps (X[8192,4096]) in {dt:.1f} s"}
+                "label": CPU_LABEL, "sample": f"{n} full oracle steps (X[8192,4096]) in {dt:.1f} s"}
     return None
 
 
@@ -179,12 +185,15 @@ def step_kernels(t, batch, kernels):
     return out
 
 
-def kernel_table(t, batch, kernels, steps=10):
+def kernel_table(t, batch, kernels, steps=20, warmup=50):
     """Average duration of each launch of the step (hipEvents around it, eager steps), the dominant one's
-    roofline, and the per-kernel entries."""
+    roofline, and the per-kernel entries. `warmup` untimed steps run first, whatever the command line's
+    --warmup, so the first kernels probed see the same clocks and cache state as the last."""
     kernels = step_kernels(t, batch, kernels)
     nk = t.kernel_count(batch)
     assert nk == len(kernels), (nk, len(kernels))
+    for _ in range(warmup):
+        t.step(batch)
     per = []
     for i in range(nk):
         t.probe(i)
@@ -224,25 +233,33 @@ def other_configs(dev, skip: int) -> dict:
     from anneal_amd import data
     from anneal_amd.backend import Trainer
 
-    def rate(t, batch, steps, graph):
-        for _ in range(3):
-            t.step(batch, graph=graph)
+    def rate(t, batch, steps, graph, per_launch=None):
+        # steps run by one library call (ah_trainer_steps): eager launches, or hipGraphs of up to 16 steps;
+        # per_launch=1 replays a one-step graph per step instead (one hipGraphLaunch per step)
+        def run(n):
+            if per_launch == 1:
+                for _ in range(n):
+                    t.step(batch, graph=True)
+            else:
+                t.steps(batch, n, graph=graph)
+        run(min(steps, 32))
         dev.sync()
         t0 = time.perf_counter()
-        for _ in range(steps):
-            t.step(batch, graph=graph)
+        run(steps)
         dev.sync()
         return steps / (time.perf_counter() - t0)
 
-    def entry(t, batch, kernels, steps=50, cfg=None):
-        # eager launches and hipGraph replay both timed; a step of a few short kernels is bound by the
-        # host's launch rate, where eager launches can beat a graph launch
+    def entry(t, batch, kernels, steps=50, cfg=None, jit=False):
+        # eager launches and hipGraph replay both timed; jit=True (config 4: the step captured once by
+        # tensor.JIT and replayed) reports the graph replay as the config's rate
         eager, graph = rate(t, batch, steps, False), rate(t, batch, steps, True)
+        graph1 = rate(t, batch, steps, True, per_launch=1)
         roof, rows = kernel_table(t, batch, kernels)
         if cfg is not None and (cfg, roof["kernel"]) in TRAFFIC_BYTES:
             roof["traffic"] = TRAFFIC_BYTES[(cfg, roof["kernel"])]   # measured HBM bytes per launch
-        return {"steps_per_s": max(eager, graph), "eager_steps_per_s": eager, "graph_steps_per_s": graph,
-                "roofline": roof, "kernels": rows}
+        return {"steps_per_s": graph if jit else max(eager, graph), "eager_steps_per_s": eager,
+                "graph_steps_per_s": graph, "graph_1step_launch_steps_per_s": graph1,
+                "roofline": roof, "kernels": rows, "kernels_sum_us": round(sum(r["avg_us"] for r in rows), 2)}
 
     out = {}
     if skip != 1:
@@ -264,7 +281,7 @@ def other_configs(dev, skip: int) -> dict:
         t = Trainer(dev, L.TRAIN_MLP_CE, [4096, 512, 2048, 512], 0.01)
         for k in ("x", "labels", "W1", "b1", "W2", "b2"):
             t.set(k, p[k])
-        out["config4_dynmlp_512-2048-512_f32"] = {f"N={n}": entry(t, n, mlp_ce_kernels(n, 512, 2048, 512), 100)
+        out["config4_dynmlp_512-2048-512_f32"] = {f"N={n}": entry(t, n, mlp_ce_kernels(n, 512, 2048, 512), 100, jit=True)
                                                   for n in (1, 7, 256, 4096)}
         t.close()
     if skip != 5:
@@ -281,6 +298,14 @@ def other_configs(dev, skip: int) -> dict:
             t.set(k, v)
         out["config3_f16_mlp_b4096"] = entry(t, batch, ks, 20)
         t.close()
+    # config 3 with the reference's f32 adjoints (dims[5] = 1: the masked adjoints as two f16 planes, so
+    # dH1, dW2 and dW1 contract twice over K); the kernel table's FLOP figures stay the algorithmic ones
+    kind, dims, lr, batch, p, ks, _ = config_workload(3)
+    t = Trainer(dev, kind, dims + [1], lr)
+    for k, v in p.items():
+        t.set(k, v)
+    out["config3_f16_mlp_b4096_f32_adjoint"] = entry(t, batch, ks, 20)
+    t.close()
     return out
 
 
@@ -380,7 +405,8 @@ def main():
     for _ in range(args.warmup):
         t.step(batch)
     dev.sync()
-    # Calibration (outside the timed region): each kernel's average duration over 10 steps.
+    # Calibration (outside the timed region): 50 more untimed steps, then each kernel's average duration
+    # over 20 steps.
     kernels = step_kernels(t, batch, kernels)
     _, kinfo = kernel_table(t, batch, kernels)
     dom = int(np.argmax([k["avg_us"] for k in kinfo]))
@@ -414,7 +440,8 @@ def main():
         "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": meta["dtype"], "data": "synthetic (splitmix64 seed 0, anneal_amd/data.py)",
         "config": {"workload": meta["workload"], "batch": meta["batch"], "parallelism": "single-gpu"},
-        "roofline": roof, "kernels": kinfo, "device": caps["arch"], "cu_count": caps["cu_count"],
+        "roofline": roof, "kernels": kinfo, "kernels_sum_us": round(sum(k["avg_us"] for k in kinfo), 2),
+        "device": caps["arch"], "cu_count": caps["cu_count"],
     }
     if "flop_per_step" in meta:
         out["step_tflops"] = meta["flop_per_step"] * sps / 1e12

@@ -292,7 +292,10 @@ int ah_chain_step_noalloc(ah_device *dev, const float *X, const float *g, int32_
 enum {
     AH_TRAIN_MLP_CE = 1,    /* dims {Bmax, D, H, C}: configs 1 and 4 */
     AH_TRAIN_CONVNET = 2,   /* dims {N, Hin, C1, C2, NC}: config 2 */
-    AH_TRAIN_MLP3_F16 = 3,  /* dims {B, D0, D1, D2, D3}: config 3 */
+    AH_TRAIN_MLP3_F16 = 3,  /* dims {B, D0, D1, D2, D3[, adjoint]}: config 3; adjoint 1 keeps the masked
+                               adjoints dZ2, dZ1 at f32 precision as two f16 planes (hi, lo) and contracts
+                               both (dH1, dW2, dW1 then cost two passes over K); 0 (default) rounds them
+                               to f16 */
     AH_TRAIN_CHAIN = 4,     /* dims {R, Cc}: config 5 */
 };
 /* Slot numbering per kind (host arrays are f32 unless noted; labels are int32):
@@ -300,7 +303,9 @@ enum {
  *  CONVNET: 0 x, 1 labels, 2 cw1, 3 cb1, 4 cw2, 5 cb2, 6 fw, 7 fb, 8 loss, 9 dcw1, 10 dcb1, 11 dcw2,
  *           12 dcb2, 13 dfw, 14 dfb
  *  MLP3   : 0 x, 1 t, 2 W1, 3 b1, 4 W2, 5 b2, 6 W3, 7 b3, 8 loss, 9 dW1, 10 db1, 11 dW2, 12 db2,
- *           13 dW3, 14 db3, 15 loss_sum (the f32 sum of squares before the f16 narrowing of the loss)
+ *           13 dW3, 14 db3, 15 loss_sum (the f32 sum of squares before the f16 narrowing of the loss),
+ *           16 H1, 17 H2 (the f16 ReLU outputs of the last step, widened; -0.0 marks a dead unit),
+ *           18 d = f16(P - t) (the last step's loss adjoint before the factor 2/(B*D3)) — read only
  *  CHAIN  : 0 X, 1 g, 2 loss, 3 dX, 4 dg
  * Gradient slots are filled only by steps run with AH_STEP_STORE_GRADS.
  * Creating an MLP3 trainer tunes its f16 contractions for shapes the device has not tuned yet: each alone
@@ -314,6 +319,11 @@ void ah_trainer_destroy(ah_trainer *t);
 int ah_trainer_set(ah_trainer *t, int32_t slot, const void *host, int64_t n);
 int ah_trainer_get(ah_trainer *t, int32_t slot, void *host, int64_t n);
 int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags);
+/* n consecutive steps (tensor.JIT's replay loop, tensor/jit.go:176-215, with the inputs left in place).
+ * With AH_STEP_GRAPH the steps run as hipGraph launches of up to 16 steps each, each graph captured once
+ * per (batch, flags, steps) and replayed: a graph launch has a fixed host and GPU cost, paid once per
+ * graph rather than once per step. Without it, n eager steps. */
+int ah_trainer_steps(ah_trainer *t, int64_t batch, int32_t flags, int32_t n);
 /* Per-kernel probe: hipEvents around the index-th kernel launch of every following step. */
 int ah_trainer_probe(ah_trainer *t, int32_t kernel_index);
 int ah_trainer_probe_read(ah_trainer *t, double *total_ms, int64_t *count);

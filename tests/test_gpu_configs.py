@@ -206,8 +206,10 @@ def test_convnet_per_op_path(dev):
     t.close()
 
 
-def test_config2_tie_split_bit_exact(dev):
-    """All-equal pooling windows (ReLU zeros) must split the adjoint exactly like the oracle."""
+def test_config2_pool_ties_vs_oracle(dev):
+    """All-equal pooling windows (ReLU zeros): the config-2 step's conv gradients match the oracle's tie
+    split at the f32 reduction bar (1e-4). The bit-exact check of the split itself is
+    tests/test_gpu_items.py (maxpool and pool-ReLU backward against the oracle's tables)."""
     p = data.convnet_inputs(N=4, seed=3)
     p["x"] = np.zeros_like(p["x"])                 # every conv output equals its bias -> many ties
     p["cb1"] = np.array([0.5, -0.5, 0, 0.25, 0, -1, 1, 0], np.float32)
@@ -221,10 +223,10 @@ def test_config2_tie_split_bit_exact(dev):
     t.close()
 
 
-def run_mlp3(dev, p, lr):
+def run_mlp3(dev, p, lr, adjoint32=False):
     B, D0 = p["x"].shape
     D1, D2, D3 = p["W1"].shape[0], p["W2"].shape[0], p["W3"].shape[0]
-    t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], lr)
+    t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3] + ([1] if adjoint32 else []), lr)
     for k in ("x", "t", "W1", "b1", "W2", "b2", "W3", "b3"):
         t.set(k, p[k])
     t.step(B, store_grads=True)
@@ -449,3 +451,76 @@ def test_config4_first_step_captured_by_caller(dev):
         out[k] = t.get(k, n)
     t.close()
     check_mlp(out, p, 0.01)
+
+
+@pytest.mark.parametrize("N", [256, 4096])
+def test_config4_tuning_changes_no_bit(dev, monkeypatch, N):
+    """The f32 trainer tunes its contractions before a batch's first step, but only among configurations
+    whose output is bit-identical to the automatic choice's: a tuned step equals, bit for bit, the step of
+    a trainer that keeps the automatic choices (AH_GEMM_TUNE=0)."""
+    from anneal_amd.backend import Device
+    p = data.mlp_ce_inputs(N, 512, 2048, 512, x_lo=-1.0, x_hi=1.0, seed=5)
+    with Device(0) as d1:
+        a = run_mlp_ce(d1, p, N, 0.01)
+    monkeypatch.setenv("AH_GEMM_TUNE", "0")
+    with Device(0) as d2:
+        b = run_mlp_ce(d2, p, N, 0.01)
+    for k in a:
+        np.testing.assert_array_equal(np.asarray(a[k]).view(np.uint32), np.asarray(b[k]).view(np.uint32), err_msg=k)
+
+
+@pytest.mark.parametrize("shape", [(256, 128, 256, 256, 128), (512, 256, 512, 384, 256)])
+def test_config3_f32_adjoint_vs_oracle(dev, shape):
+    """f32-adjoint mode (dims[5] = 1): the masked adjoints travel as two f16 planes, so the backward
+    products are the reference's f32-adjoint ones (tensor/ops.go:74-79). Against the C oracle the
+    gradients then agree at the f32 reduction bar (1e-4) instead of the f16 one."""
+    B, D0, D1, D2, D3 = shape
+    p = data.mlp3_inputs(B, D0, D1, D2, D3)
+    q = dict(p)
+    q["x"], q["t"] = data.f16_quantize(p["x"]), data.f16_quantize(p["t"])
+    lr = 1e-3
+    out = run_mlp3(dev, p, lr, adjoint32=True)
+    wl, g, new = O.mlp3_step(q, lr)
+    for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3"):
+        assert O.relerr(out[k], g[k].ravel()) < 1e-4, k
+    for k in ("W1", "b1", "W2", "b2", "W3", "b3"):
+        assert check_update(out[k], p[k], new[k], 1e-4), k
+
+
+def test_config3_f32_adjoint_full_size(dev):
+    """The f32-adjoint mode at the full config-3 shape. Against a restatement that computes the forward
+    in another summation order, both modes differ by the same ~1e-3 (f16 rounding flips of the forward
+    activations and ReLU masks, identical in the two modes), so the adjoint's precision is judged on the
+    step's own forward: the f16 activations H1, H2 and the adjoint d = f16(P - t) the trainer used are
+    read back, and the backward is recomputed from them in float64. There the f32-adjoint dW2 and dW1
+    meet the f32 reduction bar (1e-4), and the default mode shows what rounding the adjoints to f16 costs."""
+    p = data.mlp3_inputs()
+    B, D0 = p["x"].shape
+    D1, D2, D3 = p["W1"].shape[0], p["W2"].shape[0], p["W3"].shape[0]
+    x16 = data.f16_quantize(p["x"]).astype(np.float64)
+    w2h = data.f16_quantize(p["W2"]).astype(np.float64)
+    w3h = data.f16_quantize(p["W3"]).astype(np.float64)
+    err = {}
+    for mode in (0, 1):
+        t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3, mode], 1e-3)
+        for k in ("x", "t", "W1", "b1", "W2", "b2", "W3", "b3"):
+            t.set(k, p[k])
+        t.step(B, store_grads=True)
+        H1 = t.get("H1", B * D1).reshape(B, D1)
+        H2 = t.get("H2", B * D2).reshape(B, D2)
+        d = t.get("d", B * D3).reshape(B, D3).astype(np.float64)
+        got = {k: t.get(k, n) for k, n in (("dW2", D2 * D1), ("dW1", D1 * D0), ("db2", D2), ("db1", D1))}
+        t.close()
+        dead1 = (H1 == 0) & np.signbit(H1)
+        dead2 = (H2 == 0) & np.signbit(H2)
+        s = 2.0 / (B * D3)
+        dZ2 = np.where(dead2, 0.0, s * (d @ w3h))
+        dZ1 = np.where(dead1, 0.0, dZ2 @ w2h)
+        want = {"dW2": dZ2.T @ H1.astype(np.float64), "dW1": dZ1.T @ x16, "db2": dZ2.sum(0), "db1": dZ1.sum(0)}
+        err[mode] = {k: O.relerr(got[k], want[k].ravel()) for k in want}
+    print("config-3 full size, relative error vs the float64 backward of the step's own forward:",
+          {("f16-adjoint" if m == 0 else "f32-adjoint"): {k: f"{v:.2e}" for k, v in e.items()} for m, e in err.items()})
+    for k, v in err[1].items():
+        assert v < 1e-4, k
+    for k in ("dW2", "dW1"):
+        assert err[1][k] <= err[0][k], k

@@ -116,3 +116,40 @@ def test_benchmark_stats(dev):
     assert r.stddev_us >= 0 and r.cv >= 0
     with pytest.raises(L.AnnealHipError):
         ex.benchmark(item, 0, 0)
+
+
+@pytest.mark.parametrize("which", ["A", "B", "C", "bias"])
+def test_template_key_larger_than_its_buffers_is_refused(dev, which):
+    """A tmpl:gemm key whose M/N/K need more elements than a bound buffer holds is an error before any
+    launch (the hand-written kernels index by the key's shape), naming the PARAM; the same item with
+    buffers of the right size runs."""
+    M, N, K = 64, 96, 128
+    sizes = {"C": M * N, "A": M * K, "B": N * K, "bias": N}
+    short = dict(sizes)
+    short[which] -= 1
+    key = f"tmpl:gemm;dtype=f32;epi=bias;ta=0;tb=0;M={M};N={N};K={K}"
+
+    def item(sz):
+        return ExecItem(key, [Buffer(10, sz["C"], [sz["C"]]), Buffer(1, sz["A"], [sz["A"]]),
+                              Buffer(2, sz["B"], [sz["B"]]), Buffer(3, sz["bias"], [sz["bias"]])])
+    rng = np.random.default_rng(3)
+    ins = {1: rng.standard_normal(M * K, dtype=np.float32), 2: rng.standard_normal(N * K, dtype=np.float32),
+           3: np.zeros(N, np.float32)}
+    with pytest.raises(L.AnnealHipError, match="PARAM"):
+        Executor(dev).run([item(short)], ins)
+    out = Executor(dev).run([item(sizes)], ins)[10].reshape(M, N)
+    want = ins[1].reshape(M, K).astype(np.float64) @ ins[2].reshape(N, K).T.astype(np.float64)
+    assert np.abs(out - want).max() < 1e-4 * np.abs(want).max()
+
+
+def test_symbolic_template_checked_against_the_binding(dev):
+    """With a symbolic M the check uses the bound value: a binding larger than the fixed-size A buffer
+    allows is refused."""
+    N, K = 32, 64
+    key = f"tmpl:gemm;dtype=f32;epi=store;ta=0;tb=0;M=sym;N={N};K={K}"
+    it = ExecItem(key, [Buffer(10, 0, [0, N]), Buffer(1, 8 * K, [8 * K]), Buffer(2, N * K, [N * K])], sym_vars=["N"])
+    ins = {1: np.ones(8 * K, np.float32), 2: np.ones(N * K, np.float32)}
+    out = Executor(dev).run_symbolic([it], ins, {"N": 8})
+    np.testing.assert_array_equal(out[10], np.full(8 * N, K, np.float32))
+    with pytest.raises(L.AnnealHipError, match="PARAM 1"):
+        Executor(dev).run_symbolic([it], ins, {"N": 9})
