@@ -117,6 +117,7 @@ SIGNATURES = {
     "ah_gemm": (C.c_int, [_P, C.POINTER(ah_gemm_desc)]),
     "ah_translate_wgsl": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
     "ah_wgsl_template_key": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int32]),
+    "ah_wgsl_plan": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int32]),
     "ah_ckpt_open": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
     "ah_ckpt_count": (C.c_int32, [_P]),
     "ah_ckpt_entry": (C.c_int, [_P, C.c_int32, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.POINTER(C.c_int32),
@@ -179,6 +180,13 @@ def wgsl_template_key(src: str) -> str:
     """The "tmpl:..." key ah_module_get runs in place of a WGSL kernel that is a plain contraction, or ""."""
     buf = C.create_string_buffer(256)
     check(load().ah_wgsl_template_key(src.encode(), buf, 256))
+    return buf.value.decode()
+
+
+def wgsl_plan(src: str) -> str:
+    """How ah_module_get runs a rendered WGSL kernel: its "tmpl:..." key, "wave" or "thread"."""
+    buf = C.create_string_buffer(256)
+    check(load().ah_wgsl_plan(src.encode(), buf, 256))
     return buf.value.decode()
 
 

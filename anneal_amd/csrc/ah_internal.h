@@ -55,6 +55,9 @@ hipError_t gemm_dispatch(ah_device *dev, const GemmDesc &g);
 struct ah_kernel {
     hipModule_t module = nullptr;
     hipFunction_t function = nullptr;
+    // rendered in the wave-per-output form (wgsl.cpp): launched with one 64-lane block per thread of the
+    // item's grid x block
+    bool wave = false;
     ah::TemplateKernel *tmpl = nullptr;
 };
 
@@ -85,7 +88,7 @@ int template_create(const std::string &source, TemplateKernel **out);
 std::unordered_map<std::string, std::string> template_key_params(const std::string &key, std::string *name);
 // Grows the template's workspace for the binding symval (before a graph capture).
 int template_prepare(TemplateKernel *t, int64_t symval);
-std::string wgsl_to_hip(const std::string &src, std::string *err);
+std::string wgsl_to_hip(const std::string &src, std::string *err, bool *wave = nullptr);
 // A "tmpl:gemm" key for a WGSL kernel that is a plain contraction (wgsl_match.cpp), else false.
 bool wgsl_match_contraction(const std::string &src, std::string *key);
 }

@@ -9,6 +9,9 @@ constexpr int kRedRows = 64;   // rows per column-reduce chunk
 
 // Zeroes `bytes` (rounded up to whole 4-byte words) with a kernel, so graph capture records no memset node.
 hipError_t zero_fill(void *p, long bytes, hipStream_t s);
+// Contraction operand prologues: dst = z ? Where(z == max(z, 0), src, 0) : max(src, 0), n elements of f32
+// (or f16 when f16 is set).
+hipError_t operand_prologue(const void *src, const void *z, bool f16, long n, void *dst, hipStream_t s);
 // *differs (zeroed first) becomes 1 when any of the `words` 32-bit words of a and b differ.
 hipError_t words_differ(const void *a, const void *b, long words, int *differs, hipStream_t s);
 // out[m] = scale * reduce_n G[m, n] (scale not applied to max); G is f32, or f16 when f16 is set, and the

@@ -30,6 +30,20 @@ __global__ void words_differ_kernel(const uint32_t *a, const uint32_t *b, long n
     if (__any(d) && (threadIdx.x & 63) == 0) *differs = 1;   // a plain vector store of the same value
 }
 
+// ── contraction operand prologues ──
+// ReLU is Maximum(x, 0) in the reference; its backward keeps adj where z == max(z, 0), i.e. z >= 0
+// (-0 included, NaN excluded, as the comparison there decides).
+template <typename T>
+__global__ void operand_prologue_kernel(const T *src, const T *z, long n, T *dst) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        const T v = src[i];
+        if (z) dst[i] = z[i] >= (T)0.0f ? v : (T)0.0f;
+        else dst[i] = v > (T)0.0f ? v : (T)0.0f;
+    }
+}
+
 // ── reductions over a row-major [M, N] f32 matrix ──────────────────────────────────────────────────
 __device__ __forceinline__ float red_init(int op) { return op == RED_MAX ? -FLT_MAX : 0.0f; }
 __device__ __forceinline__ float red_step(int op, float acc, float v) {
@@ -214,6 +228,17 @@ hipError_t zero_fill(void *p, long bytes, hipStream_t s) {
     const long words = (bytes + 3) / 4;
     if (words <= 0) return hipSuccess;
     hipLaunchKernelGGL(zero_u32_kernel, dim3(grid_of(words, 256, 4096)), dim3(256), 0, s, (uint32_t *)p, words);
+    return hipGetLastError();
+}
+
+hipError_t operand_prologue(const void *src, const void *z, bool f16, long n, void *dst, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (f16)
+        hipLaunchKernelGGL(operand_prologue_kernel<half_t>, dim3(grid_of(n, 256, 8192)), dim3(256), 0, s, (const half_t *)src,
+                           (const half_t *)z, n, (half_t *)dst);
+    else
+        hipLaunchKernelGGL(operand_prologue_kernel<float>, dim3(grid_of(n, 256, 8192)), dim3(256), 0, s, (const float *)src,
+                           (const float *)z, n, (float *)dst);
     return hipGetLastError();
 }
 

@@ -262,7 +262,9 @@ int ah_module_get(ah_device *d, const char *source, const char *entry, ah_kernel
         const bool from_wgsl = strstr(source, "@compute") != nullptr;
         if (from_wgsl) {
             std::string err;
-            hip_src = wgsl_to_hip(source, &err);
+            const char *wv = getenv("AH_WGSL_WAVE");   // "0": one thread per output, as the WGSL is written
+            const bool try_wave = !(wv && strcmp(wv, "0") == 0);
+            hip_src = wgsl_to_hip(source, &err, try_wave ? &k->wave : nullptr);
             if (hip_src.empty()) {
                 delete k;
                 return set_error(AH_ERR_COMPILE, "wgsl: %s", err.c_str());
@@ -312,13 +314,17 @@ int ah_launch(ah_device *d, ah_kernel *k, const uint32_t grid[3], const uint32_t
     if (!d || !k) return set_error(AH_ERR_INVALID, "ah_launch: null argument");
     if (k->tmpl) return k->tmpl->run(d, k->tmpl, ptrs, n_ptrs, scalars, n_scalars);
     if (!grid || !block) return set_error(AH_ERR_INVALID, "ah_launch: null grid/block");
+    uint32_t g[3] = {grid[0], grid[1], grid[2]}, b[3] = {block[0], block[1], block[2]};
+    if (k->wave) {   // one 64-lane block per original thread
+        for (int a = 0; a < 3; a++) { g[a] = grid[a] * block[a]; b[a] = 1; }
+        b[0] = 64;
+    }
     std::vector<void *> args;
     std::vector<void *> pv(ptrs, ptrs + n_ptrs);
     std::vector<int32_t> sv(scalars, scalars + n_scalars);
     for (auto &p : pv) args.push_back(&p);
     for (auto &s : sv) args.push_back(&s);
-    AH_HIP(hipModuleLaunchKernel(k->function, grid[0], grid[1], grid[2], block[0], block[1], block[2], 0, d->stream,
-                                 args.data(), nullptr));
+    AH_HIP(hipModuleLaunchKernel(k->function, g[0], g[1], g[2], b[0], b[1], b[2], 0, d->stream, args.data(), nullptr));
     return AH_OK;
 }
 
@@ -389,5 +395,22 @@ extern "C" int ah_wgsl_template_key(const char *wgsl, char *buf, int32_t cap) {
         return AH_OK;
     }
     snprintf(buf, (size_t)cap, "%s", key.c_str());
+    return AH_OK;
+}
+
+extern "C" int ah_wgsl_plan(const char *wgsl, char *buf, int32_t cap) {
+    if (!wgsl || !buf || cap <= 0) return set_error(AH_ERR_INVALID, "ah_wgsl_plan: null argument");
+    std::string out;
+    const char *sel = getenv("AH_WGSL_TEMPLATES");
+    if (!(sel && strcmp(sel, "0") == 0) && ah::wgsl_match_contraction(wgsl, &out)) {
+    } else {
+        std::string err;
+        bool wave = false;
+        const char *wv = getenv("AH_WGSL_WAVE");
+        const bool try_wave = !(wv && strcmp(wv, "0") == 0);
+        if (ah::wgsl_to_hip(wgsl, &err, try_wave ? &wave : nullptr).empty()) return set_error(AH_ERR_COMPILE, "wgsl: %s", err.c_str());
+        out = wave ? "wave" : "thread";
+    }
+    snprintf(buf, (size_t)cap, "%s", out.c_str());
     return AH_OK;
 }

@@ -29,6 +29,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 
 #include "ah_internal.h"
@@ -134,7 +135,13 @@ int ensure_ws(TemplateKernel *t, int64_t bytes) {
 
 // ── gemm ─────────────────────────────────────────────────────────────────────────────────────────
 // "tmpl:gemm;dtype=f16|f32;epi=...;ta=0|1;tb=0|1;M=..;N=..;K=..[;scale=s][;lr=l][;variant=v][;tile=t;kg=g]
-//  [;swap_ab=1]" (swap_ab: A is the second input PARAM and B the first)
+//  [;swap_ab=1][;in_a=i;in_b=j;in_bias=k][;pa=relu|mask;za=z][;pb=relu|mask;zb=z]"
+// swap_ab: A is the second input PARAM and B the first; in_a / in_b / in_bias name the PARAM of each role
+// outright (a rendered kernel binds its inputs in the scheduler's order). Operand prologues, the
+// elementwise ops the reference's scheduler inlines into a contraction's loop: pa=relu reads max(A, 0)
+// (ReLU = Maximum(x, 0), tensor/nn/nn.go:111-114), pa=mask reads Where(Z == max(Z, 0), A, 0) with Z the
+// PARAM za (the ReLU backward rule, tensor/gradient_ruleset.go:153-161); pb/zb likewise for B. A
+// prologue is applied in one elementwise pass into the template's workspace before the MFMA kernel.
 // variant picks an f16 kernel variant, tile (64/128/256) and kg (k-groups) the f32 tiled kernel's shape.
 // M, N and K may be symbolic. PARAMs by epilogue:
 //   store      C, A, B                     C = scale*acc
@@ -181,38 +188,82 @@ int template_gemm(const Params &P, TemplateKernel *t) {
     base.splits = (int)P.integer("splits", 0);
     if (base.splits < 0 || base.splits > 16) return set_error(AH_ERR_INVALID, "tmpl gemm: splits=%d (0..16)", base.splits);
     const bool swap_ab = P.integer("swap_ab", 0) != 0;
-    const int nbuf = (base.epi == EPI_STORE || grad) ? 3 : base.epi == EPI_MSE ? 6 : 4;
+    // PARAM of each role: A, B, bias (or the first epilogue input), and the prologues' mask sources
+    const int pA = (int)P.integer("in_a", swap_ab ? 2 : 1), pB = (int)P.integer("in_b", swap_ab ? 1 : 2);
+    const int pBias = (int)P.integer("in_bias", 3);
+    static const std::map<std::string, int> pros = {{"", 0}, {"relu", 1}, {"mask", 2}};
+    auto pa_it = pros.find(P.str("pa", "")), pb_it = pros.find(P.str("pb", ""));
+    if (pa_it == pros.end() || pb_it == pros.end()) return set_error(AH_ERR_UNSUPPORTED, "tmpl gemm: prologue must be relu or mask");
+    const int proA = pa_it->second, proB = pb_it->second;
+    const int pZa = proA == 2 ? (int)P.integer("za", -1) : -1, pZb = proB == 2 ? (int)P.integer("zb", -1) : -1;
+    if ((proA == 2 && pZa < 1) || (proB == 2 && pZb < 1)) return set_error(AH_ERR_INVALID, "tmpl gemm: a mask prologue names its Z PARAM (za/zb)");
+    if ((proA || proB) && (base.epi == EPI_MSE || base.epi == EPI_MASK || base.epi == EPI_SGD))
+        return set_error(AH_ERR_UNSUPPORTED, "tmpl gemm: prologues with the store/bias/bias_relu/grad epilogues");
+    if (pA < 1 || pB < 1 || pA == pB) return set_error(AH_ERR_INVALID, "tmpl gemm: in_a/in_b must name two input PARAMs");
+    int nbuf = (base.epi == EPI_STORE || grad) ? 3 : base.epi == EPI_MSE ? 6 : 4;
+    for (int q : {pA + 1, pB + 1, pZa + 1, pZb + 1}) nbuf = std::max(nbuf, q);
+    if (base.epi == EPI_BIAS || base.epi == EPI_BIAS_RELU) nbuf = std::max(nbuf, pBias + 1);
     if (base.epi == EPI_MSE) t->side = {{5, true}};
-    t->bytes = [base, M, N, K, grad, swap_ab](int64_t sv) -> std::vector<int64_t> {
-        const int64_t m = M.with(sv), n = N.with(sv), k = K.with(sv), es = base.dtype == GEMM_F16 ? 2 : 4;
-        const int64_t a = m * k * es, bb = n * k * es;
-        std::vector<int64_t> b = {m * n * ((base.epi == EPI_SGD || grad) ? 4 : es), swap_ab ? bb : a, swap_ab ? a : bb};
+    const int es = base.dtype == GEMM_F16 ? 2 : 4;
+    // workspace: the prologue outputs, A' then B' at a 256-byte boundary
+    auto ws_layout = [M, N, K, proA, proB, es](int64_t sv, int64_t *offB) -> int64_t {
+        const int64_t a = proA ? M.with(sv) * K.with(sv) * es : 0, b = proB ? N.with(sv) * K.with(sv) * es : 0;
+        *offB = (a + 255) / 256 * 256;
+        return *offB + b;
+    };
+    if (proA || proB)
+        t->workspace = [ws_layout](int64_t sv) -> int64_t { int64_t ob; return ws_layout(sv, &ob); };
+    t->bytes = [base, M, N, K, grad, pA, pB, pBias, pZa, pZb, nbuf, es](int64_t sv) -> std::vector<int64_t> {
+        const int64_t m = M.with(sv), n = N.with(sv), k = K.with(sv);
+        std::vector<int64_t> b(nbuf, 0);
+        b[0] = m * n * ((base.epi == EPI_SGD || grad) ? 4 : es);
+        b[pA] = m * k * es;
+        b[pB] = n * k * es;
+        if (pZa > 0) b[pZa] = m * k * es;
+        if (pZb > 0) b[pZb] = n * k * es;
         switch (base.epi) {
-        case EPI_BIAS: case EPI_BIAS_RELU: b.push_back(n * es); break;
-        case EPI_MASK: b.push_back(m * n * es); break;
-        case EPI_MSE: b.push_back(n * es); b.push_back(m * n * es); b.push_back((m + 31) / 32 * ((n + 31) / 32) * 4); break;
-        case EPI_SGD: if (!grad) b.push_back(m * n * 4); break;
+        case EPI_BIAS: case EPI_BIAS_RELU: b[pBias] = n * es; break;
+        case EPI_MASK: b[3] = m * n * es; break;
+        case EPI_MSE: b[3] = n * es; b[4] = m * n * es; b[5] = (m + 31) / 32 * ((n + 31) / 32) * 4; break;
+        case EPI_SGD: if (!grad) b[3] = m * n * 4; break;
         default: break;
         }
         return b;
     };
     const std::string key = t->key;
-    t->run = [base, M, N, K, nbuf, grad, key, swap_ab](ah_device *d, TemplateKernel *, void *const *ptrs, int32_t n_ptrs,
-                                         const int32_t *sc, int32_t ns) -> int {
+    t->run = [base, M, N, K, nbuf, grad, key, pA, pB, pBias, proA, proB, pZa, pZb, ws_layout](
+                 ah_device *d, TemplateKernel *self, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, nbuf)) return rc;
         GemmDesc g = base;
         AT(M, m);
         AT(N, n);
         AT(K, k);
         g.M = (int)m; g.N = (int)n; g.K = (int)k;
-        g.A = ptrs[swap_ab ? 2 : 1];   // swap_ab: the first-bound input is B
-        g.B = ptrs[swap_ab ? 1 : 2];
+        g.A = ptrs[pA];
+        g.B = ptrs[pB];
         g.lda = g.ta ? g.M : g.K;
         g.ldb = g.tb ? g.N : g.K;
         g.ldc = g.N;
         g.C = ptrs[0];
+        if (proA || proB) {   // prologues into the workspace, then the contraction reads them there
+            const int64_t sv = (M.sym || N.sym || K.sym) && ns > 0 ? sc[0] : 0;
+            int64_t offB = 0;
+            const int64_t bytes = ws_layout(sv, &offB);
+            if (int rc = ensure_ws(self, bytes)) return rc;
+            const bool f16 = base.dtype == GEMM_F16;
+            if (proA) {
+                void *dst = self->ws;
+                AH_HIP(operand_prologue(ptrs[pA], proA == 2 ? ptrs[pZa] : nullptr, f16, m * k, dst, d->stream));
+                g.A = dst;
+            }
+            if (proB) {
+                void *dst = (char *)self->ws + offB;
+                AH_HIP(operand_prologue(ptrs[pB], proB == 2 ? ptrs[pZb] : nullptr, f16, n * k, dst, d->stream));
+                g.B = dst;
+            }
+        }
         switch (g.epi) {
-        case EPI_BIAS: case EPI_BIAS_RELU: g.bias = ptrs[3]; break;
+        case EPI_BIAS: case EPI_BIAS_RELU: g.bias = ptrs[pBias]; break;
         case EPI_MASK: g.aux = ptrs[3]; g.ldaux = g.N; break;
         case EPI_MSE:
             g.bias = ptrs[3]; g.aux = ptrs[4]; g.ldaux = g.N; g.lossacc = (float *)ptrs[5];

@@ -67,6 +67,14 @@ template <class To, class From> __device__ __forceinline__ To wg_bitcast(From v)
     else if constexpr (sizeof(To) == 2) return __builtin_bit_cast(To, (unsigned short)v);
     else return __builtin_bit_cast(To, (unsigned)__builtin_bit_cast(unsigned short, v));
 }
+__device__ __forceinline__ float wg_wave_sum(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wg_wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
 struct wg_vec4 { float x, y, z, w; };
 __device__ __forceinline__ wg_vec4 wg_make4(float a, float b, float c, float d) { return wg_vec4{a, b, c, d}; }
 __device__ __forceinline__ wg_vec4 wg_make4(float a) { return wg_vec4{a, a, a, a}; }
@@ -288,8 +296,76 @@ bool decl(const std::string &rest, bool is_const, std::string &out, std::string 
 
 }  // namespace
 
-// Returns HIP source with an extern "C" entry point `kernel`, or "" with *err set.
-std::string wgsl_to_hip(const std::string &src, std::string *err) {
+// Wave-per-output form of a single-reduce kernel. codegen/lower.go:654-719 gives every output element
+// one thread that runs the whole reduce loop serially. When the body is exactly: output-axis lets and
+// guards, one f32 accumulator, one outermost loop (nested loops inside allowed) whose statements are lets
+// and the accumulator's update `acc = acc + e` or `acc = max(acc, e)`, then lets and stores, the kernel
+// is rendered with one 64-lane wave per output element instead: lane l runs the outermost loop's
+// iterations l, l+64, ..., the lanes' partials are combined by a shuffle tree (sum or max), and lane 0
+// runs the statements after the loop. Sums then add in a different (fixed) order than the serial loop.
+// Returns the line indices (of `lines`) of the accumulator's declaration and of the outermost loop's
+// first and closing lines, with the accumulator's name and update operator.
+struct WavePlan {
+    bool ok = false;
+    size_t decl = 0, loop = 0, close = 0;
+    std::string acc;
+    bool is_max = false;
+};
+
+WavePlan plan_wave(const std::vector<std::string> &lines, size_t body_start) {
+    WavePlan w;
+    int depth = 0;
+    bool in_loop = false, after = false, updated = false;
+    for (size_t i = body_start; i < lines.size(); i++) {
+        std::string l = trim(lines[i]);
+        if (l.empty() || starts(l, "//")) continue;
+        if (l == "}") {
+            if (depth == 0) return (w.ok = after && updated, w);
+            depth--;
+            if (in_loop && depth == 0) { w.close = i; in_loop = false; after = true; }
+            continue;
+        }
+        if (l.find("workgroupBarrier") != std::string::npos || l.find("lid.") != std::string::npos ||
+            (l.find("wid.") != std::string::npos && !starts(l, "let flat_wid_")))
+            return w;
+        if (starts(l, "var ")) {
+            if (!w.acc.empty() || in_loop || after) return w;
+            const size_t c = l.find(':'), e = l.find('=');
+            if (c == std::string::npos || e == std::string::npos || trim(l.substr(c + 1, e - c - 1)) != "f32") return w;
+            w.acc = trim(l.substr(4, c - 4));
+            w.decl = i;
+            continue;
+        }
+        if (starts(l, "for (")) {
+            if (w.acc.empty() || after) return w;
+            if (!in_loop) { in_loop = true; w.loop = i; }
+            depth++;
+            continue;
+        }
+        if (starts(l, "if (")) {
+            // only the early-return guards before the accumulator
+            if (!w.acc.empty() || l.size() < 12 || l.compare(l.size() - 11, 11, "{ return; }") != 0) return w;
+            continue;
+        }
+        if (starts(l, "let ")) continue;
+        if (!w.acc.empty() && starts(l, (w.acc + " = ").c_str())) {
+            if (!in_loop || updated) return w;
+            const std::string r = trim(l.substr(w.acc.size() + 3));
+            if (starts(r, (w.acc + " + ").c_str())) w.is_max = false;
+            else if (starts(r, ("max(" + w.acc + ", ").c_str())) w.is_max = true;
+            else return w;
+            updated = true;
+            continue;
+        }
+        if (after && starts(l, "data")) continue;   // stores after the loop
+        return w;
+    }
+    return w;
+}
+
+// Returns HIP source with an extern "C" entry point `kernel`, or "" with *err set. *wave (optional) is set
+// when the kernel was rendered in the wave-per-output form (launched with 64 lanes per original thread).
+std::string wgsl_to_hip(const std::string &src, std::string *err, bool *wave) {
     std::vector<std::string> lines;
     {
         size_t a = 0;
@@ -370,11 +446,30 @@ std::string wgsl_to_hip(const std::string &src, std::string *err) {
         return "";
     }
     // body
+    WavePlan wp;
+    if (wave) {
+        wp = plan_wave(lines, i);
+        *wave = wp.ok && shared.empty();
+        wp.ok = *wave;
+    }
     for (; i < lines.size(); i++) {
         std::string l = trim(lines[i]);
         if (l.empty() || starts(l, "//")) continue;
         std::string out;
-        if (l == "}") {
+        if (wp.ok && i == wp.loop) {
+            // for (var rN: i32 = 0; COND; rN++) {  ->  the lane's strided share of the iterations
+            char v[32];
+            if (sscanf(l.c_str(), "for (var %31[^:]: i32 = 0;", v) != 1) { *err = "unsupported reduce loop: " + l; return ""; }
+            const size_t s1 = l.find(';'), s2 = l.find(';', s1 + 1);
+            std::string c;
+            if (!expr(trim(l.substr(s1 + 1, s2 - s1 - 1)), c, err)) return "";
+            out = std::string("for (int ") + v + " = (int)wg_lane; " + c + "; " + v + " += 64) {";
+            depth++;
+        } else if (wp.ok && i == wp.close) {
+            depth--;
+            out = "}\n" + std::string(2 * (depth + 1), ' ') + wp.acc + " = " + (wp.is_max ? "wg_wave_max(" : "wg_wave_sum(") +
+                  wp.acc + ");\n" + std::string(2 * (depth + 1), ' ') + "if (wg_lane != 0u) return;";
+        } else if (l == "}") {
             if (depth == 0) { depth = -1; break; }   // end of main
             out = "}";
             depth--;
@@ -431,7 +526,8 @@ std::string wgsl_to_hip(const std::string &src, std::string *err) {
     if (depth != -1) { *err = "unterminated fn main"; return ""; }
     // assemble
     std::string s = kPrelude;
-    s += "\nextern \"C\" __global__ void __launch_bounds__(" + std::to_string(ws[0] * ws[1] * ws[2]) + ") kernel(";
+    const long nthreads = wp.ok ? 64 : ws[0] * ws[1] * ws[2];
+    s += "\nextern \"C\" __global__ void __launch_bounds__(" + std::to_string(nthreads) + ") kernel(";
     for (size_t k = 0; k < params.size(); k++) {
         if (params[k].binding != (int)k) { *err = "bindings must be 0..n-1 in order"; return ""; }
         s += (k ? ", " : "") + params[k].decl;
@@ -439,10 +535,18 @@ std::string wgsl_to_hip(const std::string &src, std::string *err) {
     if (symbolic) s += std::string(params.empty() ? "" : ", ") + "int wg_n0, int wg_n1, int wg_n2, int wg_n3";
     s += ") {\n";
     for (auto &sh : shared) s += "  " + sh + "\n";
-    s += "  const wg_uvec3 lid = {threadIdx.x, threadIdx.y, threadIdx.z};\n";
-    s += "  const wg_uvec3 wid = {blockIdx.x, blockIdx.y, blockIdx.z};\n";
-    s += "  const wg_uvec3 gid = {blockIdx.x * blockDim.x + threadIdx.x, blockIdx.y * blockDim.y + threadIdx.y,"
-         " blockIdx.z * blockDim.z + threadIdx.z};\n";
+    if (wp.ok) {
+        // one wave per original thread: the grid's blocks are the original threads (ah_launch scales it)
+        s += "  // wave-per-output rendering: lane wg_lane of the wave that stands for one original thread\n";
+        s += "  const unsigned wg_lane = threadIdx.x;\n";
+        s += "  const wg_uvec3 gid = {blockIdx.x, blockIdx.y, blockIdx.z};\n";
+        s += "  const wg_uvec3 wid = {0u, 0u, 0u};\n";
+    } else {
+        s += "  const wg_uvec3 lid = {threadIdx.x, threadIdx.y, threadIdx.z};\n";
+        s += "  const wg_uvec3 wid = {blockIdx.x, blockIdx.y, blockIdx.z};\n";
+        s += "  const wg_uvec3 gid = {blockIdx.x * blockDim.x + threadIdx.x, blockIdx.y * blockDim.y + threadIdx.y,"
+             " blockIdx.z * blockDim.z + threadIdx.z};\n";
+    }
     if (symbolic)
         s += "  const struct { unsigned n0, n1, n2, n3; } params_n = {(unsigned)wg_n0, (unsigned)wg_n1, (unsigned)wg_n2,"
              " (unsigned)wg_n3};\n";
@@ -456,7 +560,7 @@ std::string wgsl_to_hip(const std::string &src, std::string *err) {
 extern "C" int ah_translate_wgsl(const char *wgsl, char *out, int64_t cap, int64_t *needed) {
     if (!wgsl) return ah::set_error(AH_ERR_INVALID, "ah_translate_wgsl: null source");
     std::string err;
-    std::string hip = ah::wgsl_to_hip(wgsl, &err);
+    std::string hip = ah::wgsl_to_hip(wgsl, &err, nullptr);
     if (hip.empty()) return ah::set_error(AH_ERR_COMPILE, "wgsl: %s", err.c_str());
     if (needed) *needed = (int64_t)hip.size() + 1;
     if (out && cap > 0) {

@@ -79,15 +79,25 @@ int ah_module_get(ah_device *dev, const char *source, const char *entry, ah_kern
  * on its own (no device needed): writes at most cap bytes of NUL-terminated HIP source to out and the
  * full size to *needed; AH_ERR_COMPILE if the WGSL is outside the subset the reference emits. */
 int ah_translate_wgsl(const char *wgsl, char *out, int64_t cap, int64_t *needed);
-/* Template selection for a rendered WGSL kernel (host only, no device): when the kernel is a contraction
- * REDUCE(ADD, MUL(load, load)) of f32 buffers, stored as-is or plus a column bias (data3[n]: the Linear
- * forward), whose load and store indices are affine
- * with zero offset (the scheduler's unsimplified index chains evaluated, codegen/lower.go:98-550 as
- * rendered by codegen/wgsl.go:36-238), writes the "tmpl:gemm;..." key ah_module_get runs in its place
- * (the MFMA contraction template) to buf; otherwise writes "". No counterpart in the reference, whose
- * backend renders every kernel: it exposes the selection ah_module_get and ah_run make (set
- * AH_WGSL_TEMPLATES=0 to turn it off). */
+/* Template selection for a rendered WGSL kernel (host only, no device). The kernel's body, in the form
+ * codegen/lower.go:98-719 lowers and codegen/wgsl.go:41-386 renders it (one let per ALU node and load,
+ * GIDVar axes, one accumulator and loop per reduce, f16 reduces widened and narrowed with f16(acc),
+ * params_n for a symbolic batch), is parsed with every let substituted, and two families select a
+ * hand-written kernel: a contraction REDUCE(ADD, MUL(a, b)) whose operands are loads, ReLU prologues
+ * max(x, 0.0) or ReLU-backward mask prologues select(0.0, adj, z == max(z, 0.0)), stored as acc,
+ * f16(acc), c*acc, acc + bias[n] or max(acc + bias[n], 0.0) -> "tmpl:gemm;..." (dtype f32 or f16, M/N/K
+ * "sym" where symbolic); and a reduction REDUCE(ADD|MAX, load) along a row or down a column (or over a
+ * whole 1-D buffer) stored into f32 -> "tmpl:reduce;...". Index expressions must evaluate as affine with
+ * zero offset over the axes. Writes the key ah_module_get runs in the kernel's place to buf, or "". No
+ * counterpart in the reference, whose backend renders every kernel: it exposes the selection
+ * ah_module_get and ah_run make (AH_WGSL_TEMPLATES=0 turns it off). */
 int ah_wgsl_template_key(const char *wgsl, char *buf, int32_t cap);
+/* How ah_module_get runs a rendered WGSL kernel (host only): writes the template key when one is selected
+ * (as above), "wave" when the kernel is rendered in the wave-per-output form (a single-reduce kernel:
+ * one 64-lane wave per output element, the lanes striding the outermost reduce loop and combining their
+ * partials with a shuffle tree, AH_WGSL_WAVE=0 turns it off), or "thread" for the one-thread-per-output
+ * rendering of ah_translate_wgsl. AH_ERR_COMPILE if the WGSL is outside the subset. */
+int ah_wgsl_plan(const char *wgsl, char *buf, int32_t cap);
 int ah_launch(ah_device *dev, ah_kernel *k, const uint32_t grid[3], const uint32_t block[3],
               void *const *ptrs, int32_t n_ptrs, const int32_t *scalars, int32_t n_scalars);
 

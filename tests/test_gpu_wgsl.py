@@ -77,3 +77,77 @@ def test_selected_bias_contraction_matches_rendering(dev, monkeypatch, form):
     with Device(0) as d2:
         ref = Executor(d2).run([item], inp)[30].reshape(M, N)
     assert np.abs(got - ref).max() / scale < 1e-5
+
+
+# ── the configs-1/4 training step as rendered kernels (tests/wgsl_lower.py) ────────────────────────
+
+import oracle_lib as O  # noqa: E402
+import wgsl_lower as WL  # noqa: E402
+from anneal_amd import data  # noqa: E402
+
+
+def run_rendered_step(dev, B, D, H, C, symbolic, inputs):
+    ks, lv, outs = WL.mlp_ce_step(B, D, H, C, symbolic=symbolic)
+    items = [ExecItem(src, [Buffer(u, n, sh, dtype=dt) for (u, n, dt, sh) in bufs], sym_vars=["N"] if symbolic else [],
+                      local_size=ws, workgroup_count=wc) for _, src, bufs, ws, wc, _ in ks]
+    feed = {lv[k]: (inputs[k].view(np.float32) if k == "labels" else inputs[k].ravel()) for k in lv}
+    ex = Executor(dev)
+    got = ex.run_symbolic(items, feed, {"N": B}) if symbolic else ex.run(items, feed)
+    return {k: got[u] for k, u in outs.items()}
+
+
+@pytest.mark.parametrize("B,D,H,C,symbolic", [(64, 784, 128, 10, False), (7, 512, 2048, 512, True),
+                                              (256, 512, 2048, 512, True)])
+def test_rendered_mlp_ce_step_matches_oracle(dev, B, D, H, C, symbolic):
+    """The configs-1/4 step as the reference's rendered kernels (14 WGSL kernels, restated from its
+    scheduler's rules and lowering), run through ah_run / ah_run_symbolic: five contractions and two
+    reductions on the hand-written templates, six prologue reductions on the wave rendering, dZ on the
+    thread rendering. Loss and gradients match ora_mlp_ce_step at the f32 reduction bar (1e-4)."""
+    p = data.mlp_ce_inputs(B, D, H, C, **({} if B == 64 else {"x_lo": -1.0, "x_hi": 1.0}))
+    got = run_rendered_step(dev, B, D, H, C, symbolic, p)
+    wl, g, _ = O.mlp_ce_step(p, 0.0)
+    assert abs(got["loss"][0] - wl) <= 1e-4 * max(1.0, abs(wl))
+    for k in ("dW1", "db1", "dW2", "db2"):
+        assert O.relerr(got[k], g[k].ravel()) < 1e-4, k
+
+
+def test_rendered_step_templates_match_the_plain_rendering(dev, monkeypatch):
+    """The same rendered step with every kernel rendered one thread per output (templates and the wave
+    form off) gives the same results to summation order."""
+    from anneal_amd.backend import Device
+    B, D, H, C = 64, 784, 128, 10
+    p = data.mlp_ce_inputs(B, D, H, C)
+    fast = run_rendered_step(dev, B, D, H, C, False, p)
+    monkeypatch.setenv("AH_WGSL_TEMPLATES", "0")
+    monkeypatch.setenv("AH_WGSL_WAVE", "0")
+    with Device(0) as d2:
+        plain = run_rendered_step(d2, B, D, H, C, False, p)
+    for k in fast:
+        assert O.relerr(fast[k], plain[k]) < 1e-5, k
+
+
+@pytest.mark.parametrize("relu", [False, True])
+def test_selected_f16_contraction_matches_rendering(dev, monkeypatch, relu):
+    """An f16 Linear forward (widened loads, f16(acc) narrowing, f16 bias add) on the f16 MFMA template
+    matches float64 within f16 rounding, and the WGSL rendering to the rounding of f16(acc) and the add."""
+    from anneal_amd.backend import Device
+    M, N, K = 256, 128, 192
+    src, bufs, ws, wc, key = WL.f16_linear(M, N, K, bias=True, relu_a=relu)
+    rng = np.random.default_rng(11)
+    A = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
+    W = (rng.standard_normal((N, K)) * 0.1).astype(np.float16).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float16).astype(np.float32)
+    item = ExecItem(src, [Buffer(u, n, sh, dtype=dt) for (u, n, dt, sh) in bufs], local_size=ws, workgroup_count=wc)
+    inp = {1: A.ravel(), 2: W.ravel(), 3: b}
+    got = Executor(dev).run([item], inp)[30].reshape(M, N)
+    Ar = np.maximum(A, 0) if relu else A
+    want = (Ar.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float16).astype(np.float64) + b
+    assert np.max(np.abs(got - want)) <= 2e-3 * np.max(np.abs(want))
+    monkeypatch.setenv("AH_WGSL_TEMPLATES", "0")
+    with Device(0) as d2:
+        ref = Executor(d2).run([item], inp)[30].reshape(M, N)
+    # f16(acc) may differ by one ulp of the accumulator (summation order), and the f16 bias add rounds once
+    # more: one ulp at |acc| plus one at the result
+    acc = np.abs(ref - b).astype(np.float16)
+    ulp = np.abs(np.spacing(acc)).astype(np.float32) + np.abs(np.spacing(ref.astype(np.float16))).astype(np.float32)
+    assert np.all(np.abs(got - ref) <= ulp + 1e-7)

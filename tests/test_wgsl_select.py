@@ -47,7 +47,7 @@ def test_swapped_bindings_select_swap_ab():
 @pytest.mark.parametrize("mutate", [
     lambda s: s.replace("var acc0: f32 = 0.0;", "var acc0 = 0.0;"),            # no type: not the emitted form
     lambda s: s.replace("acc0 = acc0 + (t9 * t12);", "acc0 = acc0 + (t9 + t12);"),
-    lambda s: s.replace("data0[((r0 * 2) + r1)] = acc0;", "data0[((r0 * 2) + r1)] = (acc0 * 2.0);"),
+    lambda s: s.replace("data0[((r0 * 2) + r1)] = acc0;", "data0[((r0 * 2) + r1)] = (acc0 - 2.0);"),
     lambda s: s.replace("let t9: f32 = data1[", "let t9: f32 = data1[((("),   # unbalanced parentheses
     lambda s: s[: len(s) // 2],                                                  # truncated
     lambda s: "",
@@ -70,3 +70,60 @@ def test_bias_epilogue_is_selected(form):
 def test_bias_over_rows_is_not_a_column_bias():
     src, _, _ = W.matmul_wgsl(64, 48, 32, bias="rows")
     assert L.wgsl_template_key(src) == ""
+
+
+def test_scaled_store_is_selected_with_its_scale():
+    # acc * c (a constant scale, e.g. a mean's 1/B) is the store epilogue's scale, spelled exactly
+    src = W.kernels()["matmul_known_answer"][0].replace("data0[((r0 * 2) + r1)] = acc0;",
+                                                       "data0[((r0 * 2) + r1)] = (acc0 * 2.0);")
+    assert L.wgsl_template_key(src) == "tmpl:gemm;dtype=f32;epi=store;ta=0;tb=1;M=2;N=2;K=3;scale=0x1p+1"
+
+
+# ── the configs-1/4 step as rendered kernels (tests/wgsl_lower.py) ──────────────────────────────────
+
+import wgsl_lower as WL  # noqa: E402
+
+
+@pytest.mark.parametrize("symbolic", [False, True])
+@pytest.mark.parametrize("shape", [(64, 784, 128, 10), (256, 512, 2048, 512)])
+def test_rendered_mlp_ce_step_selects_a_template_or_the_wave_rendering(shape, symbolic):
+    """Every kernel of the rendered step is run by a hand-written template (the contractions with their
+    ReLU and mask prologues and bias epilogues, the plain row max and column sum) or, for the reductions
+    with elementwise prologues, by the wave-per-output rendering; only the elementwise dZ kernel keeps the
+    one-thread-per-output rendering."""
+    B, D, H, C = shape
+    ks, _, _ = WL.mlp_ce_step(B, D, H, C, symbolic=symbolic)
+    plans = {name: L.wgsl_plan(src) for name, src, *_ in ks}
+    for name, src, bufs, ws, wc, want in ks:
+        assert plans[name] == want, (name, plans[name], want)
+    assert sum(p.startswith("tmpl:gemm") for p in plans.values()) == 5
+    assert sum(p.startswith("tmpl:reduce") for p in plans.values()) == 2
+    assert [n for n, p in plans.items() if p == "thread"] == ["dZ"]
+
+
+@pytest.mark.parametrize("bias,relu", [(True, False), (False, False), (True, True)])
+def test_f16_contraction_with_narrowing_is_selected(bias, relu):
+    """An f16 reduce (loads widened to f32 in the loop, f16(acc) after it) selects the f16 MFMA template."""
+    src, _, _, _, key = WL.f16_linear(256, 128, 192, bias=bias, relu_a=relu)
+    assert L.wgsl_template_key(src) == key
+
+
+def test_mask_prologue_needs_the_same_index_for_z_and_the_adjoint():
+    """Where(z == max(z, 0), adj, 0) is the ReLU backward only when z is read where adj is."""
+    ks, _, _ = WL.mlp_ce_step(64, 784, 128, 10)
+    src = dict((n, s) for n, s, *_ in ks)["dW1"]
+    assert "pa=mask" in L.wgsl_template_key(src)
+    bad = src.replace("let t5: f32 = data2[(r2 * 128) + r0];", "let t5: f32 = data2[(r2 * 128) + ((r0 + 1) % 128)];")
+    assert bad != src
+    assert L.wgsl_template_key(bad) == ""
+
+
+def test_reduce_with_scale_and_scalar_output():
+    """Sum over a whole 1-D buffer times a constant (a mean) is tmpl:reduce with M=1 and the scale."""
+    k = WL.Kernel([(20, [1], L.AH_F32), (1, [300], L.AH_F32)], [])
+    k.acc()
+    r = k.loop(300)
+    k.update(k.load(1, r))
+    k.end()
+    k.store(k.let("(acc0 * 0.5)"))
+    assert L.wgsl_template_key(k.source()) == "tmpl:reduce;op=sum;axis=1;M=1;N=300;scale=0x1p-1"

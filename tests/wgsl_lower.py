@@ -1,0 +1,396 @@
+"""The configs-1/4 training step as the WGSL kernels anneal's codegen renders, for the template-selection
+tests (tests/test_wgsl_select.py, host) and the rendered-step parity test (tests/test_gpu_wgsl.py, GPU).
+
+TEST INFRASTRUCTURE ONLY. Without a Go toolchain the reference's scheduler cannot be run, so the kernel
+partition is restated from its rules and the text from its lowering, not captured:
+  - partition (schedule/kernels.go, SPEC.md sections 7.5-7.6): every REDUCE materialises its output; an
+    elementwise consumer that is a reduce's sole consumer is fused after it (Pass 5, epilogue fusion: the
+    Linear bias add); other elementwise chains are inlined into the kernels that read them (ReLU's
+    Maximum(z, 0) into the contractions that read the activation, the ReLU backward's
+    Where(z == relu(z), adj, 0) into the reductions over the batch, tensor/gradient_ruleset.go:153-161);
+    the softmax-CE adjoint dZ, read by three reductions, is materialised by its own elementwise kernel;
+  - text (codegen/lower.go:98-719, codegen/wgsl.go:41-386): GIDVar lets per output range (dims assigned
+    from the innermost range, `i32(flat_gid_C % R)` with an axis guard, symbolic ranges all on x as
+    `i32(flat_gid_x / S)` with a params_n bounds check), one `let tN: T = ...;` per load and ALU node,
+    one accumulator per reduce (`var acc0: f32 = <identity>;`, `acc0 = acc0 + tN;` or
+    `acc0 = max(acc0, tN);`), loops `for (var rN: i32 = 0; rN < K; rN++)` (`i32(params_n.n0)` when
+    symbolic), f32 constants in FormatFloat(v, 'f', -1, 32) form, and one store
+    `data0[(u32(r0) * S) + u32(r1)] = v;`.
+The softmax cross-entropy and its backward follow the graph the oracle restates (ora_softmax_ce,
+oracle/anneal_oracle.c): m = Max(z), zs = z - m, e = Exp2(zs * 1/ln2), s = Sum(e), logp = zs -
+Log2(s) * ln2, loss = Sum(logp * onehot) * (-1/B), and the rule-by-rule backward with the row max's
+tie split.
+"""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+
+from wgsl_kernels import F16, F32, I32, header, main_open
+
+LOG2E = "1.442695"   # FormatFloat(1/ln2, 'f', -1, 32)
+LN2 = "0.6931472"    # FormatFloat(ln2, 'f', -1, 32)
+R0 = "r0"
+
+
+def f32_lit(v: float) -> str:
+    """A constant as constLiteral writes it: the shortest decimal that reads back as the same f32."""
+    f = struct.unpack("f", struct.pack("f", v))[0]
+    for digits in range(1, 12):
+        s = f"{f:.{digits}g}"
+        if struct.unpack("f", struct.pack("f", float(s)))[0] == f:
+            break
+    if "e" in s:
+        s = f"{float(s):.{12}f}".rstrip("0")
+    if "." not in s:
+        s += ".0"
+    return s
+
+
+class Kernel:
+    """Builds one kernel's text in the lowering's emit order."""
+
+    def __init__(self, bufs, out_axes, sym=False, f16=False):
+        """bufs: [(uop, shape, dtype)] in PARAM order (data0 the output); out_axes: the output ranges,
+        outermost first, as sizes (the string "N" for the symbolic batch, None for a kept size-1 dim)."""
+        self.bufs, self.sym, self.f16 = bufs, sym, f16
+        self.lines = []
+        self.depth = 1
+        self.t = 5
+        self.next_r = 0
+        self.out = []                 # (range name or None, size)
+        for size in out_axes:
+            if size is None:
+                self.out.append((None, 1))
+            else:
+                self.out.append((f"r{self.next_r}", size))
+                self.next_r += 1
+        self._gid()
+
+    def emit(self, s):
+        self.lines.append("  " * self.depth + s)
+
+    def _gid(self):
+        """GIDVar lets, guards and the symbolic bounds check (codegen/lower.go:194-466)."""
+        dims = [[], [], []]
+        has_sym = any(s == "N" for _, s in self.out)
+        k = 0
+        for name, size in reversed(self.out):
+            dims[0 if has_sym else k % 3].append((name, size))
+            k += 1
+        self.ws = [1, 1, 1]
+        self.wc = [1, 1, 1]
+        self.dim1_used = False
+        for d in range(3):
+            stride = 1
+            for name, size in dims[d]:
+                if name is None:
+                    continue
+                base = "flat_gid_" + "xyz"[d]
+                if size == "N":
+                    e = f"i32({base})" if stride == 1 else f"i32({base} / {stride}u)"
+                    self.emit(f"let {name}: i32 = {e};")
+                else:
+                    e = f"i32({base} % {size}u)" if stride == 1 else f"i32(({base} / {stride}u) % {size}u)"
+                    self.emit(f"let {name}: i32 = {e};")
+                    if size > 1:
+                        self.emit(f"if ({name} >= {size}) {{ return; }}")
+                    stride *= size
+                if d > 0:
+                    self.dim1_used = True
+            if d == 0 and any(n is not None for n, _ in dims[0]):
+                self.ws[0] = 64
+            total = 1
+            for n, s in dims[d]:
+                if n is not None:
+                    total *= 64 if s == "N" else s
+            self.wc[d] = max(1, (total + self.ws[d] - 1) // self.ws[d])
+        if has_sym:
+            trailing = 1
+            seen = False
+            for _, s in self.out:
+                if s == "N":
+                    seen = True
+                elif seen:
+                    trailing *= s
+            self.emit("if (gid_x >= params_n.n0 * %du) { return; }" % trailing if trailing > 1 else
+                      "if (gid_x >= params_n.n0) { return; }")
+
+    def let(self, expr, ty="f32"):
+        name = f"t{self.t}"
+        self.t += 1 + (self.t % 3 == 0)   # arena indices are not consecutive
+        self.emit(f"let {name}: {ty} = {expr};")
+        return name
+
+    def load(self, buf, idx, ty="f32", widen=False):
+        e = f"data{buf}[{idx}]"
+        if widen:
+            return self.let(f"f32({e})", "f32")
+        return self.let(e, ty)
+
+    def idx2(self, a, stride, b):
+        """An index as the lowering chains it: (a * stride) then (+ b), each its own i32 let."""
+        t = self.let(f"({a} * {stride})", "i32")
+        return self.let(f"({t} + {b})", "i32")
+
+    def acc(self, op="+"):
+        self.emit("var acc0: f32 = %s;" % ("0.0" if op == "+" else "bitcast<f32>(0xff7fffffu)"))
+        self.accop = op
+
+    def loop(self, size):
+        name = f"r{self.next_r}"
+        self.next_r += 1
+        bound = "i32(params_n.n0)" if size == "N" else str(size)
+        self.emit(f"for (var {name}: i32 = 0; {name} < {bound}; {name}++) {{")
+        self.depth += 1
+        return name
+
+    def update(self, v):
+        self.emit(f"acc0 = acc0 + {v};" if self.accop == "+" else f"acc0 = max(acc0, {v});")
+
+    def end(self):
+        self.depth -= 1
+        self.emit("}")
+
+    def store(self, v):
+        terms, stride = [], 1
+        for name, size in reversed(self.out):
+            if name is None:
+                continue
+            terms.append(f"u32({name})" if stride == 1 else f"(u32({name}) * {stride}u)")
+            stride *= 1 if size == "N" else size
+        idx = " + ".join(reversed(terms)) if terms else "0u"
+        self.emit(f"data0[{idx}] = {v};")
+
+    def source(self):
+        types = {F32: "f32", F16: "f16", I32: "i32"}
+        src = header([types[d] for _, _, d in self.bufs], self.ws, self.wc, sym_params=True if self.sym else None,
+                     f16=self.f16)
+        src += main_open(self.ws, self.wc, dim1_used=self.dim1_used)
+        return "\n".join(src + self.lines + ["}"])
+
+
+def mlp_ce_step(B: int, D: int, H: int, C: int, symbolic: bool = False):
+    """Linear(D->H) ReLU Linear(H->C), softmax-CE mean loss and its backward, as rendered kernels.
+    Returns [(name, wgsl, bufs, ws, wc, plan)] where plan is what ah_wgsl_plan should select ("tmpl:..." with
+    the batch written as {B}, "wave" or "thread"), plus the leaf and output uop maps. With symbolic=True
+    the batch is bound at run time (NewSymbolicBatchInput) and B only sets the -1/B constant."""
+    N = "N" if symbolic else B
+    Bk = "sym" if symbolic else str(B)
+    a = f32_lit(-1.0 / B)
+    leaves = dict(x=1, labels=2, W1=3, b1=4, W2=5, b2=6)
+    uZ1, uZ, um, utie, us, uloss, ugls, ugm, udZ, udb2, udW2, udH1, udb1, udW1 = range(10, 24)
+
+    def bshape(*rest):
+        return [N if symbolic else B] + list(rest)
+
+    ks = []
+
+    def add(name, k, plan):
+        bufs = []
+        for uop, shape, dt in k.bufs:
+            if symbolic and shape and shape[0] == "N":
+                bufs.append((uop, 0, dt, [0] + list(shape[1:])))
+            else:
+                bufs.append((uop, int(np.prod(shape)), dt, list(shape)))
+        ks.append((name, k.source(), bufs, tuple(k.ws), tuple(k.wc), plan))
+
+    # 1. Z1 = x W1^T + b1 (the bias add fused after the reduce)
+    k = Kernel([(uZ1, bshape(H), F32), (1, bshape(D), F32), (3, [H, D], F32), (4, [H], F32)], [N, H], symbolic)
+    k.acc()
+    r2 = k.loop(D)
+    tx = k.load(1, k.idx2("r0", D, r2))
+    tw = k.load(2, f"(r1 * {D}) + {r2}")
+    k.update(k.let(f"({tx} * {tw})"))
+    k.end()
+    k.store(k.let(f"(acc0 + {k.load(3, 'r1')})"))
+    add("fc1", k, f"tmpl:gemm;dtype=f32;epi=bias;ta=0;tb=0;M={Bk};N={H};K={D}")
+
+    # 2. Z = relu(Z1) W2^T + b2: the ReLU inlined into the loop (W2 bound first)
+    k = Kernel([(uZ, bshape(C), F32), (5, [C, H], F32), (uZ1, bshape(H), F32), (6, [C], F32)], [N, C], symbolic)
+    k.acc()
+    r2 = k.loop(H)
+    tz = k.load(2, f"(r0 * {H}) + {r2}")
+    tr = k.let(f"max({tz}, 0.0)")
+    tw = k.load(1, k.idx2("r1", H, r2))
+    k.update(k.let(f"({tr} * {tw})"))
+    k.end()
+    k.store(k.let(f"({k.load(3, 'r1')} + acc0)"))
+    add("fc2", k, f"tmpl:gemm;dtype=f32;epi=bias;ta=0;tb=0;M={Bk};N={C};K={H};pa=relu;swap_ab=1")
+
+    # 3. m = Max(z, [1], keepdim)
+    k = Kernel([(um, bshape(1), F32), (uZ, bshape(C), F32)], [N, None], symbolic)
+    k.acc("max")
+    r1 = k.loop(C)
+    k.update(k.load(1, f"(r0 * {C}) + {r1}"))
+    k.end()
+    k.store("acc0")
+    add("rowmax", k, f"tmpl:reduce;op=max;axis=1;M={Bk};N={C}")
+
+    def zs(k, zbuf, mbuf, r1):
+        tz = k.load(zbuf, f"(r0 * {C}) + {r1}")
+        tm = k.load(mbuf, "r0")
+        return tz, tm, k.let(f"({tz} - {tm})")
+
+    def onehot(k, lbuf, r1):
+        tl = k.load(lbuf, "r0", "i32")
+        return k.let(f"select(0.0, 1.0, {k.let(f'({tl} == {r1})', 'bool')})")
+
+    def gzs(k, zbuf, mbuf, sbuf, gbuf, lbuf, r1):
+        tz, tm, d = zs(k, zbuf, mbuf, r1)
+        e = k.let(f"exp2({k.let(f'({d} * {LOG2E})')})")
+        g1 = k.let(f"({k.load(gbuf, 'r0')} * {LN2})")
+        rs = k.let(f"(1.0 / {k.let(f'({k.load(sbuf, R0)} * {LN2})')})")
+        gs = k.let(f"({g1} * {rs})")
+        gv = k.let(f"({k.let(f'({gs} * {e})')} * {LN2})")
+        g2 = k.let(f"({gv} * {LOG2E})")
+        gl = k.let(f"({a} * {onehot(k, lbuf, r1)})")
+        return tz, tm, k.let(f"({gl} + {g2})")
+
+    # 4. tie count: Sum(Cast(z == m)) (the max rule's tie split, tensor/gradient_ruleset.go:307-320)
+    k = Kernel([(utie, bshape(1), F32), (um, bshape(1), F32), (uZ, bshape(C), F32)], [N, None], symbolic)
+    k.acc()
+    r1 = k.loop(C)
+    tz = k.load(2, f"(r0 * {C}) + {r1}")
+    eq = k.let(f"({tz} == {k.load(1, 'r0')})", "bool")
+    k.update(k.let(f"select(0.0, 1.0, {eq})"))
+    k.end()
+    k.store("acc0")
+    add("tie", k, "wave")
+
+    # 5. s = Sum(Exp2((z - m) * 1/ln2))
+    k = Kernel([(us, bshape(1), F32), (uZ, bshape(C), F32), (um, bshape(1), F32)], [N, None], symbolic)
+    k.acc()
+    r1 = k.loop(C)
+    _, _, d = zs(k, 1, 2, r1)
+    k.update(k.let(f"exp2({k.let(f'({d} * {LOG2E})')})"))
+    k.end()
+    k.store("acc0")
+    add("sumexp", k, "wave")
+
+    # 6. loss = Sum((zs - Log2(s) * ln2) * onehot) * (-1/B), over both axes
+    k = Kernel([(uloss, [1], F32), (2, bshape(), I32), (uZ, bshape(C), F32), (um, bshape(1), F32),
+                (us, bshape(1), F32)], [], symbolic)
+    k.acc()
+    k.loop(N)
+    r1 = k.loop(C)
+    _, _, d = zs(k, 2, 3, r1)
+    ls = k.let(f"({k.let(f'log2({k.load(4, R0)})')} * {LN2})")
+    lp = k.let(f"({d} - {ls})")
+    k.update(k.let(f"({lp} * {onehot(k, 1, r1)})"))
+    k.end()
+    k.end()
+    k.store(k.let(f"(acc0 * {a})"))
+    add("loss", k, "wave")
+
+    # 7. gls = Sum(-(a * onehot)) (Sub's src1 -> Neg, expanded and summed back)
+    k = Kernel([(ugls, bshape(1), F32), (2, bshape(), I32)], [N, None], symbolic)
+    k.acc()
+    r1 = k.loop(C)
+    k.update(k.let(f"(-{k.let(f'({a} * {onehot(k, 1, r1)})')})"))
+    k.end()
+    k.store("acc0")
+    add("gls", k, "wave")
+
+    # 8. gm = Sum(-gzs): the adjoint of the row max
+    k = Kernel([(ugm, bshape(1), F32), (uZ, bshape(C), F32), (um, bshape(1), F32), (us, bshape(1), F32),
+                (ugls, bshape(1), F32), (2, bshape(), I32)], [N, None], symbolic)
+    k.acc()
+    r1 = k.loop(C)
+    _, _, g = gzs(k, 1, 2, 3, 4, 5, r1)
+    k.update(k.let(f"(-{g})"))
+    k.end()
+    k.store("acc0")
+    add("gmax", k, "wave")
+
+    # 9. dZ = gzs + Where(z == m, gm / tie, 0): elementwise, materialised for its three readers
+    k = Kernel([(udZ, bshape(C), F32), (uZ, bshape(C), F32), (um, bshape(1), F32), (us, bshape(1), F32),
+                (ugls, bshape(1), F32), (2, bshape(), I32), (ugm, bshape(1), F32), (utie, bshape(1), F32)], [N, C], symbolic)
+    tz, tm, g = gzs(k, 1, 2, 3, 4, 5, "r1")
+    share = k.let(f"({k.load(6, 'r0')} * {k.let(f'(1.0 / {k.load(7, R0)})')})")
+    sel = k.let(f"select(0.0, {share}, {k.let(f'({tz} == {tm})', 'bool')})")
+    k.store(k.let(f"({g} + {sel})"))
+    add("dZ", k, "thread")
+
+    # 10. db2 = Sum(dZ, [0])
+    k = Kernel([(udb2, [C], F32), (udZ, bshape(C), F32)], [C], symbolic)
+    k.acc()
+    r1 = k.loop(N)
+    k.update(k.load(1, k.idx2(r1, C, "r0")))
+    k.end()
+    k.store("acc0")
+    add("db2", k, f"tmpl:reduce;op=sum;axis=0;M={Bk};N={C}")
+
+    # 11. dW2 = dZ^T relu(Z1): the ReLU inlined into the batch loop (Z1 bound first)
+    k = Kernel([(udW2, [C, H], F32), (uZ1, bshape(H), F32), (udZ, bshape(C), F32)], [C, H], symbolic)
+    k.acc()
+    r2 = k.loop(N)
+    tdz = k.load(2, k.idx2(r2, C, "r0"))
+    tz = k.load(1, f"({r2} * {H}) + r1")
+    k.update(k.let(f"({tdz} * {k.let(f'max({tz}, 0.0)')})"))
+    k.end()
+    k.store("acc0")
+    add("dW2", k, f"tmpl:gemm;dtype=f32;epi=store;ta=1;tb=1;M={C};N={H};K={Bk};pb=relu;swap_ab=1")
+
+    # 12. dH1 = dZ W2
+    k = Kernel([(udH1, bshape(H), F32), (udZ, bshape(C), F32), (5, [C, H], F32)], [N, H], symbolic)
+    k.acc()
+    r2 = k.loop(C)
+    tdz = k.load(1, f"(r0 * {C}) + {r2}")
+    tw = k.load(2, k.idx2(r2, H, "r1"))
+    k.update(k.let(f"({tdz} * {tw})"))
+    k.end()
+    k.store("acc0")
+    add("dH1", k, f"tmpl:gemm;dtype=f32;epi=store;ta=0;tb=1;M={Bk};N={H};K={C}")
+
+    def masked(k, zbuf, abuf, r):
+        tz = k.load(zbuf, f"({r} * {H}) + r0")
+        eq = k.let(f"({tz} == {k.let(f'max({tz}, 0.0)')})", "bool")
+        return k.let(f"select(0.0, {k.load(abuf, k.idx2(r, H, 'r0'))}, {eq})")
+
+    # 13. db1 = Sum(Where(Z1 == relu(Z1), dH1, 0), [0])
+    k = Kernel([(udb1, [H], F32), (uZ1, bshape(H), F32), (udH1, bshape(H), F32)], [H], symbolic)
+    k.acc()
+    r1 = k.loop(N)
+    k.update(masked(k, 1, 2, r1))
+    k.end()
+    k.store("acc0")
+    add("db1", k, "wave")
+
+    # 14. dW1 = Where(Z1 == relu(Z1), dH1, 0)^T x
+    k = Kernel([(udW1, [H, D], F32), (udH1, bshape(H), F32), (uZ1, bshape(H), F32), (1, bshape(D), F32)], [H, D], symbolic)
+    k.acc()
+    r2 = k.loop(N)
+    m = masked(k, 2, 1, r2)
+    tx = k.load(3, f"({r2} * {D}) + r1")
+    k.update(k.let(f"({m} * {tx})"))
+    k.end()
+    k.store("acc0")
+    add("dW1", k, f"tmpl:gemm;dtype=f32;epi=store;ta=1;tb=1;M={H};N={D};K={Bk};pa=mask;in_a=1;in_b=3;za=2")
+
+    outs = dict(loss=uloss, dW1=udW1, db1=udb1, dW2=udW2, db2=udb2)
+    return ks, leaves, outs
+
+
+def f16_linear(M: int, N: int, K: int, bias: bool = True, relu_a: bool = False):
+    """An f16 Linear forward as the lowering renders an f16 reduce: loads widened to f32 inside the loop,
+    f32 accumulation, f16(acc) after it (codegen/lower.go:667-716), the bias add in f16. Returns
+    (wgsl, bufs, ws, wc, expected key)."""
+    k = Kernel([(30, [M, N], F16), (1, [M, K], F16), (2, [N, K], F16)] + ([(3, [N], F16)] if bias else []),
+               [M, N], f16=True)
+    k.acc()
+    r2 = k.loop(K)
+    tx = k.load(1, k.idx2("r0", K, r2), widen=True)
+    if relu_a:
+        tx = k.let(f"max({tx}, 0.0)")
+    tw = k.load(2, f"(r1 * {K}) + {r2}", widen=True)
+    k.update(k.let(f"({tx} * {tw})"))
+    k.end()
+    if bias:
+        k.store(k.let(f"(f16(acc0) + {k.load(3, 'r1', 'f16')})", "f16"))
+    else:
+        k.store("f16(acc0)")
+    key = f"tmpl:gemm;dtype=f16;epi={'bias' if bias else 'store'};ta=0;tb=0;M={M};N={N};K={K}" + (";pa=relu" if relu_a else "")
+    bufs = [(u, int(np.prod(s)), d, list(s)) for u, s, d in k.bufs]
+    return k.source(), bufs, tuple(k.ws), tuple(k.wc), key
