@@ -609,6 +609,20 @@ struct Mlp3Trainer : ah_trainer {
             FILE *f = fopen(cache, "r");
             if (f) { fclose(f); int rc0 = ah_gemm_tune_cache(dev, cache, 0); if (rc0) return rc0; }
         }
+        // AH_MLP3_VARIANTS="v0,...,v7" fixes the eight contractions' variants (0: tune that one), for
+        // measurements of one choice against another
+        const char *fixed = getenv("AH_MLP3_VARIANTS");
+        if (fixed && *fixed) {
+            const char *p = fixed;
+            for (int i = 0; i < kGemms; i++) {
+                char *end = nullptr;
+                const long v = strtol(p, &end, 10);
+                if (end == p || v < 0 || v > kGemm16Variants)
+                    return set_error(AH_ERR_INVALID, "AH_MLP3_VARIANTS: 8 variants, 0..%d", kGemm16Variants);
+                if (v) dev->gemm_variant[tune_key(gemm(i, false))] = (int)v;
+                p = *end == ',' ? end + 1 : end;
+            }
+        }
         size_t most = 0;
         for (int i = 0; i < kGemms; i++) {
             GemmDesc g = gemm(i, false);
