@@ -12,6 +12,8 @@
 #include <float.h>
 
 #include <algorithm>
+#include <mutex>
+
 #include "ah_common.h"
 #include "rowops.h"
 #include "softmax_row.h"
@@ -90,22 +92,25 @@ __global__ __launch_bounds__(256) void softmax_ce_kernel(const float *z, const i
 }
 
 // Softmax-CE with the logit gradient's column sums (the output bias gradient) fused in: each wave
-// takes rows blockIdx.x * 4 + wave, then every 4 * gridDim.x rows further, holding each row in
-// registers, and keeps the column sums of its rows' dz in registers; the block's four waves add theirs
+// takes rows blockIdx.x * kSmWaves + wave, then every kSmWaves * gridDim.x rows further, holding each
+// row in registers, and keeps the column sums of its rows' dz in registers; the block's waves add theirs
 // in wave order into partial row blockIdx.x of part[gridDim.x][C] (summed in row order by the step's
-// tail), so the result does not depend on timing.
+// tail), so the result does not depend on timing. With 16 waves per block and up to 256 blocks, a batch
+// of up to 4096 rows gives every wave one row: the row's three dependent wave reductions then overlap
+// across waves instead of running back to back in one.
+constexpr int kSmWaves = 16;
 template <int VPR>
-__global__ __launch_bounds__(256) void softmax_ce_cols_kernel(const float *z, const int32_t *labels, int B, int C,
-                                                               float a, float *dz, float *rowloss, float *part) {
-    __shared__ float red[4][64 * VPR];
+__global__ __launch_bounds__(64 * kSmWaves) void softmax_ce_cols_kernel(const float *z, const int32_t *labels, int B, int C,
+                                                                        float a, float *dz, float *rowloss, float *part) {
+    __shared__ float red[kSmWaves][64 * VPR];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float col[VPR];
 #pragma unroll
     for (int j = 0; j < VPR; j++) col[j] = 0.0f;
     // the next row's loads are issued before this row's arithmetic, so a wave with several rows keeps
     // one row's loads in flight
-    const int step = gridDim.x * 4;
-    int row = blockIdx.x * 4 + wave;
+    const int step = gridDim.x * kSmWaves;
+    int row = blockIdx.x * kSmWaves + wave;
     float nv[VPR];
     if (row < B) softmax_ce_row_load<VPR>(z + (long)row * C, C, lane, nv);
     for (; row < B; row += step) {
@@ -119,8 +124,11 @@ __global__ __launch_bounds__(256) void softmax_ce_cols_kernel(const float *z, co
 #pragma unroll
     for (int j = 0; j < VPR; j++) red[wave][lane + 64 * j] = col[j];
     __syncthreads();
-    for (int c = threadIdx.x; c < C; c += 256)
-        part[(long)blockIdx.x * C + c] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
+    for (int c = threadIdx.x; c < C; c += 64 * kSmWaves) {
+        float acc = red[0][c];
+        for (int w = 1; w < kSmWaves; w++) acc += red[w][c];
+        part[(long)blockIdx.x * C + c] = acc;
+    }
 }
 
 // out[0] = (Sum_i v[i]) * a   (single block, fixed-order tree)
@@ -765,13 +773,13 @@ hipError_t softmax_ce(const float *z, const int32_t *labels, int B, int C, float
     return hipGetLastError();
 }
 int softmax_ce_cols_blocks(int B) {
-    const int b = (B + 3) / 4;
+    const int b = (B + kSmWaves - 1) / kSmWaves;
     return b < kSoftmaxColsMaxBlocks ? (b < 1 ? 1 : b) : kSoftmaxColsMaxBlocks;
 }
 hipError_t softmax_ce_cols(const float *z, const int32_t *labels, int B, int C, float a, float *dz, float *rowloss,
                            float *part, hipStream_t s) {
     if (B <= 0) return hipSuccess;
-    const dim3 grid(softmax_ce_cols_blocks(B)), block(256);
+    const dim3 grid(softmax_ce_cols_blocks(B)), block(64 * kSmWaves);
     if (C <= 64) hipLaunchKernelGGL(softmax_ce_cols_kernel<1>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
     else if (C <= 128) hipLaunchKernelGGL(softmax_ce_cols_kernel<2>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
     else if (C <= 256) hipLaunchKernelGGL(softmax_ce_cols_kernel<4>, grid, block, 0, s, z, labels, B, C, a, dz, rowloss, part);
@@ -847,6 +855,9 @@ long chain_scratch_floats() { return kChainScratchFloats; }
 // from ah_open; later calls return the stored address.
 hipError_t chain_scratch_init(int ordinal, float **out) {
     if (ordinal < 0 || ordinal >= kMaxDevices) return hipErrorInvalidDevice;
+    // handles opened from several threads look the address up under one lock (the table is per process)
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
     if (!g_scratch_ptr[ordinal]) {
         void *p = nullptr;
         hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));

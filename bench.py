@@ -147,9 +147,9 @@ def mlp_ce_kernels(B, D, H, C):
     if B <= 64 and D <= 896 and H <= 128 and C <= 16:
         return [("hidden", *f(B, H, D)), ("head", "flop32", 2 * 2.0 * B * C * H),
                 ("grad", "flop32", 2.0 * B * H * D + 2.0 * B * C * H)]
-    # softmax-CE (C <= 1024) also writes the output bias gradient's column sums as min(256, B/4)
+    # softmax-CE (C <= 1024) also writes the output bias gradient's column sums as min(256, B/16)
     # partial rows, which the tail sums; a wider C takes a separate column-sum launch (db2)
-    parts = min(256, max(1, (B + 3) // 4)) if C <= 1024 else 0
+    parts = min(256, max(1, (B + 15) // 16)) if C <= 1024 else 0
     return [("fc1", *f(B, H, D)), ("fc2", *f(B, C, H)), ("softmax_ce", "bytes", 8.0 * B * C + 8.0 * B + 4.0 * parts * C),
             ("db2", "bytes", 4.0 * B * C), ("dH1", *f(B, H, C)), ("dW2", *f(C, H, B)), ("dW1", *f(H, D, B)),
             ("tail", "bytes", 4.0 * B + 16.0 * (H + C) + 4.0 * parts * C)]
