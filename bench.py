@@ -83,24 +83,27 @@ def config_workload(cfg: int, batch4: int = 4096):
     raise SystemExit(f"bench: unknown config {cfg}")
 
 
-def cpu_baseline(cfg: int, inputs: dict):
+def cpu_baseline(cfg: int, inputs: dict, full: bool = False):
     """Oracle (CPU restatement, OpenMP over the host cores) on a bounded sample of the same workload,
-    about 10 s of CPU work."""
+    about 10 s of CPU work; full=True times config 3's whole batch-4096 step once (about a minute)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     threads = O.load().ora_num_threads()
     if cfg == 3:
         from anneal_amd.data import f16_quantize
-        Bs = 512
+        Bs = 4096 if full else 512
         q = {k: v for k, v in inputs.items()}
         q["x"], q["t"] = f16_quantize(inputs["x"][:Bs]), f16_quantize(inputs["t"][:Bs])
         t0 = time.perf_counter()
         O.mlp3_step(q, 1e-3)
         dt = time.perf_counter() - t0
-        full = dt * (4096 / Bs)
+        full = dt * (4096 / Bs)   # seconds per full step
+        if Bs == 4096:
+            sample = f"one full oracle step (batch 4096, full layer widths), {dt:.1f} s"
+        else:
+            sample = f"one oracle step at batch {Bs} of 4096 (full layer widths), {dt:.1f} s, scaled x{4096 // Bs} to a full step"
         return {"value": 1.0 / full, "unit": "train steps/s", "cores": threads, "kind": "port",
-                "label": CPU_LABEL, "sample": f"one oracle step at batch {Bs} of 4096 (full layer widths), {dt:.1f} s, "
-                          f"scaled x{4096 // Bs} to a full step"}
+                "label": CPU_LABEL, "sample": sample}
     if cfg == 4:
         B = len(inputs["labels"])
         Bs = min(512, B)
@@ -376,6 +379,7 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--batch", type=int, default=4096, help="config 4's batch N (1 to 4096)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-full", action="store_true", help="config 3: time one whole batch-4096 oracle step")
     ap.add_argument("--no-others", action="store_true", help="skip the steps/s of the other configs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 5 times (HBM counter calibration)")
@@ -445,7 +449,7 @@ def main():
     }
     if "flop_per_step" in meta:
         out["step_tflops"] = meta["flop_per_step"] * sps / 1e12
-    out["cpu_baseline"] = None if args.no_cpu else cpu_baseline(args.config, p)
+    out["cpu_baseline"] = None if args.no_cpu else cpu_baseline(args.config, p, full=args.cpu_full)
     t.close()
     if not args.no_others:
         out["other_configs"] = other_configs(dev, args.config)
