@@ -138,6 +138,7 @@ SIGNATURES = {
     "ah_trainer_step": (C.c_int, [_P, C.c_int64, C.c_int32]),
     "ah_trainer_steps": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32]),
     "ah_trainer_probe": (C.c_int, [_P, C.c_int32]),
+    "ah_trainer_probe_span": (C.c_int, [_P, C.c_int32, C.c_int32]),
     "ah_trainer_probe_read": (C.c_int, [_P, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "ah_trainer_kernel_count": (C.c_int, [_P, C.c_int64, C.POINTER(C.c_int32)]),
     "ah_trainer_kernel_name": (C.c_int, [_P, C.c_int32, C.c_char_p, C.c_int32]),

@@ -170,6 +170,10 @@ class Trainer:
     def probe(self, kernel_index: int) -> None:
         L.check(self.dev.lib.ah_trainer_probe(self.h, kernel_index))
 
+    def probe_span(self, first: int, last: int) -> None:
+        """hipEvents before launch `first` and after launch `last` of each following step."""
+        L.check(self.dev.lib.ah_trainer_probe_span(self.h, first, last))
+
     def probe_read(self):
         ms, n = C.c_double(), C.c_int64()
         L.check(self.dev.lib.ah_trainer_probe_read(self.h, C.byref(ms), C.byref(n)))

@@ -34,7 +34,8 @@ struct ah_trainer {
     std::vector<int64_t> dims;
     float lr = 0.0f;
     std::vector<void *> allocs;
-    int probe_index = -1;
+    int probe_index = -1;   // first launch a probe brackets (-1: no probe)
+    int probe_last = -1;    // last launch it brackets; probe_index - 1 brackets nothing (event cost alone)
     int launch_idx = 0;
     std::vector<hipEvent_t> ev_a, ev_b;
     size_t n_probe = 0;
@@ -66,26 +67,30 @@ struct ah_trainer {
         return AH_OK;
     }
 
-    // Every kernel of a step goes through here so a probe can bracket the index-th launch.
+    // Every kernel of a step goes through here so a probe can bracket launches probe_index..probe_last.
     template <class F>
     int launch(const char *what, F &&f) {
-        bool probe = (launch_idx == probe_index);
-        if (probe) {
+        const bool open = probe_index >= 0 && launch_idx == probe_index;
+        if (open) {
             if (n_probe >= ev_a.size()) {
                 hipEvent_t a, b;
                 // timing-only events: no system-scope fence (cache writeback and invalidate) at
-                // record time, which would add to the bracketed kernel's measured duration
+                // record time, which would add to the bracketed kernels' measured duration
                 AH_HIP(hipEventCreateWithFlags(&a, hipEventDisableSystemFence));
                 AH_HIP(hipEventCreateWithFlags(&b, hipEventDisableSystemFence));
                 ev_a.push_back(a);
                 ev_b.push_back(b);
             }
             AH_HIP(hipEventRecord(ev_a[n_probe], dev->stream));
+            if (probe_last < probe_index) {
+                AH_HIP(hipEventRecord(ev_b[n_probe], dev->stream));
+                n_probe++;
+            }
         }
         if (record_names) names.push_back(what);
         hipError_t e = f();
         if (e != hipSuccess) return set_error(AH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-        if (probe) {
+        if (probe_index >= 0 && probe_last >= probe_index && launch_idx == probe_last) {
             AH_HIP(hipEventRecord(ev_b[n_probe], dev->stream));
             n_probe++;
         }
@@ -683,7 +688,7 @@ struct Mlp3Trainer : ah_trainer {
         AH_HIP(fill_hash(b3, b3h, D3, 8u, 0.01f, s));
         constexpr int kSteps = 4;
         int rc = AH_OK;
-        const int saved = probe_index;
+        const int saved = probe_index, saved_last = probe_last;
         auto steps = [&](int n) {
             for (int k = 0; k < n; k++) {
                 launch_idx = 0;
@@ -703,10 +708,11 @@ struct Mlp3Trainer : ah_trainer {
                 for (int v = 1; v <= kGemm16Variants && rc == AH_OK; v++) {
                     dev->gemm_variant[keys[i]] = v;
                     if ((rc = steps(1))) break;   // the variant's first launch is not timed
-                    probe_index = i;
+                    probe_index = probe_last = i;
                     n_probe = 0;
                     rc = steps(kSteps);
                     probe_index = saved;
+                    probe_last = saved_last;
                     double ms = 0.0;
                     int64_t n = 0;
                     if (rc == AH_OK) rc = ah_trainer_probe_read(this, &ms, &n);
@@ -718,6 +724,7 @@ struct Mlp3Trainer : ah_trainer {
             dev->gemm_variant[keys[i]] = bv;
         }
         probe_index = saved;
+        probe_last = saved_last;
         n_probe = 0;
         launch_idx = 0;
         return rc;
@@ -1104,7 +1111,17 @@ int ah_trainer_steps(ah_trainer *t, int64_t batch, int32_t flags, int32_t n) {
 
 int ah_trainer_probe(ah_trainer *t, int32_t kernel_index) {
     if (!t) return set_error(AH_ERR_INVALID, "ah_trainer_probe: null trainer");
-    t->probe_index = kernel_index;
+    t->probe_index = t->probe_last = kernel_index < 0 ? -1 : kernel_index;
+    t->n_probe = 0;
+    return AH_OK;
+}
+
+int ah_trainer_probe_span(ah_trainer *t, int32_t first, int32_t last) {
+    if (!t) return set_error(AH_ERR_INVALID, "ah_trainer_probe_span: null trainer");
+    if (first < 0 || last < first - 1)
+        return set_error(AH_ERR_INVALID, "ah_trainer_probe_span: span [%d, %d]", first, last);
+    t->probe_index = first;
+    t->probe_last = last;
     t->n_probe = 0;
     return AH_OK;
 }

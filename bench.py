@@ -33,7 +33,7 @@ PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
 # the reference's own WebGPU path needs Go and a software Vulkan adapter, neither of which is on the box.
 CPU_LABEL = "CPU restatement \u2014 not the reference binary"
 
-TRAFFIC_BYTES = {(3, "dW2"): 268.6e6 + 100.7e6, (5, "chain_resident"): 134.8e6 + 143.0e6,
+TRAFFIC_BYTES = {(3, "dW2"): 268.6e6 + 100.7e6, (5, "chain_resident"): 134.8e6 + 139.5e6,
                  (5, "chain_grad"): 134.4e6 + 134.4e6,
                  (5, "chain_stats"): 134.3e6 + 4.2e6}
 
@@ -189,21 +189,30 @@ def step_kernels(t, batch, kernels):
 
 
 def kernel_table(t, batch, kernels, steps=20, warmup=50):
-    """Average duration of each launch of the step (hipEvents around it, eager steps), the dominant one's
-    roofline, and the per-kernel entries. `warmup` untimed steps run first, whatever the command line's
-    --warmup, so the first kernels probed see the same clocks and cache state as the last."""
+    """Average duration of each launch of the step (hipEvents on the trainer's stream, eager steps), the
+    dominant one's roofline, and the per-kernel entries. A launch's duration is the difference of two
+    probes that differ by that launch alone: events before launch i-1 and after launch i, less events
+    before launch i-1 and after launch i-1 (for launch 0: events around it, less the two events back to
+    back). The events' own cost is in both terms and cancels, so the launches' durations add up to the
+    step: each is the kernel's run time plus the dispatch gap in front of it. `warmup` untimed steps run
+    first, whatever the command line's --warmup, so the first kernels probed see the same clocks and
+    cache state as the last."""
     kernels = step_kernels(t, batch, kernels)
     nk = t.kernel_count(batch)
     assert nk == len(kernels), (nk, len(kernels))
     for _ in range(warmup):
         t.step(batch)
-    per = []
-    for i in range(nk):
-        t.probe(i)
+
+    def span(first, last):
+        t.probe_span(first, last)
         for _ in range(steps):
             t.step(batch)
         ms, n = t.probe_read()
-        per.append(ms / max(n, 1))
+        return ms / max(n, 1)
+    per = []
+    for i in range(nk):
+        j = max(i - 1, 0)
+        per.append(max(span(j, i) - span(j, i - 1), 1e-6))
     t.probe(-1)
     rows = []
     for (kname, kkind, amt), ms in zip(kernels, per):
@@ -414,16 +423,26 @@ def main():
     kernels = step_kernels(t, batch, kernels)
     _, kinfo = kernel_table(t, batch, kernels)
     dom = int(np.argmax([k["avg_us"] for k in kinfo]))
-    # Timed region: K steps, the dominant kernel bracketed by hipEvents on the library stream.
-    t.probe(dom)
+    # Timed region: K steps. The dominant kernel's duration is measured as in kernel_table, over the
+    # timed steps themselves: hipEvents before launch dom-1 and after launch dom in the first half, before
+    # launch dom-1 and after launch dom-1 in the second; the difference of the two averages is the launch.
+    # Reading the first half's events synchronizes the stream once, inside the timed region.
+    j = max(dom - 1, 0)
+    half = max(args.steps // 2, 1)
+    t.probe_span(j, dom)
     dev.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(half):
+        t.step(batch)
+    a_ms, a_n = t.probe_read()
+    t.probe_span(j, dom - 1)
+    for _ in range(args.steps - half):
         t.step(batch)
     dev.sync()
     elapsed = time.perf_counter() - t0
-    dom_ms, dom_n = t.probe_read()
+    b_ms, b_n = t.probe_read()
     t.probe(-1)
+    dom_ms, dom_n = (a_ms / max(a_n, 1) - (b_ms / b_n if b_n else 0.0)), 1
     dom_avg_s = dom_ms / max(dom_n, 1) / 1e3
 
     name, kk, amount = kernels[dom]

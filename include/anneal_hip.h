@@ -336,6 +336,10 @@ int ah_trainer_step(ah_trainer *t, int64_t batch, int32_t flags);
 int ah_trainer_steps(ah_trainer *t, int64_t batch, int32_t flags, int32_t n);
 /* Per-kernel probe: hipEvents around the index-th kernel launch of every following step. */
 int ah_trainer_probe(ah_trainer *t, int32_t kernel_index);
+/* Probe of launches first..last of every following step: one hipEvent before launch `first`, one after
+ * launch `last`; last = first - 1 records the two events back to back (their own cost alone). Two spans
+ * that differ by one launch give that launch's share of the step with the events' cost cancelled. */
+int ah_trainer_probe_span(ah_trainer *t, int32_t first, int32_t last);
 int ah_trainer_probe_read(ah_trainer *t, double *total_ms, int64_t *count);
 int ah_trainer_kernel_count(ah_trainer *t, int64_t batch, int32_t *count);
 /* Name of the index-th launch of a step, as counted by the last ah_trainer_kernel_count (NUL-terminated,

@@ -31,6 +31,7 @@ def test_null_device_calls_fail_cleanly():
     assert lib.ah_trainer_create(None, L.TRAIN_MLP_CE, dims, 4, C.c_float(0.01), C.byref(h)) == 1
     assert lib.ah_trainer_step(None, 64, 0) == 1
     assert lib.ah_trainer_probe(None, 0) == 1
+    assert lib.ah_trainer_probe_span(None, 0, 0) == 1
     assert lib.ah_chain_step(None, None, None, 8, 8, None, None, None) == 1
     assert lib.ah_softmax_ce(None, None, None, 4, 4, None, None) == 1
 

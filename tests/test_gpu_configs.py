@@ -276,6 +276,64 @@ def test_config3_steps_bit_repeatable(dev):
         np.testing.assert_array_equal(runs[0][k], runs[1][k], err_msg=k)
 
 
+def _params_bits(t, p, names):
+    return {k: t.get(k, p[k].size).view(np.uint32).copy() for k in names}
+
+
+@pytest.mark.parametrize("cfg", ["mlp3", "mlp_ce"])
+def test_multi_step_graphs_match_eager_steps(dev, cfg):
+    """ah_trainer_steps with graphs (19 steps = one 16-step graph + one 3-step graph, then again, so both
+    graphs are also replayed) leaves every parameter bit-identical to 38 eager steps; a probe span over
+    the eager steps changes no bit either and records one event pair per step."""
+    if cfg == "mlp3":
+        B, dims = 512, [512, 256, 512, 384, 256]
+        p = data.mlp3_inputs(*dims)
+        kind, keys, lr = L.TRAIN_MLP3_F16, ("x", "t", "W1", "b1", "W2", "b2", "W3", "b3"), 1e-3
+        names = ("W1", "b1", "W2", "b2", "W3", "b3")
+    else:
+        B, dims = 256, [256, 512, 2048, 512]
+        p = data.mlp_ce_inputs(*dims, x_lo=-1.0, x_hi=1.0)
+        kind, keys, lr = L.TRAIN_MLP_CE, ("x", "labels", "W1", "b1", "W2", "b2"), 0.01
+        names = ("W1", "b1", "W2", "b2")
+    runs = []
+    for graph in (False, True):
+        t = Trainer(dev, kind, dims, lr)
+        for k in keys:
+            t.set(k, p[k])
+        if graph:
+            t.steps(B, 19, graph=True)
+            t.steps(B, 19, graph=True)
+        else:
+            nk = t.kernel_count(B)
+            t.probe_span(0, nk - 1)
+            t.steps(B, 38)
+            ms, n = t.probe_read()
+            t.probe(-1)
+            assert n == 38 and ms > 0.0
+        runs.append(_params_bits(t, p, names))
+        t.close()
+    for k in names:
+        np.testing.assert_array_equal(runs[0][k], runs[1][k], err_msg=k)
+
+
+def test_probe_span_arguments(dev):
+    p = data.mlp_ce_inputs(64, 784, 128, 10)
+    t = Trainer(dev, L.TRAIN_MLP_CE, [64, 784, 128, 10], 0.01)
+    for k in ("x", "labels", "W1", "b1", "W2", "b2"):
+        t.set(k, p[k])
+    with pytest.raises(RuntimeError):
+        t.probe_span(2, 0)
+    with pytest.raises(RuntimeError):
+        t.probe_span(-1, 0)
+    t.probe_span(0, -1)          # the two events back to back
+    for _ in range(3):
+        t.step(64)
+    ms, n = t.probe_read()
+    assert n == 3 and ms >= 0.0
+    t.probe(-1)
+    t.close()
+
+
 @pytest.mark.parametrize("variant", [27, 30])
 def test_config3_paired_launches(dev, monkeypatch, variant):
     """dW3 split over K beside dH1, and dW1 split over K beside dW2, each pair one launch: the step
