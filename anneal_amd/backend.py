@@ -131,7 +131,7 @@ class Trainer:
     """One BASELINE config's device-resident training step (slot numbering in include/anneal_hip.h)."""
 
     SLOTS = {
-        L.TRAIN_MLP_CE: ["x", "labels", "W1", "b1", "W2", "b2", "loss", "dW1", "db1", "dW2", "db2"],
+        L.TRAIN_MLP_CE: ["x", "labels", "W1", "b1", "W2", "b2", "loss", "dW1", "db1", "dW2", "db2", "H1"],
         L.TRAIN_CONVNET: ["x", "labels", "cw1", "cb1", "cw2", "cb2", "fw", "fb", "loss", "dcw1", "dcb1", "dcw2",
                           "dcb2", "dfw", "dfb"],
         L.TRAIN_MLP3_F16: ["x", "t", "W1", "b1", "W2", "b2", "W3", "b3", "loss", "dW1", "db1", "dW2", "db2", "dW3",

@@ -353,8 +353,8 @@ struct MlpCeTrainer : ah_trainer {
     int get(int slot, void *h, int64_t n) override {
         struct { void *p; int64_t n; } t[] = {{x, (int64_t)Bmax * D}, {lab, Bmax}, {W1, (int64_t)H * D}, {b1, H},
                                               {W2, (int64_t)C * H}, {b2, C}, {loss, 1}, {gW1, (int64_t)H * D},
-                                              {gb1, H}, {gW2, (int64_t)C * H}, {gb2, C}};
-        if (slot < 0 || slot > 10) return set_error(AH_ERR_INVALID, "MLP_CE: bad slot %d", slot);
+                                              {gb1, H}, {gW2, (int64_t)C * H}, {gb2, C}, {H1, (int64_t)Bmax * H}};
+        if (slot < 0 || slot > 11) return set_error(AH_ERR_INVALID, "MLP_CE: bad slot %d", slot);
         if (n > t[slot].n) return set_error(AH_ERR_INVALID, "MLP_CE: slot %d too small", slot);
         return copy_out(dev, h, t[slot].p, (size_t)n * 4);
     }

@@ -309,7 +309,8 @@ enum {
     AH_TRAIN_CHAIN = 4,     /* dims {R, Cc}: config 5 */
 };
 /* Slot numbering per kind (host arrays are f32 unless noted; labels are int32):
- *  MLP_CE : 0 x, 1 labels, 2 W1, 3 b1, 4 W2, 5 b2, 6 loss, 7 dW1, 8 db1, 9 dW2, 10 db2
+ *  MLP_CE : 0 x, 1 labels, 2 W1, 3 b1, 4 W2, 5 b2, 6 loss, 7 dW1, 8 db1, 9 dW2, 10 db2,
+ *           11 H1 (the last step's ReLU outputs, batch rows first; -0.0 marks a dead unit) — read only
  *  CONVNET: 0 x, 1 labels, 2 cw1, 3 cb1, 4 cw2, 5 cb2, 6 fw, 7 fb, 8 loss, 9 dcw1, 10 dcb1, 11 dcw2,
  *           12 dcb2, 13 dfw, 14 dfb
  *  MLP3   : 0 x, 1 t, 2 W1, 3 b1, 4 W2, 5 b2, 6 W3, 7 b3, 8 loss, 9 dW1, 10 db1, 11 dW2, 12 db2,

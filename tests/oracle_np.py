@@ -85,6 +85,29 @@ def mlp_ce_step_f64(p: dict, lr: float):
     return loss, g, new
 
 
+def mlp_ce_grads_given_hidden_f64(p: dict, H1):
+    """The float64 backward of mlp_ce_step_f64 from a given hidden layer H1 (an f32 device readback of
+    the ReLU outputs, -0.0 marking a unit whose pre-activation was negative): the loss and the gradients
+    with the device's own ReLU mask, so rows whose mask f32 rounding decides can be checked too. With
+    H1 = relu(Z1) and a mask Z1 >= 0 it reduces to mlp_ce_step_f64 (tested on the CPU)."""
+    x = np.asarray(p["x"], np.float64)
+    lab = np.asarray(p["labels"], np.int64)
+    W2, b2 = (np.asarray(p[k], np.float64) for k in ("W2", "b2"))
+    h32 = np.ascontiguousarray(H1, np.float32)
+    live = h32.view(np.uint32) != np.uint32(0x80000000)
+    Hd = h32.astype(np.float64)
+    B = x.shape[0]
+    Z = Hd @ W2.T + b2
+    Zs = Z - Z.max(1, keepdims=True)
+    logp = Zs - np.log(np.exp(Zs).sum(1, keepdims=True))
+    onehot = np.zeros_like(Z)
+    onehot[np.arange(B), lab] = 1.0
+    loss = float((onehot * logp).sum() * (-1.0 / B))
+    dZ = (np.exp(logp) - onehot) / B
+    dZ1 = np.where(live, dZ @ W2, 0.0)
+    return loss, {"dW2": dZ.T @ Hd, "db2": dZ.sum(0), "dW1": dZ1.T @ x, "db1": dZ1.sum(0)}
+
+
 def relu_ambiguous_units(p: dict, atol: float = 1e-5):
     """Hidden units whose ReLU mask an f32 evaluation may set differently from another one: some batch
     row has |z| below atol (about ten times the f32 rounding of these 512-term pre-activations). Rounding decides Where(z == relu(z)) there, so a gradient row of such

@@ -30,7 +30,7 @@ def run_mlp_ce(dev, p, B, lr, graph=False):
     for k in ("x", "labels", "W1", "b1", "W2", "b2"):
         t.set(k, p[k])
     t.step(B, store_grads=True, graph=graph)
-    out = {"loss": t.get("loss", 1)[0]}
+    out = {"loss": t.get("loss", 1)[0], "H1": t.get("H1", B * H).reshape(B, H)}
     for k, n in (("dW1", H * D), ("db1", H), ("dW2", Cn * H), ("db2", Cn), ("W1", H * D), ("b1", H),
                  ("W2", Cn * H), ("b2", Cn)):
         out[k] = t.get(k, n)
@@ -150,6 +150,21 @@ def test_config4_n4096_vs_f64_closed_form(dev):
         assert check_update(keep1(out[k], n), keep1(p[k], n), keep1(new[k], n), 1e-4), k
     for k in ("W2", "b2"):
         assert check_update(out[k], p[k], new[k], 1e-4), k
+    # Every row, the ambiguous ones included, against the float64 backward run from the device's own
+    # hidden layer: first that hidden layer against the f64 forward (values to f32 rounding; the dead-unit
+    # tag wherever the pre-activation is clearly negative or positive), then all of dW1 and db1.
+    from oracle_np import mlp_ce_grads_given_hidden_f64
+    x64 = np.asarray(p["x"], np.float64)
+    Z1 = x64 @ np.asarray(p["W1"], np.float64).T + np.asarray(p["b1"], np.float64)
+    H1 = out["H1"]
+    assert np.max(np.abs(H1 - np.maximum(Z1, 0.0))) <= 1e-5 * max(1.0, np.max(np.abs(Z1)))
+    dead = H1.view(np.uint32) == np.uint32(0x80000000)
+    clear = np.abs(Z1) >= 1e-5
+    np.testing.assert_array_equal(dead[clear], (Z1 < 0)[clear])
+    cl, cg = mlp_ce_grads_given_hidden_f64(p, H1)
+    assert abs(out["loss"] - cl) <= 1e-4 * max(1, abs(cl))
+    for k, n in (("dW1", 512), ("db1", 1), ("dW2", 2048), ("db2", 1)):
+        assert O.relerr(out[k], cg[k].ravel()) < 1e-4, k
 
 
 def test_config4_one_capture_many_batches(dev):

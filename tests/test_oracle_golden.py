@@ -352,3 +352,32 @@ def test_mlp_ce_f64_closed_form_matches_c_oracle(B, D, H, Cn):
     assert abs(fl - wl) <= 1e-5 * max(1.0, abs(wl))
     for k in g:
         assert O.relerr(g[k], fg[k]) < 1e-5, k
+
+
+def test_mlp_ce_grads_given_hidden_reduces_to_closed_form():
+    """With the exact hidden layer relu(Z1) (dead units tagged -0.0), the conditioned backward equals the
+    float64 closed form; flipping one live unit's tag to dead removes exactly that unit's row of dZ1
+    from dW1 and db1 for that sample."""
+    from anneal_amd import data
+    from oracle_np import mlp_ce_grads_given_hidden_f64, mlp_ce_step_f64
+    p = data.mlp_ce_inputs(96, 64, 48, 10, seed=5, x_lo=-1.0, x_hi=1.0)
+    Z1 = np.asarray(p["x"], np.float64) @ np.asarray(p["W1"], np.float64).T + np.asarray(p["b1"], np.float64)
+    H1 = np.where(Z1 < 0, np.float32(-0.0), Z1.astype(np.float32)).astype(np.float32)
+    fl, fg, _ = mlp_ce_step_f64(p, 0.01)
+    gl, gg = mlp_ce_grads_given_hidden_f64(p, H1)
+    assert abs(gl - fl) < 1e-6
+    for k in fg:
+        assert O.relerr(gg[k], fg[k]) < 1e-6, k
+    n, j = np.argwhere(Z1 > 0.1)[0]
+    H2 = H1.copy()
+    H2[n, j] = np.float32(-0.0)          # the mask now drops (n, j); the forward sees 0 there
+    _, g2 = mlp_ce_grads_given_hidden_f64(p, H2)
+    H3 = H1.copy()
+    H3[n, j] = np.float32(0.0)           # same forward value, unit alive
+    _, g3 = mlp_ce_grads_given_hidden_f64(p, H3)
+    # the two differ only in the (n, j) term of dZ1: dW1[j] by dZ1[n, j] * x[n], db1[j] by dZ1[n, j]
+    dz1 = g3["db1"][j] - g2["db1"][j]
+    assert dz1 != 0
+    np.testing.assert_allclose(g3["dW1"][j] - g2["dW1"][j], dz1 * np.asarray(p["x"], np.float64)[n], rtol=1e-9, atol=1e-15)
+    rows = np.arange(48) != j
+    np.testing.assert_array_equal(g3["dW1"][rows], g2["dW1"][rows])
