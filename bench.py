@@ -85,13 +85,13 @@ def config_workload(cfg: int, batch4: int = 4096):
 
 def cpu_baseline(cfg: int, inputs: dict, full: bool = False):
     """Oracle (CPU restatement, OpenMP over the host cores) on a bounded sample of the same workload,
-    about 10 s of CPU work; full=True times config 3's whole batch-4096 step once (about a minute)."""
+    about 10-20 s of CPU work; full=True times config 3's whole batch-4096 step once (about a minute)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     threads = O.load().ora_num_threads()
     if cfg == 3:
         from anneal_amd.data import f16_quantize
-        Bs = 4096 if full else 512
+        Bs = 4096 if full else 1024
         q = {k: v for k, v in inputs.items()}
         q["x"], q["t"] = f16_quantize(inputs["x"][:Bs]), f16_quantize(inputs["t"][:Bs])
         t0 = time.perf_counter()
