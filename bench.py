@@ -1,7 +1,8 @@
 """Benchmark of anneal's training hot path on one MI355X.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
-  python bench.py --library-probe     (config-3 GEMM shapes here vs hipBLASLt, store epilogue)
+  python bench.py --library-probe     (config-3 GEMM shapes here vs hipBLASLt, store epilogue;
+                                       with --config 4 the config-4 f32 shapes at N = 4096)
 
 One "step" is one full training step of a BASELINE config (forward, backward, SGD) with inputs and
 parameters resident in HBM. Prints ONE JSON line: steps/s for the config, the roofline of its dominant
@@ -333,24 +334,34 @@ def copy_probe(mib: int):
     print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}))
 
 
-def library_probe():
-    """The eight config-3 contractions with a plain f16 store epilogue: this library (each shape tuned,
-    then timed) next to hipBLASLt (torch.matmul on the same layouts), 20 launches each, hipEvents."""
+def library_probe(cfg: int = 3):
+    """A config's contractions with a plain store epilogue: this library (each shape tuned, then timed)
+    next to hipBLASLt (torch.matmul on the same layouts), 20 launches each, hipEvents. Config 3: the
+    eight f16 shapes; config 4: the five f32 shapes at N = 4096 (torch with TF32 off, so both run the
+    f32 MFMA path)."""
     import torch
     from anneal_amd import _lib as L
     from anneal_amd.backend import Device
     dev = Device(0)
-    B, D0, D1, D2, D3 = 4096, 1024, 4096, 4096, 1024
-    shapes = [("fc1", 0, 0, B, D1, D0), ("fc2", 0, 0, B, D2, D1), ("fc3", 0, 0, B, D3, D2), ("dH2", 0, 1, B, D2, D3),
-              ("dW3", 1, 1, D3, D2, B), ("dH1", 0, 1, B, D1, D2), ("dW2", 1, 1, D2, D1, B), ("dW1", 1, 1, D1, D0, B)]
+    if cfg == 4:
+        torch.backends.cuda.matmul.allow_tf32 = False
+        N, D, H, C = 4096, 512, 2048, 512
+        shapes = [("fc1", 0, 0, N, H, D), ("fc2", 0, 0, N, C, H), ("dH1", 0, 1, N, H, C), ("dW2", 1, 1, C, H, N),
+                  ("dW1", 1, 1, H, D, N)]
+        dt, ndt, tdt = L.AH_F32, np.float32, torch.float32
+    else:
+        B, D0, D1, D2, D3 = 4096, 1024, 4096, 4096, 1024
+        shapes = [("fc1", 0, 0, B, D1, D0), ("fc2", 0, 0, B, D2, D1), ("fc3", 0, 0, B, D3, D2), ("dH2", 0, 1, B, D2, D3),
+                  ("dW3", 1, 1, D3, D2, B), ("dH1", 0, 1, B, D1, D2), ("dW2", 1, 1, D2, D1, B), ("dW1", 1, 1, D1, D0, B)]
+        dt, ndt, tdt = L.AH_F16, np.float16, torch.float16
     rng = np.random.default_rng(0)
-    big = 4096 * 4096
-    A = dev.buffer((rng.standard_normal(big) * 0.1).astype(np.float16), L.AH_F16)
-    Bb = dev.buffer((rng.standard_normal(big) * 0.1).astype(np.float16), L.AH_F16)
-    Cc = dev.buffer(big, L.AH_F16)
+    big = max(max(M * K, N_ * K, M * N_) for _, _, _, M, N_, K in shapes)   # elements of the largest operand
+    A = dev.buffer((rng.standard_normal(big) * 0.1).astype(ndt), dt)
+    Bb = dev.buffer((rng.standard_normal(big) * 0.1).astype(ndt), dt)
+    Cc = dev.buffer(big, dt)
     rows = []
     for name, ta, tb, M, N, K in shapes:
-        kw = dict(dtype=L.AH_F16, epi=L.EPI_STORE, ta=ta, tb=tb, M=M, N=N, K=K, A=A, B=Bb, lda=M if ta else K,
+        kw = dict(dtype=dt, epi=L.EPI_STORE, ta=ta, tb=tb, M=M, N=N, K=K, A=A, B=Bb, lda=M if ta else K,
                   ldb=N if tb else K, C_out=Cc, ldc=N, scale=1.0)
         variant, _ = dev.gemm_tune(iterations=3, **kw)
         for _ in range(3):
@@ -360,8 +371,8 @@ def library_probe():
         for _ in range(20):
             dev.gemm(**kw)
         ours = dev.timer_stop() / 20 * 1e3
-        a = torch.randn((K, M) if ta else (M, K), device="cuda", dtype=torch.float16)
-        b = torch.randn((K, N) if tb else (N, K), device="cuda", dtype=torch.float16)
+        a = torch.randn((K, M) if ta else (M, K), device="cuda", dtype=tdt)
+        b = torch.randn((K, N) if tb else (N, K), device="cuda", dtype=tdt)
         a2, b2 = (a.t() if ta else a), (b if tb else b.t())
         for _ in range(3):
             c = a2 @ b2
@@ -377,7 +388,7 @@ def library_probe():
         rows.append({"gemm": name, "M": M, "N": N, "K": K, "ta": ta, "tb": tb, "variant": variant,
                      "us": round(ours, 1), "tflops": round(fl / ours / 1e6), "hipblaslt_us": round(blas, 1),
                      "hipblaslt_tflops": round(fl / blas / 1e6)})
-    print(json.dumps({"library_probe": rows}))
+    print(json.dumps({"library_probe": rows, "config": cfg}))
 
 
 def main():
@@ -396,7 +407,7 @@ def main():
                     help="only time the config-3 contraction shapes here and in hipBLASLt (store epilogue)")
     args = ap.parse_args()
     if args.library_probe:
-        library_probe()
+        library_probe(args.config if args.config == 4 else 3)
         return
     if args.copy_probe:
         copy_probe(args.copy_probe)
