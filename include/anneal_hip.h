@@ -67,7 +67,8 @@ float ah_f16_to_f32(uint16_t h);   /* uop/dtype.go:447 Float16ToFloat32 */
 /* ── 3./4. modules and launches ──────────────────────────────────────────────
  * Replaces CreateShaderModule + pipeline creation + Dispatch (backend/webgpu/executor.go:254-395).
  * `source` is either HIP C++ source (compiled once by hiprtc for gfx950, cached by source hash) or a
- * template key "tmpl:<name>;k=v;..." selecting a hand-written kernel.
+ * template key "tmpl:<name>;k=v;..." selecting a hand-written kernel (the names and their keys are
+ * listed in anneal_amd/csrc/templates.cpp).
  * Kernel arguments: n_ptrs device pointers (data0 = output, data1.. = inputs, PARAM order as in
  * codegen/wgsl.go:58-76), then n_scalars int32 values (the params_n uniform of symbolic kernels). */
 int ah_module_get(ah_device *dev, const char *source, const char *entry, ah_kernel **out);

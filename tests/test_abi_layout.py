@@ -1,5 +1,5 @@
-"""Struct layouts of include/anneal_hip.h, as the C compiler lays them out, against the table the Go
-binding (package hip init) and the Python ctypes mirror (anneal_amd/_lib.py) assume.
+"""Struct layouts of include/anneal_hip.h, as the C compiler lays them out, against the table a Go
+binding of the header (its package init check) and the Python ctypes mirror (anneal_amd/_lib.py) assume.
 CPU only: compiles an offsetof() probe of the header with gcc."""
 import ctypes as C
 import os
