@@ -9,9 +9,9 @@
 //   UPCAST(axis 0|1, f in {2,4})      MFMA register tile per wave along M or N: f blocks of 32, the waves
 //                                     unchanged (the tile grows or shrinks); f32 kernel: tile 64*f
 //   TILE(axis 2, TS in {8,16,32})     the reduce-axis tile staged through LDS: k per stage and stages in
-//                                     flight, (32, 4), (64, 2), (64, 3)
+//                                     flight, (32, 4), (64, 2), (64, 3) (f32: the direct-to-LDS kernel's)
 //   VECTORIZE(axis 2, 4)              16-byte LDS-DMA staging issued from asm with the cross-barrier
-//                                     fragment prefetch (fetch mode 4)
+//                                     fragment prefetch (fetch mode 4); f32: the direct-to-LDS kernel
 //   GROUP(axis 2, g in {2,4})         k-groups: g wave sets split K and reduce through LDS
 //   SCHEDULE(axis 0, m in {5,6,7})    where the DMAs and fragment reads sit between the MFMAs (fetch mode m)
 // Without VECTORIZE or SCHEDULE the fetch scheduling is left to the kernel (any of the compiler-scheduled
@@ -53,8 +53,10 @@ struct Knobs {
     G16Params p{};   // f16
     int tile = 0;    // f32 (0 = by shape)
     int kg = 0;      // f32 (0 = by shape)
+    bool dma = false;   // f32: the direct-to-LDS kernel, with k per stage bk and stages ns
+    int bk = 0, ns = 0;
     bool operator==(const Knobs &o) const {
-        return f16 == o.f16 && tile == o.tile && kg == o.kg &&
+        return f16 == o.f16 && tile == o.tile && kg == o.kg && dma == o.dma && bk == o.bk && ns == o.ns &&
                (!f16 || memcmp(&p, &o.p, sizeof p) == 0);
     }
 };
@@ -109,8 +111,24 @@ int key_info(const std::string &key, KeyInfo *ki) {
     } else {
         ki->knobs.tile = (int)geti(ki->kv, "tile", 0);
         ki->knobs.kg = (int)geti(ki->kv, "kg", 0);
+        const int dma = (int)geti(ki->kv, "dma", -1);
+        if (dma >= 0) {
+            if (!gemm32d_config(kGemm32dBase + dma, &ki->knobs.tile, &ki->knobs.bk, &ki->knobs.ns))
+                return set_error(AH_ERR_INVALID, "opts: dma=%d", dma);
+            ki->knobs.dma = true;
+            ki->knobs.kg = 0;
+        }
     }
     return AH_OK;
+}
+
+// The direct-to-LDS configuration index with these parameters, or -1.
+int dma_index(const Knobs &k) {
+    for (int i = 0; i < kGemm32dConfigs; i++) {
+        int bm, bk, ns;
+        if (gemm32d_config(kGemm32dBase + i, &bm, &bk, &ns) && bm == k.tile && bk == k.bk && ns == k.ns) return i;
+    }
+    return -1;
 }
 
 // Applies one Opt to the parameters; false if the Opt does not apply to this kernel.
@@ -155,6 +173,8 @@ bool apply_opt(Knobs &k, const ah_opt &o) {
         default: return false;
         }
     }
+    // f32: UPCAST sets the tile (64 * f); the register-staged kernel takes GROUP (k-groups); VECTORIZE
+    // selects the direct-to-LDS kernel (gemm32d.hip), whose TILE sets k per stage and stages in flight
     switch (o.kind) {
     case AH_OPT_UPCAST:
         if ((o.axis != 0 && o.axis != 1) || (o.arg != 2 && o.arg != 4)) return false;
@@ -162,16 +182,31 @@ bool apply_opt(Knobs &k, const ah_opt &o) {
         if (k.kg && !gemm32_kgroups_ok(k.tile, k.kg)) k.kg = 1;
         return true;
     case AH_OPT_GROUP:
-        if (o.axis != 2 || (o.arg != 2 && o.arg != 4)) return false;
+        if (k.dma || o.axis != 2 || (o.arg != 2 && o.arg != 4)) return false;
         if (!k.tile) k.tile = 64;
         k.kg = o.arg;
         return gemm32_kgroups_ok(k.tile, k.kg);
+    case AH_OPT_VECTORIZE:
+        if (k.dma || k.kg || o.axis != 2 || o.arg != 4) return false;
+        k.dma = true;
+        if (!k.tile) k.tile = 64;
+        k.bk = 32;
+        k.ns = 4;
+        return true;
+    case AH_OPT_TILE:
+        if (!k.dma || o.axis != 2) return false;
+        if (o.arg == 8) { k.bk = 32; k.ns = 4; }
+        else if (o.arg == 16) { k.bk = 64; k.ns = 2; }
+        else if (o.arg == 32) { k.bk = 64; k.ns = 3; }
+        else return false;
+        return true;
     default: return false;
     }
 }
 
 bool instantiated(const Knobs &k) {
     if (k.f16) return f16_variant_of(k.p) != 0;
+    if (k.dma) return k.kg == 0 && dma_index(k) >= 0;
     return k.tile == 0 || (k.tile == 64 || k.tile == 128 || k.tile == 256);
 }
 
@@ -183,8 +218,14 @@ std::string emit_key(const KeyInfo &ki, const Knobs &k) {
     } else {
         kv.erase("tile");
         kv.erase("kg");
-        if (k.tile) kv["tile"] = std::to_string(k.tile);
-        if (k.kg) kv["kg"] = std::to_string(k.kg);
+        kv.erase("dma");
+        if (k.dma) {
+            kv.erase("splits");
+            kv["dma"] = std::to_string(dma_index(k));
+        } else {
+            if (k.tile) kv["tile"] = std::to_string(k.tile);
+            if (k.kg) kv["kg"] = std::to_string(k.kg);
+        }
     }
     std::string out = "tmpl:" + ki.name;
     for (auto &e : kv) out += ";" + e.first + "=" + e.second;

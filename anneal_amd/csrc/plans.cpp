@@ -147,6 +147,7 @@ static const std::vector<F32Cfg> &f32_cfgs() {
                     c.push_back({tile, kg, sp});
                 }
             }
+        for (int i = 0; i < kGemm32dConfigs; i++) c.push_back({kGemm32dBase + i, 0, 0});   // direct-to-LDS stages
         return c;
     }();
     return v;

@@ -135,7 +135,7 @@ int ensure_ws(TemplateKernel *t, int64_t bytes) {
 
 // ── gemm ─────────────────────────────────────────────────────────────────────────────────────────
 // "tmpl:gemm;dtype=f16|f32;epi=...;ta=0|1;tb=0|1;M=..;N=..;K=..[;scale=s][;lr=l][;variant=v][;tile=t;kg=g]
-//  [;swap_ab=1][;in_a=i;in_b=j;in_bias=k][;pa=relu|mask;za=z][;pb=relu|mask;zb=z]"
+//  [;splits=s][;dma=i][;swap_ab=1][;in_a=i;in_b=j;in_bias=k][;pa=relu|mask;za=z][;pb=relu|mask;zb=z]"
 // swap_ab: A is the second input PARAM and B the first; in_a / in_b / in_bias name the PARAM of each role
 // outright (a rendered kernel binds its inputs in the scheduler's order). Operand prologues, the
 // elementwise ops the reference's scheduler inlines into a contraction's loop: pa=relu reads max(A, 0)
@@ -187,6 +187,13 @@ int template_gemm(const Params &P, TemplateKernel *t) {
         return set_error(AH_ERR_INVALID, "tmpl gemm: kg=%d needs a tile that admits it", base.kgroups);
     base.splits = (int)P.integer("splits", 0);
     if (base.splits < 0 || base.splits > 16) return set_error(AH_ERR_INVALID, "tmpl gemm: splits=%d (0..16)", base.splits);
+    // dma=i: f32 configuration i of the direct-to-LDS kernel (gemm32d.hip) in place of tile / kg / splits
+    const int dma = (int)P.integer("dma", -1);
+    if (dma >= 0) {
+        if (dma >= kGemm32dConfigs || base.tile || base.kgroups || base.splits)
+            return set_error(AH_ERR_INVALID, "tmpl gemm: dma=%d (0..%d, without tile, kg or splits)", dma, kGemm32dConfigs - 1);
+        base.tile = kGemm32dBase + dma;
+    }
     const bool swap_ab = P.integer("swap_ab", 0) != 0;
     // PARAM of each role: A, B, bias (or the first epilogue input), and the prologues' mask sources
     const int pA = (int)P.integer("in_a", swap_ab ? 2 : 1), pB = (int)P.integer("in_b", swap_ab ? 1 : 2);

@@ -339,8 +339,9 @@ def test_gemm_f32_split_k(dev, epi, splits):
 
 def test_gemm_f32_tune_and_cache(dev, tmp_path):
     """The tuner over the f32 kernel's (tile, k-groups, splits) configurations: it returns an index into
-    the 38-entry table, later automatic launches of the shape use the winner (against float64), and the
-    choice survives the disk cache, where an index past the table is rejected."""
+    the 43-entry table (38 register-staged, 5 direct-to-LDS), later automatic launches of the shape use
+    the winner (against float64), and the choice survives the disk cache, where an index past the table
+    is rejected."""
     M, N, K = 256, 512, 2048
     A = RNG.standard_normal((M, K)).astype(np.float32)
     B = RNG.standard_normal((N, K)).astype(np.float32)
@@ -349,7 +350,7 @@ def test_gemm_f32_tune_and_cache(dev, tmp_path):
     common = dict(dtype=L.AH_F32, epi=L.EPI_STORE, ta=0, tb=0, M=M, N=N, K=K, A=dA, B=dB, lda=K, ldb=K, C_out=dC,
                   ldc=N)
     best, us = dev.gemm_tune(iterations=2, **common)
-    assert 0 <= best < 38 and us > 0
+    assert 0 <= best < 43 and us > 0
     dev.gemm(**common)
     ref = A.astype(np.float64) @ B.astype(np.float64).T
     assert O.relerr(dC.read().reshape(M, N), ref) < 1e-5
@@ -359,11 +360,71 @@ def test_gemm_f32_tune_and_cache(dev, tmp_path):
     assert f"0/0/0/{M}/{N}/{K} {best}" in lines
     dev.gemm_tune_cache(str(path), False)
     bad = tmp_path / "bad32.txt"
-    bad.write_text(lines[0] + f"\n0/0/0/{M}/{N}/{K} 38\n")
+    bad.write_text(lines[0] + f"\n0/0/0/{M}/{N}/{K} 43\n")
     with pytest.raises(L.AnnealHipError, match="bad line"):
         dev.gemm_tune_cache(str(bad), False)
     for b in (dA, dB, dC):
         b.free()
+
+
+# direct-to-LDS f32 configurations (gemm32d.hip): (tile, k per stage, stages)
+DMA_CFGS = [(64, 64, 3), (64, 64, 4), (64, 32, 4), (128, 32, 4), (128, 64, 2)]
+
+
+@pytest.mark.parametrize("dma", range(5))
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("epi", ["store", "bias_relu", "mask", "grad"])
+def test_gemm_f32_dma_same_bits_as_register_staged(dev, dma, ta, tb, epi):
+    """The direct-to-LDS f32 kernel adds K in the order of the register-staged kernel with one k-group
+    and no split, so each of its configurations gives the same bits as that kernel at the same tile, for
+    every layout and epilogue, on a ragged shape (M, N not multiples of the tile); both against float64.
+    The 128-wide configurations take only the store and bias epilogues and run the automatic choice for
+    the others, which must then match that choice's bits."""
+    from anneal_amd.executor import Buffer, ExecItem, Executor
+    tile = DMA_CFGS[dma][0]
+    M, N, K = 200, 300, 1024
+    common = f"tmpl:gemm;dtype=f32;epi={epi};ta={ta};tb={tb};M={M};N={N};K={K}"
+    dma_key = common + f";dma={dma}"
+    fallback = tile == 128 and epi in ("mask", "grad")
+    ref_key = common if fallback else common + f";tile={tile};kg=1;splits=1"
+    bufs = [Buffer(10, M * N, [M, N], L.AH_F32), Buffer(1, M * K, [K, M] if ta else [M, K], L.AH_F32),
+            Buffer(2, N * K, [K, N] if tb else [N, K], L.AH_F32)]
+    rng = np.random.default_rng(31 + dma)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K)).astype(np.float32)
+    ins = {1: store_operand(A, ta).ravel(), 2: store_operand(B, tb).ravel()}
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    if epi in ("bias_relu", "mask"):
+        bufs.append(Buffer(3, N if epi == "bias_relu" else M * N, [N] if epi == "bias_relu" else [M, N], L.AH_F32))
+    if epi == "bias_relu":
+        bias = rng.standard_normal(N).astype(np.float32)
+        ins[3] = bias
+        ref = np.maximum(ref + bias, 0)
+    elif epi == "mask":
+        H = rng.standard_normal((M, N)).astype(np.float32)
+        H = np.where(H < 0, np.float32(-0.0), H).astype(np.float32)
+        ins[3] = H.ravel()
+        ref = np.where(np.signbit(H) & (H == 0), 0.0, ref)
+    elif epi == "grad":
+        ref = -ref   # SGD with lr 1 on a zeroed array: the array becomes -g
+    ex = Executor(dev)
+    got = ex.run([ExecItem(dma_key, bufs)], ins)[10].reshape(M, N)
+    want = ex.run([ExecItem(ref_key, bufs)], ins)[10].reshape(M, N)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    if epi == "grad":
+        return   # the grad key's scale and sign are the register-staged kernel's, checked by its own tests
+    assert O.relerr(got, ref) < 1e-5
+
+
+def test_gemm_f32_dma_key_checks(dev):
+    """dma=i is a configuration index, and it excludes tile / kg / splits."""
+    from anneal_amd.executor import Buffer, ExecItem, Executor
+    bufs = [Buffer(10, 64 * 64, [64, 64], L.AH_F32), Buffer(1, 64 * 64, [64, 64], L.AH_F32),
+            Buffer(2, 64 * 64, [64, 64], L.AH_F32)]
+    ins = {1: np.ones(64 * 64, np.float32), 2: np.ones(64 * 64, np.float32)}
+    for bad in ("dma=5", "dma=0;tile=64", "dma=1;splits=2"):
+        with pytest.raises(L.AnnealHipError, match="dma"):
+            Executor(dev).run([ExecItem(f"tmpl:gemm;dtype=f32;epi=store;ta=0;tb=0;M=64;N=64;K=64;{bad}", bufs)], ins)
 
 
 @pytest.mark.parametrize("cfg", [(64, 0, 4), (64, 4, 2), (128, 2, 8), (128, 0, 16), (64, 1, 3)])

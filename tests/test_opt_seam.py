@@ -66,3 +66,24 @@ def test_f32_tile_and_kgroups():
         apply_opts(F32, [(L.OPT_UPCAST, 0, 4), (L.OPT_GROUP, 2, 4)])   # a 256 tile admits no k-groups
     acts = action_space(F32)
     assert (L.OPT_UPCAST, 0, 2) in acts and (L.OPT_GROUP, 2, 2) in acts and (L.OPT_LOCAL, 0, 8) not in acts
+
+
+def test_f32_direct_to_lds_opts():
+    """VECTORIZE selects the f32 direct-to-LDS kernel (key dma=i, no tile / kg / splits), TILE then sets
+    its k per stage and stages in flight, UPCAST its tile; k-groups do not combine with it, and a
+    (tile, stage) pair it does not instantiate fails closed."""
+    k = apply_opts(F32, [(L.OPT_VECTORIZE, 2, 4)])
+    assert params(k)["dma"] == "2" and "tile" not in params(k) and "kg" not in params(k)   # 64 tile, k 32 x 4
+    assert params(apply_opts(F32, [(L.OPT_VECTORIZE, 2, 4), (L.OPT_TILE, 2, 32)]))["dma"] == "0"   # k 64 x 3
+    assert params(apply_opts(F32, [(L.OPT_VECTORIZE, 2, 4), (L.OPT_UPCAST, 0, 2)]))["dma"] == "3"  # 128, k 32 x 4
+    assert params(apply_opts(F32, [(L.OPT_VECTORIZE, 2, 4), (L.OPT_UPCAST, 1, 2), (L.OPT_TILE, 2, 16)]))["dma"] == "4"
+    with pytest.raises(L.AnnealHipError):
+        apply_opts(F32, [(L.OPT_VECTORIZE, 2, 4), (L.OPT_TILE, 2, 16)])      # a 64 tile with k 64 x 2: none
+    with pytest.raises(L.AnnealHipError):
+        apply_opts(F32, [(L.OPT_GROUP, 2, 2), (L.OPT_VECTORIZE, 2, 4)])      # k-groups stay register-staged
+    with pytest.raises(L.AnnealHipError):
+        apply_opts(F32, [(L.OPT_VECTORIZE, 2, 4), (L.OPT_GROUP, 2, 2)])
+    acts = action_space(F32)
+    assert (L.OPT_VECTORIZE, 2, 4) in acts and (L.OPT_TILE, 2, 8) not in acts   # TILE only after VECTORIZE
+    dk = apply_opts(F32, [(L.OPT_VECTORIZE, 2, 4)])
+    assert (L.OPT_TILE, 2, 32) in action_space(dk) and (L.OPT_GROUP, 2, 2) not in action_space(dk)
