@@ -206,7 +206,8 @@ typedef struct {
     float lr;
     float *gout;
     float *lossacc;
-    int32_t tile;           /* 0 = auto, 64, 128, 256 */
+    int32_t tile;           /* 0 = auto, 64, 128, 256 (register-staged f32 kernel), 1000 + i (f32 direct-to-LDS
+                               configuration i, 0..4; see ah_gemm_tune) */
     int32_t variant;        /* f16 kernel variant: 0 = auto (the tuned choice if any), 1..31 = fixed tile /
                                wave / fetch / k-group choices (table Var<V>, gemm16_kernel.h);
                                the knob a BEAM-style search times (codegen/beam.go:41-541) */
@@ -223,12 +224,16 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * tiling and scheduling and accumulate each output over k in the same order (bit-identical results);
  * the k-group variants 10, 11, 15, 25, 28 and 31 add two k-halves, which rounds differently in f32 (relative
  * 1e-6 level). For an f32 contraction (dtype AH_F32) the candidates are the f32 kernel's (tile, k-groups,
- * splits of K across workgroups) configurations, 38 of them, and *best_variant is the winner's index:
- * 0 is the shape's automatic choice, then tile 64 and 128 each with k-groups auto / 1 / 2 / 4 (as the
- * tile admits) and splits auto / 1 / 2 / 4 / 8 / 16 in that nesting order (a fixed k-group count takes
- * no automatic split, so splits auto is listed only with k-groups auto). Later f32 launches of the shape
- * with tile, k-groups and splits all automatic use it. Configurations add K in different orders, so
- * their results differ at the rounding level. */
+ * splits of K across workgroups) configurations and the direct-to-LDS kernel's, 43 in all, and
+ * *best_variant is the winner's index: 0 is the shape's automatic choice, then the register-staged
+ * kernel's tile 64 and 128 each with k-groups auto / 1 / 2 / 4 (as the tile admits) and splits auto / 1 /
+ * 2 / 4 / 8 / 16 in that nesting order (a fixed k-group count takes no automatic split, so splits auto is
+ * listed only with k-groups auto), indices 1-37; then the direct-to-LDS configurations 0-4 (tile 64 with
+ * k 64 x 3 stages, 64 x 4, 32 x 4; tile 128 with k 32 x 4, 64 x 2), indices 38-42. The automatic choice is
+ * the direct-to-LDS kernel on 64-wide tiles when they number at least 256, the register-staged kernel
+ * otherwise. Later f32 launches of the shape with tile, k-groups and splits all automatic use the
+ * winner. Configurations add K in different orders, so their results differ at the rounding level;
+ * those of one tile width without k-groups or splits give the same bits in either kernel. */
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us);
 /* BEAM's disk cache (codegen/beam.go:118-169): save (save != 0) the device's tuned choices to path, one
  * "dtype/ta/tb/M/N/K variant" line each under a header naming the gfx arch, or merge a saved file into
@@ -242,7 +247,8 @@ int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save);
  * template key's tuning parameters instead of an AST: LOCAL(axis 0|1, 8|16|32) the waves along M or N
  * (arg/8), UPCAST(axis 0|1, 2|4) the MFMA register tile per wave (f32 kernel: tile 64*arg), TILE(axis 2,
  * 8|16|32) the LDS stage (k 32 x 4 stages, 64 x 2, 64 x 3), VECTORIZE(axis 2, 4) 16-byte asm LDS-DMA
- * staging; GROUP(axis 2, 2|4) k-groups and SCHEDULE(axis 0, 5..7) the DMA/fragment-read interleave are
+ * staging (f32: the direct-to-LDS kernel, whose stage TILE then sets; the key gets dma=i);
+ * GROUP(axis 2, 2|4) k-groups and SCHEDULE(axis 0, 5..7) the DMA/fragment-read interleave are
  * MI355X additions. Only "tmpl:gemm" keys have tunable parameters. */
 enum { AH_OPT_IDENTITY = 0, AH_OPT_LOCAL = 1, AH_OPT_TILE = 2, AH_OPT_UPCAST = 3, AH_OPT_VECTORIZE = 4,
        AH_OPT_GROUP = 5, AH_OPT_SCHEDULE = 6 };
