@@ -516,11 +516,13 @@ hipError_t gemm_launch(const GemmDesc &d, hipStream_t s) {
         return launch_layout<half_t>(d, s);
     }
     if (d.A2 || d.C2) return hipErrorInvalidValue;
-    // The automatic f32 choice: the direct-to-LDS kernel on 64-wide tiles when they fill the chip (every
-    // 64-wide configuration adds K in the same order, so tuning among them never changes a result),
-    // with deeper stages for long K; the register-staged kernel with its k-groups and splits otherwise.
+    // The automatic f32 choice: the direct-to-LDS kernel on 64-wide tiles when they fill the chip, or half
+    // of it at K <= 1024 (every 64-wide configuration adds K in the same order, so tuning among them never
+    // changes a result), with deeper stages for long K; otherwise the register-staged kernel, whose
+    // k-groups and splits of K spread a long K over more waves.
+    const long t64 = (long)((d.M + 63) / 64) * ((d.N + 63) / 64);
     if (d.dtype == GEMM_F32 && d.tile == 0 && d.kgroups == 0 && d.splits == 0 && !use_dot(d) &&
-        (long)((d.M + 63) / 64) * ((d.N + 63) / 64) >= 256) {
+        (t64 >= 256 || (t64 >= 128 && d.K <= 1024))) {
         const int cfg = kGemm32dBase + (d.K >= 4096 ? 0 : 2);
         int bm, bk, ns;
         if (gemm32d_config(cfg, &bm, &bk, &ns) && gemm32d_ok(d, bm, bk)) {

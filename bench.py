@@ -334,10 +334,10 @@ def copy_probe(mib: int):
     print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}))
 
 
-def library_probe(cfg: int = 3):
+def library_probe(cfg: int = 3, batch: int = 4096):
     """A config's contractions with a plain store epilogue: this library (each shape tuned, then timed)
     next to hipBLASLt (torch.matmul on the same layouts), 20 launches each, hipEvents. Config 3: the
-    eight f16 shapes; config 4: the five f32 shapes at N = 4096 (torch with TF32 off, so both run the
+    eight f16 shapes; config 4: the five f32 shapes at N = batch (torch with TF32 off, so both run the
     f32 MFMA path)."""
     import torch
     from anneal_amd import _lib as L
@@ -345,7 +345,7 @@ def library_probe(cfg: int = 3):
     dev = Device(0)
     if cfg == 4:
         torch.backends.cuda.matmul.allow_tf32 = False
-        N, D, H, C = 4096, 512, 2048, 512
+        N, D, H, C = batch, 512, 2048, 512
         shapes = [("fc1", 0, 0, N, H, D), ("fc2", 0, 0, N, C, H), ("dH1", 0, 1, N, H, C), ("dW2", 1, 1, C, H, N),
                   ("dW1", 1, 1, H, D, N)]
         dt, ndt, tdt = L.AH_F32, np.float32, torch.float32
@@ -407,7 +407,7 @@ def main():
                     help="only time the config-3 contraction shapes here and in hipBLASLt (store epilogue)")
     args = ap.parse_args()
     if args.library_probe:
-        library_probe(args.config if args.config == 4 else 3)
+        library_probe(args.config if args.config == 4 else 3, args.batch)
         return
     if args.copy_probe:
         copy_probe(args.copy_probe)

@@ -230,8 +230,8 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * 2 / 4 / 8 / 16 in that nesting order (a fixed k-group count takes no automatic split, so splits auto is
  * listed only with k-groups auto), indices 1-37; then the direct-to-LDS configurations 0-4 (tile 64 with
  * k 64 x 3 stages, 64 x 4, 32 x 4; tile 128 with k 32 x 4, 64 x 2), indices 38-42. The automatic choice is
- * the direct-to-LDS kernel on 64-wide tiles when they number at least 256, the register-staged kernel
- * otherwise. Later f32 launches of the shape with tile, k-groups and splits all automatic use the
+ * the direct-to-LDS kernel on 64-wide tiles when they number at least 256 (at least 128 for K <= 1024),
+ * the register-staged kernel otherwise. Later f32 launches of the shape with tile, k-groups and splits all automatic use the
  * winner. Configurations add K in different orders, so their results differ at the rounding level;
  * those of one tile width without k-groups or splits give the same bits in either kernel. */
 int ah_gemm_tune(ah_device *dev, const ah_gemm_desc *d, int32_t iterations, int32_t *best_variant, double *best_us);
