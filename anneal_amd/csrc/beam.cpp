@@ -220,7 +220,6 @@ std::string emit_key(const KeyInfo &ki, const Knobs &k) {
         kv.erase("kg");
         kv.erase("dma");
         if (k.dma) {
-            kv.erase("splits");
             kv["dma"] = std::to_string(dma_index(k));
         } else {
             if (k.tile) kv["tile"] = std::to_string(k.tile);

@@ -108,12 +108,13 @@ bool gemm16_variant_params(int variant, G16Params *out);
 // The variant an f16 contraction with variant 0 and no tuned choice runs (chosen by shape).
 int gemm16_default_variant(const GemmDesc &d);
 // f32 contractions with direct global->LDS stages (gemm32d.hip): GemmDesc::tile = kGemm32dBase + i selects
-// configuration i (tile, k per stage, stages in flight) of gemm32d_config; kgroups and splits do not
-// apply. A shape a configuration does not take (gemm32d_ok) runs the automatic choice instead, which is
-// the direct-to-LDS kernel on 64-wide tiles where those fill the chip (gemm_launch).
+// configuration i (tile, k per stage, stages in flight) of gemm32d_config; kgroups does not apply, and
+// splits > 1 splits K across workgroups as the register-staged kernel does (gemm32d_splits). A shape a
+// configuration does not take (gemm32d_ok) runs the automatic choice instead (gemm_launch).
 constexpr int kGemm32dBase = 1000, kGemm32dConfigs = 5;
 bool gemm32d_config(int tile, int *bm, int *bk, int *ns);
 bool gemm32d_ok(const GemmDesc &d, int bm, int bk);
+int gemm32d_splits(const GemmDesc &d, int bm, int bk);
 hipError_t gemm32d_launch(const GemmDesc &d, hipStream_t s);
 // k-groups an f32 tile size admits (LDS budget): 64 -> 1, 2, 4; 128 -> 1, 2; 256 -> 1.
 inline bool gemm32_kgroups_ok(int tile, int kg) {

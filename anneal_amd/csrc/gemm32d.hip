@@ -23,6 +23,17 @@
 #include "gemm_epi.h"
 
 namespace ah {
+
+// Workgroups splitting K per tile: GemmDesc::splits when above 1, the K range a whole number of stages
+// per split and the device's split-K workspace large enough; else 1.
+int gemm32d_splits(const GemmDesc &d, int bm, int bk) {
+    int sp = d.splits > 16 ? 16 : d.splits;
+    if (sp <= 1 || !d.sk_sync || !d.sk_part) return 1;
+    const long tiles = (long)((d.M + bm - 1) / bm) * ((d.N + bm - 1) / bm);
+    if (tiles > kSplitKMaxTiles || d.K % (bk * sp) || tiles * sp * bm * bm > d.sk_cap) return 1;
+    return sp;
+}
+
 namespace g32 {
 
 // Byte offset of 16-byte chunk c (k = 4c .. 4c+3) of row r in a K-contiguous stage of BK floats per row.
@@ -156,9 +167,12 @@ __global__ __launch_bounds__(256) void gemm32d_kernel(GemmDesc d) {
     Fetch<BM, TB, BK> fb;
     fa.init(d.lda, m0, d.M, wave, lane);
     fb.init(d.ldb, n0, d.N, wave, lane);
-    const char *Ab = (const char *)d.A + (TA == 0 ? (long)m0 * d.lda * 4 : (long)m0 * 4);
-    const char *Bb = (const char *)d.B + (TB == 0 ? (long)n0 * d.ldb * 4 : (long)n0 * 4);
-    const int nk = d.K / BK;
+    // split-K: the gridDim.y workgroups of a tile each contract one K / gridDim.y range (whole stages)
+    const int nsplit = gridDim.y, split = blockIdx.y;
+    const int nk = d.K / BK / nsplit;
+    const long kb = (long)split * nk * BK;
+    const char *Ab = (const char *)d.A + (TA == 0 ? (long)m0 * d.lda * 4 + kb * 4 : (long)m0 * 4 + kb * d.lda * 4);
+    const char *Bb = (const char *)d.B + (TB == 0 ? (long)n0 * d.ldb * 4 + kb * 4 : (long)n0 * 4 + kb * d.ldb * 4);
 
     floatx16 acc[FM][FM], acc2[FM][FM];
 #pragma unroll
@@ -227,13 +241,64 @@ __global__ __launch_bounds__(256) void gemm32d_kernel(GemmDesc d) {
 #pragma unroll
             for (int j = 0; j < FM; j++) acc[i][j] += acc2[i][j];
     }
+    if (nsplit > 1) {
+        // The register-staged kernel's split-K finish: every split stores its partial with 16-byte sc1
+        // buffer stores (written through, coherent across the XCDs' L2s), waits for them, and takes a
+        // ticket from the tile's arrival counter (acquire-release); the split drawing the last ticket adds
+        // all partials in split order (its own from registers), resets the counter and runs the epilogue.
+        // Partial layout: 16-byte chunk c of thread t at byte 16 * (c * 256 + t) of its split.
+        constexpr int NC = FM * FM * 4, PART = NC * 256 * 16, SC1 = 16;
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
+        const int tile = (m0 / BM) * tiles_n + n0 / BM;
+        int *const count = d.sk_sync + 2 * tile;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            d.sk_part + (long)tile * nsplit * (PART / 4), (short)0, nsplit * PART, 0x00020000);
+        __shared__ int ticket;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const floatx16 &a = acc[c / (FM * 4)][(c / 4) % FM];
+            const int e = (c % 4) * 4;
+            const floatx4 v = {a[e], a[e + 1], a[e + 2], a[e + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, split * PART + (c * 256 + tid) * 16, 0, SC1);
+            // wait states before the store's data registers may be rewritten (a compiler-placed VALU write
+            // two instructions behind a 16-byte store has reached memory in kernels of this library)
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 4" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) ticket = ticket_take(count);
+        __syncthreads();
+        if (ticket != nsplit - 1) return;
+#pragma unroll
+        for (int bl = 0; bl < FM * FM; bl++) {
+            floatx16 &a = acc[bl / FM][bl % FM];
+            floatx4 sum[4];
+            for (int q = 0; q < nsplit; q++) {
+                floatx4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (q == split) v[u] = (floatx4){a[4 * u], a[4 * u + 1], a[4 * u + 2], a[4 * u + 3]};
+                    else v[u] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, q * PART + ((bl * 4 + u) * 256 + tid) * 16, 0, SC1));
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) sum[u] = q == 0 ? v[u] : sum[u] + v[u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int x = 0; x < 4; x++) a[4 * u + x] = sum[u][x];
+        }
+        if (tid == 0) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+    }
     epilogue_tile<EPI, float, FM, FM>(d, acc, m0 + wm0, n0 + wn0, lane);
 }
 
 template <int BM, int BK, int NS, int TA, int TB, int EPI>
 static hipError_t launch(const GemmDesc &d, hipStream_t s) {
     const int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm32d_kernel<BM, TA, TB, EPI, BK, NS>), dim3(tiles), dim3(256), 0, s, d);
+    hipLaunchKernelGGL((gemm32d_kernel<BM, TA, TB, EPI, BK, NS>), dim3(tiles, gemm32d_splits(d, BM, BK)), dim3(256), 0, s, d);
     return hipGetLastError();
 }
 

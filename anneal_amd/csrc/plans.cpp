@@ -148,6 +148,8 @@ static const std::vector<F32Cfg> &f32_cfgs() {
                 }
             }
         for (int i = 0; i < kGemm32dConfigs; i++) c.push_back({kGemm32dBase + i, 0, 0});   // direct-to-LDS stages
+        for (int i = 0; i < kGemm32dConfigs; i++)                                           // ... splitting K
+            for (int sp : {2, 4, 8}) c.push_back({kGemm32dBase + i, 0, sp});
         return c;
     }();
     return v;

@@ -187,11 +187,12 @@ int template_gemm(const Params &P, TemplateKernel *t) {
         return set_error(AH_ERR_INVALID, "tmpl gemm: kg=%d needs a tile that admits it", base.kgroups);
     base.splits = (int)P.integer("splits", 0);
     if (base.splits < 0 || base.splits > 16) return set_error(AH_ERR_INVALID, "tmpl gemm: splits=%d (0..16)", base.splits);
-    // dma=i: f32 configuration i of the direct-to-LDS kernel (gemm32d.hip) in place of tile / kg / splits
+    // dma=i: f32 configuration i of the direct-to-LDS kernel (gemm32d.hip) in place of tile / kg (splits
+    // still split K across workgroups)
     const int dma = (int)P.integer("dma", -1);
     if (dma >= 0) {
-        if (dma >= kGemm32dConfigs || base.tile || base.kgroups || base.splits)
-            return set_error(AH_ERR_INVALID, "tmpl gemm: dma=%d (0..%d, without tile, kg or splits)", dma, kGemm32dConfigs - 1);
+        if (dma >= kGemm32dConfigs || base.tile || base.kgroups)
+            return set_error(AH_ERR_INVALID, "tmpl gemm: dma=%d (0..%d, without tile or kg)", dma, kGemm32dConfigs - 1);
         base.tile = kGemm32dBase + dma;
     }
     const bool swap_ab = P.integer("swap_ab", 0) != 0;

@@ -224,12 +224,14 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * tiling and scheduling and accumulate each output over k in the same order (bit-identical results);
  * the k-group variants 10, 11, 15, 25, 28 and 31 add two k-halves, which rounds differently in f32 (relative
  * 1e-6 level). For an f32 contraction (dtype AH_F32) the candidates are the f32 kernel's (tile, k-groups,
- * splits of K across workgroups) configurations and the direct-to-LDS kernel's, 43 in all, and
+ * splits of K across workgroups) configurations and the direct-to-LDS kernel's, 58 in all, and
  * *best_variant is the winner's index: 0 is the shape's automatic choice, then the register-staged
  * kernel's tile 64 and 128 each with k-groups auto / 1 / 2 / 4 (as the tile admits) and splits auto / 1 /
  * 2 / 4 / 8 / 16 in that nesting order (a fixed k-group count takes no automatic split, so splits auto is
  * listed only with k-groups auto), indices 1-37; then the direct-to-LDS configurations 0-4 (tile 64 with
- * k 64 x 3 stages, 64 x 4, 32 x 4; tile 128 with k 32 x 4, 64 x 2), indices 38-42. The automatic choice is
+ * k 64 x 3 stages, 64 x 4, 32 x 4; tile 128 with k 32 x 4, 64 x 2), indices 38-42, then each of those
+ * with K split across 2 / 4 / 8 workgroups (43-57; the partials folded in split order as the
+ * register-staged kernel folds them). The automatic choice is
  * the direct-to-LDS kernel on 64-wide tiles when they number at least 256 (at least 128 for K <= 1024),
  * the register-staged kernel otherwise. Later f32 launches of the shape with tile, k-groups and splits all automatic use the
  * winner. Configurations add K in different orders, so their results differ at the rounding level;

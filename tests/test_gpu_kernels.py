@@ -339,7 +339,8 @@ def test_gemm_f32_split_k(dev, epi, splits):
 
 def test_gemm_f32_tune_and_cache(dev, tmp_path):
     """The tuner over the f32 kernel's (tile, k-groups, splits) configurations: it returns an index into
-    the 43-entry table (38 register-staged, 5 direct-to-LDS), later automatic launches of the shape use
+    the 58-entry table (38 register-staged, 5 direct-to-LDS, those 5 with K split 2 / 4 / 8 ways), later
+    automatic launches of the shape use
     the winner (against float64), and the choice survives the disk cache, where an index past the table
     is rejected."""
     M, N, K = 256, 512, 2048
@@ -350,7 +351,7 @@ def test_gemm_f32_tune_and_cache(dev, tmp_path):
     common = dict(dtype=L.AH_F32, epi=L.EPI_STORE, ta=0, tb=0, M=M, N=N, K=K, A=dA, B=dB, lda=K, ldb=K, C_out=dC,
                   ldc=N)
     best, us = dev.gemm_tune(iterations=2, **common)
-    assert 0 <= best < 43 and us > 0
+    assert 0 <= best < 58 and us > 0
     dev.gemm(**common)
     ref = A.astype(np.float64) @ B.astype(np.float64).T
     assert O.relerr(dC.read().reshape(M, N), ref) < 1e-5
@@ -360,7 +361,7 @@ def test_gemm_f32_tune_and_cache(dev, tmp_path):
     assert f"0/0/0/{M}/{N}/{K} {best}" in lines
     dev.gemm_tune_cache(str(path), False)
     bad = tmp_path / "bad32.txt"
-    bad.write_text(lines[0] + f"\n0/0/0/{M}/{N}/{K} 43\n")
+    bad.write_text(lines[0] + f"\n0/0/0/{M}/{N}/{K} 58\n")
     with pytest.raises(L.AnnealHipError, match="bad line"):
         dev.gemm_tune_cache(str(bad), False)
     for b in (dA, dB, dC):
@@ -416,14 +417,55 @@ def test_gemm_f32_dma_same_bits_as_register_staged(dev, dma, ta, tb, epi):
     assert O.relerr(got, ref) < 1e-5
 
 
+@pytest.mark.parametrize("dma,splits", [(0, 2), (2, 4), (1, 8), (3, 2), (4, 4)])
+@pytest.mark.parametrize("epi", ["store", "mask", "grad"])
+def test_gemm_f32_dma_split_k_same_bits(dev, dma, splits, epi):
+    """The direct-to-LDS kernel splitting K across workgroups folds the partials as the register-staged
+    kernel does (split order, the last arriver's own from registers), so dma=i with splits=s gives the bits
+    of tile=BM with one k-group and s splits; two launches in a row give the same bits and leave the
+    arrival counters at zero (a second launch on other inputs differs)."""
+    from anneal_amd.executor import Buffer, ExecItem, Executor
+    tile = DMA_CFGS[dma][0]
+    M, N, K, ta, tb = (256, 192, 2048, 0, 0) if epi == "store" else (192, 256, 2048, 1, 1)
+    if epi == "mask":
+        ta, tb = 0, 1
+    common = f"tmpl:gemm;dtype=f32;epi={epi};ta={ta};tb={tb};M={M};N={N};K={K}"
+    fallback = tile == 128 and epi in ("mask", "grad")
+    dma_key = common + f";dma={dma};splits={splits}"
+    ref_key = common if fallback else common + f";tile={tile};kg=1;splits={splits}"
+    bufs = [Buffer(10, M * N, [M, N], L.AH_F32), Buffer(1, M * K, [K, M] if ta else [M, K], L.AH_F32),
+            Buffer(2, N * K, [K, N] if tb else [N, K], L.AH_F32)]
+    if epi == "mask":
+        bufs.append(Buffer(3, M * N, [M, N], L.AH_F32))
+    ex = Executor(dev)
+    prev = None
+    for rep in range(2):
+        rng = np.random.default_rng(50 + rep)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K)).astype(np.float32)
+        ins = {1: store_operand(A, ta).ravel(), 2: store_operand(B, tb).ravel()}
+        if epi == "mask":
+            H = rng.standard_normal((M, N)).astype(np.float32)
+            ins[3] = np.where(H < 0, np.float32(-0.0), H).astype(np.float32).ravel()
+        got = ex.run([ExecItem(dma_key, bufs)], ins)[10]
+        again = ex.run([ExecItem(dma_key, bufs)], ins)[10]
+        want = ex.run([ExecItem(ref_key, bufs)], ins)[10]
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
+        if epi == "store":
+            assert O.relerr(got.reshape(M, N), A.astype(np.float64) @ B.astype(np.float64).T) < 1e-5
+        assert prev is None or not np.array_equal(prev, got)
+        prev = got
+
+
 def test_gemm_f32_dma_key_checks(dev):
-    """dma=i is a configuration index, and it excludes tile / kg / splits."""
+    """dma=i is a configuration index, and it excludes tile / kg."""
     from anneal_amd.executor import Buffer, ExecItem, Executor
     bufs = [Buffer(10, 64 * 64, [64, 64], L.AH_F32), Buffer(1, 64 * 64, [64, 64], L.AH_F32),
             Buffer(2, 64 * 64, [64, 64], L.AH_F32)]
     ins = {1: np.ones(64 * 64, np.float32), 2: np.ones(64 * 64, np.float32)}
-    for bad in ("dma=5", "dma=0;tile=64", "dma=1;splits=2"):
-        with pytest.raises(L.AnnealHipError, match="dma"):
+    for bad in ("dma=5", "dma=0;tile=64", "dma=1;kg=2"):
+        with pytest.raises(L.AnnealHipError, match="dma|kg"):
             Executor(dev).run([ExecItem(f"tmpl:gemm;dtype=f32;epi=store;ta=0;tb=0;M=64;N=64;K=64;{bad}", bufs)], ins)
 
 
