@@ -372,18 +372,20 @@ def test_gemm_f32_tune_and_cache(dev, tmp_path):
 DMA_CFGS = [(64, 64, 3), (64, 64, 4), (64, 32, 4), (128, 32, 4), (128, 64, 2)]
 
 
+@pytest.mark.parametrize("shape", [(200, 300, 1024), (36, 20, 128)])
 @pytest.mark.parametrize("dma", range(5))
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("epi", ["store", "bias_relu", "mask", "grad"])
-def test_gemm_f32_dma_same_bits_as_register_staged(dev, dma, ta, tb, epi):
+def test_gemm_f32_dma_same_bits_as_register_staged(dev, dma, ta, tb, epi, shape):
     """The direct-to-LDS f32 kernel adds K in the order of the register-staged kernel with one k-group
     and no split, so each of its configurations gives the same bits as that kernel at the same tile, for
-    every layout and epilogue, on a ragged shape (M, N not multiples of the tile); both against float64.
+    every layout and epilogue, on ragged shapes (M, N not multiples of the tile, down to one tile smaller
+    than the tile); both against float64.
     The 128-wide configurations take only the store and bias epilogues and run the automatic choice for
     the others, which must then match that choice's bits."""
     from anneal_amd.executor import Buffer, ExecItem, Executor
     tile = DMA_CFGS[dma][0]
-    M, N, K = 200, 300, 1024
+    M, N, K = shape
     common = f"tmpl:gemm;dtype=f32;epi={epi};ta={ta};tb={tb};M={M};N={N};K={K}"
     dma_key = common + f";dma={dma}"
     fallback = tile == 128 and epi in ("mask", "grad")
