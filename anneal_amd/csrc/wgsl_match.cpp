@@ -15,7 +15,8 @@
 //                max(load, 0.0), or the ReLU-backward mask prologue select(0.0, adj, z == max(z, 0.0))
 //                (tensor/gradient_ruleset.go:153-161 with ReLU = Maximum(x, 0), tensor/nn/nn.go:111-114);
 //                stored as acc, f16(acc), c*acc, acc + bias[n] (f16: f16(acc) + bias) or
-//                max(acc + bias[n], 0.0)  ->  "tmpl:gemm" with ta/tb, prologues pa/pb and PARAM roles;
+//                max(acc + bias[n], 0.0) (f16: max(f16(acc) + bias, 0.0))  ->  "tmpl:gemm" with ta/tb,
+//                prologues pa/pb and PARAM roles;
 //   reduction    REDUCE(ADD|MAX, load) over the innermost or the outermost axis of a 2-D buffer (or all
 //                of a 1-D one), stored as acc or c*acc into f32  ->  "tmpl:reduce".
 //
@@ -664,9 +665,9 @@ std::string classify(const std::string &src, int64_t n0) {
         scale = (float)(v->a[0]->k == Node::NUM ? v->a[0]->num : v->a[1]->num);
     } else if (bias_sum(v)) {
         epi = "bias";
-    } else if (dt == "f32" && v->k == Node::CALL && v->s == "max" && v->a.size() == 2 &&
+    } else if (v->k == Node::CALL && v->s == "max" && v->a.size() == 2 &&
                (is_zero(v->a[1]) || is_zero(v->a[0])) && bias_sum(is_zero(v->a[1]) ? v->a[0] : v->a[1])) {
-        epi = "bias_relu";
+        epi = "bias_relu";   // f16: max(f16(acc) + bias, 0), the f16 add rounding once as the template's does
     } else {
         return "";
     }

@@ -126,13 +126,17 @@ def test_rendered_step_templates_match_the_plain_rendering(dev, monkeypatch):
         assert O.relerr(fast[k], plain[k]) < 1e-5, k
 
 
-@pytest.mark.parametrize("relu", [False, True])
-def test_selected_f16_contraction_matches_rendering(dev, monkeypatch, relu):
-    """An f16 Linear forward (widened loads, f16(acc) narrowing, f16 bias add) on the f16 MFMA template
-    matches float64 within f16 rounding, and the WGSL rendering to the rounding of f16(acc) and the add."""
+@pytest.mark.parametrize("relu,relu_out", [(False, False), (True, False), (False, True)])
+def test_selected_f16_contraction_matches_rendering(dev, monkeypatch, relu, relu_out):
+    """An f16 Linear forward (widened loads, f16(acc) narrowing, f16 bias add, ReLU on the input or on
+    the output) on the f16 MFMA template matches float64 within f16 rounding, and the WGSL rendering to
+    the rounding of f16(acc) and the add (the template writes a dead unit as -0.0, equal to the
+    rendering's +0.0)."""
+    from anneal_amd import _lib as L
     from anneal_amd.backend import Device
     M, N, K = 256, 128, 192
-    src, bufs, ws, wc, key = WL.f16_linear(M, N, K, bias=True, relu_a=relu)
+    src, bufs, ws, wc, key = WL.f16_linear(M, N, K, bias=True, relu_a=relu, relu_out=relu_out)
+    assert L.wgsl_template_key(src) == key
     rng = np.random.default_rng(11)
     A = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
     W = (rng.standard_normal((N, K)) * 0.1).astype(np.float16).astype(np.float32)
@@ -142,12 +146,14 @@ def test_selected_f16_contraction_matches_rendering(dev, monkeypatch, relu):
     got = Executor(dev).run([item], inp)[30].reshape(M, N)
     Ar = np.maximum(A, 0) if relu else A
     want = (Ar.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float16).astype(np.float64) + b
+    if relu_out:
+        want = np.maximum(want, 0)
     assert np.max(np.abs(got - want)) <= 2e-3 * np.max(np.abs(want))
     monkeypatch.setenv("AH_WGSL_TEMPLATES", "0")
     with Device(0) as d2:
         ref = Executor(d2).run([item], inp)[30].reshape(M, N)
     # f16(acc) may differ by one ulp of the accumulator (summation order), and the f16 bias add rounds once
     # more: one ulp at |acc| plus one at the result
-    acc = np.abs(ref - b).astype(np.float16)
+    acc = np.abs(ref - b).astype(np.float16)   # (with relu_out, an upper bound where the output was clamped)
     ulp = np.abs(np.spacing(acc)).astype(np.float32) + np.abs(np.spacing(ref.astype(np.float16))).astype(np.float32)
     assert np.all(np.abs(got - ref) <= ulp + 1e-7)

@@ -101,10 +101,12 @@ def test_rendered_mlp_ce_step_selects_a_template_or_the_wave_rendering(shape, sy
     assert [n for n, p in plans.items() if p == "thread"] == ["dZ"]
 
 
-@pytest.mark.parametrize("bias,relu", [(True, False), (False, False), (True, True)])
-def test_f16_contraction_with_narrowing_is_selected(bias, relu):
-    """An f16 reduce (loads widened to f32 in the loop, f16(acc) after it) selects the f16 MFMA template."""
-    src, _, _, _, key = WL.f16_linear(256, 128, 192, bias=bias, relu_a=relu)
+@pytest.mark.parametrize("bias,relu,relu_out", [(True, False, False), (False, False, False), (True, True, False),
+                                               (True, False, True), (True, True, True)])
+def test_f16_contraction_with_narrowing_is_selected(bias, relu, relu_out):
+    """An f16 reduce (loads widened to f32 in the loop, f16(acc) after it) selects the f16 MFMA template,
+    with the ReLU as the input's prologue, as the output's epilogue, or both."""
+    src, _, _, _, key = WL.f16_linear(256, 128, 192, bias=bias, relu_a=relu, relu_out=relu_out)
     assert L.wgsl_template_key(src) == key
 
 

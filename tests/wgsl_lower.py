@@ -373,10 +373,12 @@ def mlp_ce_step(B: int, D: int, H: int, C: int, symbolic: bool = False):
     return ks, leaves, outs
 
 
-def f16_linear(M: int, N: int, K: int, bias: bool = True, relu_a: bool = False):
+def f16_linear(M: int, N: int, K: int, bias: bool = True, relu_a: bool = False, relu_out: bool = False):
     """An f16 Linear forward as the lowering renders an f16 reduce: loads widened to f32 inside the loop,
-    f32 accumulation, f16(acc) after it (codegen/lower.go:667-716), the bias add in f16. Returns
-    (wgsl, bufs, ws, wc, expected key)."""
+    f32 accumulation, f16(acc) after it (codegen/lower.go:667-716), the bias add in f16; relu_a applies
+    the ReLU of the previous layer to the loaded input (the consumer-side form), relu_out applies it to
+    this layer's output (max(f16(acc) + b, 0.0h), the producer-side form). Returns (wgsl, bufs, ws, wc,
+    expected key)."""
     k = Kernel([(30, [M, N], F16), (1, [M, K], F16), (2, [N, K], F16)] + ([(3, [N], F16)] if bias else []),
                [M, N], f16=True)
     k.acc()
@@ -388,9 +390,11 @@ def f16_linear(M: int, N: int, K: int, bias: bool = True, relu_a: bool = False):
     k.update(k.let(f"({tx} * {tw})"))
     k.end()
     if bias:
-        k.store(k.let(f"(f16(acc0) + {k.load(3, 'r1', 'f16')})", "f16"))
+        t = k.let(f"(f16(acc0) + {k.load(3, 'r1', 'f16')})", "f16")
+        k.store(k.let(f"max({t}, 0.0h)", "f16") if relu_out else t)
     else:
         k.store("f16(acc0)")
-    key = f"tmpl:gemm;dtype=f16;epi={'bias' if bias else 'store'};ta=0;tb=0;M={M};N={N};K={K}" + (";pa=relu" if relu_a else "")
+    epi = ("bias_relu" if relu_out else "bias") if bias else "store"
+    key = f"tmpl:gemm;dtype=f16;epi={epi};ta=0;tb=0;M={M};N={N};K={K}" + (";pa=relu" if relu_a else "")
     bufs = [(u, int(np.prod(s)), d, list(s)) for u, s, d in k.bufs]
     return k.source(), bufs, tuple(k.ws), tuple(k.wc), key
