@@ -157,3 +157,28 @@ def test_selected_f16_contraction_matches_rendering(dev, monkeypatch, relu, relu
     acc = np.abs(ref - b).astype(np.float16)   # (with relu_out, an upper bound where the output was clamped)
     ulp = np.abs(np.spacing(acc)).astype(np.float32) + np.abs(np.spacing(ref.astype(np.float16))).astype(np.float32)
     assert np.all(np.abs(got - ref) <= ulp + 1e-7)
+
+
+@pytest.mark.parametrize("shape", [(128, 96, 128, 64, 32), (256, 128, 256, 256, 128)])
+def test_rendered_mlp3_step_matches_oracle(dev, shape):
+    """Config 3's step as the reference's rendered kernels (13 WGSL kernels: three f16 Linear layers on the
+    f16 MFMA template with the bias epilogue and the ReLU prologue, the f16 MSE reduce, the loss adjoint,
+    the f32 column sum on the reduce template, the mixed f32 x f16 backward contractions and masked column
+    sums on the wave rendering), run through ah_run: loss and gradients match ora_mlp3_f16_step at the
+    config-3 bar (2e-2; the f16 forward's roundings differ with the summation order)."""
+    B, D0, D1, D2, D3 = shape
+    p = data.mlp3_inputs(B, D0, D1, D2, D3)
+    q = dict(p)
+    q["x"], q["t"] = data.f16_quantize(p["x"]), data.f16_quantize(p["t"])
+    ks, lv, outs = WL.mlp3_step(B, D0, D1, D2, D3)
+    from anneal_amd import _lib as L
+    for name, src, _, _, _, plan in ks:
+        assert L.wgsl_plan(src) == plan, name
+    items = [ExecItem(src, [Buffer(u, n, sh, dtype=dt) for (u, n, dt, sh) in bufs], local_size=ws, workgroup_count=wc)
+             for _, src, bufs, ws, wc, _ in ks]
+    got = Executor(dev).run(items, {lv[k]: q[k].ravel() for k in lv})
+    wl, g, _ = O.mlp3_step(q, 0.0)
+    loss = got[outs["loss"]][0]
+    assert abs(loss - wl) < 2e-2 * abs(wl)
+    for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3"):
+        assert O.relerr(got[outs[k]], g[k].ravel()) < 2e-2, k

@@ -129,3 +129,16 @@ def test_reduce_with_scale_and_scalar_output():
     k.end()
     k.store(k.let("(acc0 * 0.5)"))
     assert L.wgsl_template_key(k.source()) == "tmpl:reduce;op=sum;axis=1;M=1;N=300;scale=0x1p-1"
+
+
+def test_rendered_mlp3_step_selects_templates_for_its_same_type_kernels():
+    """Config 3's rendered step: the three f16 layers select the f16 contraction template (ReLU prologue on
+    the second and third), the output bias gradient the column-sum template; the f32 x f16 backward
+    contractions and the masked column sums keep the wave rendering, the loss adjoint the thread one."""
+    ks, _, _ = WL.mlp3_step(256, 128, 256, 256, 128)
+    plans = {name: L.wgsl_plan(src) for name, src, *_ in ks}
+    for name, src, _, _, _, plan in ks:
+        assert plans[name] == plan, name
+    assert [n for n, p in plans.items() if p.startswith("tmpl:gemm")] == ["fc1", "fc2", "fc3"]
+    assert plans["db3"].startswith("tmpl:reduce") and plans["gP"] == "thread"
+    assert sum(p == "wave" for p in plans.values()) == 8

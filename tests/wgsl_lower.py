@@ -1,5 +1,6 @@
-"""The configs-1/4 training step as the WGSL kernels anneal's codegen renders, for the template-selection
-tests (tests/test_wgsl_select.py, host) and the rendered-step parity test (tests/test_gpu_wgsl.py, GPU).
+"""The configs-1/4 and config-3 training steps as the WGSL kernels anneal's codegen renders, for the
+template-selection tests (tests/test_wgsl_select.py, host) and the rendered-step parity tests
+(tests/test_gpu_wgsl.py, GPU).
 
 TEST INFRASTRUCTURE ONLY. Without a Go toolchain the reference's scheduler cannot be run, so the kernel
 partition is restated from its rules and the text from its lowering, not captured:
@@ -398,3 +399,129 @@ def f16_linear(M: int, N: int, K: int, bias: bool = True, relu_a: bool = False, 
     key = f"tmpl:gemm;dtype=f16;epi={epi};ta=0;tb=0;M={M};N={N};K={K}" + (";pa=relu" if relu_a else "")
     bufs = [(u, int(np.prod(s)), d, list(s)) for u, s, d in k.bufs]
     return k.source(), bufs, tuple(k.ws), tuple(k.wc), key
+
+
+def mlp3_step(B: int, D0: int, D1: int, D2: int, D3: int):
+    """Config 3's step (three f16 Linear layers with ReLU, MSE mean loss, f32 backward) as rendered
+    kernels, following the graph the oracle restates (ora_mlp3_f16_step, oracle/anneal_oracle.c): each
+    forward layer an f16 reduce (widened loads, f32 accumulation, f16(acc)) with the f16 bias add fused
+    after it and the previous layer's ReLU inlined into its loop; loss = f16(Sum((P - t)^2)) * (1/(B*D3))
+    as one f16 reduce over both axes; the loss adjoint gP = s*d + s*d with d = f16(P - t), materialised
+    for its three readers; the backward contractions in f32 (an f32 adjoint times an f16 weight or
+    activation promotes to f32, tensor/ops.go:74-79), the ReLU masks Where(z == max(z, 0), adj, 0)
+    inlined into the contractions and column sums that read the adjoint. Returns (kernels, leaves,
+    outputs) like mlp_ce_step. The mixed f32 x f16 contractions have no template (an MFMA takes one
+    operand type) and take the wave-per-output rendering."""
+    s = f32_lit(1.0 / (B * D3))
+    leaves = dict(x=1, t=2, W1=3, b1=4, W2=5, b2=6, W3=7, b3=8)
+    uZ1, uZ2, uP, uloss, ugP, udb3, udW3, udH2, udb2, udW2, udH1, udb1, udW1 = range(10, 23)
+    ks = []
+
+    def add(name, k, plan):
+        ks.append((name, k.source(), [(u, int(np.prod(sh)), dt, list(sh)) for u, sh, dt in k.bufs], tuple(k.ws),
+                   tuple(k.wc), plan))
+
+    def linear(name, out, xin, xdim, w, b, n, relu_in):
+        k = Kernel([(out, [B, n], F16), (xin, [B, xdim], F16), (w, [n, xdim], F16), (b, [n], F16)], [B, n], f16=True)
+        k.acc()
+        r2 = k.loop(xdim)
+        tx = k.load(1, k.idx2("r0", xdim, r2), widen=True)
+        if relu_in:
+            tx = k.let(f"max({tx}, 0.0)")
+        tw = k.load(2, f"(r1 * {xdim}) + {r2}", widen=True)
+        k.update(k.let(f"({tx} * {tw})"))
+        k.end()
+        k.store(k.let(f"(f16(acc0) + {k.load(3, 'r1', 'f16')})", "f16"))
+        add(name, k, f"tmpl:gemm;dtype=f16;epi=bias;ta=0;tb=0;M={B};N={n};K={xdim}" + (";pa=relu" if relu_in else ""))
+
+    linear("fc1", uZ1, 1, D0, 3, 4, D1, False)
+    linear("fc2", uZ2, uZ1, D1, 5, 6, D2, True)
+    linear("fc3", uP, uZ2, D2, 7, 8, D3, True)
+
+    # loss = f16(Sum((P - t)^2)) * s: an f16 reduce over both axes, the f32 constant promoting after it
+    k = Kernel([(uloss, [1], F32), (uP, [B, D3], F16), (2, [B, D3], F16)], [], f16=True)
+    k.acc()
+    r0 = k.loop(B)
+    r1 = k.loop(D3)
+    tp = k.load(1, k.idx2(r0, D3, r1), widen=True)
+    tt = k.load(2, k.idx2(r0, D3, r1), widen=True)
+    d = k.let(f"({tp} - {tt})")
+    k.update(k.let(f"({d} * {d})"))
+    k.end()
+    k.end()
+    k.store(k.let(f"(f32({k.let('f16(acc0)', 'f16')}) * {s})"))
+    add("loss", k, "wave")
+
+    # gP = s*d + s*d, d = f16(P - t): elementwise, materialised for db3, dW3 and dH2
+    k = Kernel([(ugP, [B, D3], F32), (uP, [B, D3], F16), (2, [B, D3], F16)], [B, D3], f16=True)
+    i = k.idx2("r0", D3, "r1")
+    d = k.let(f"({k.load(1, i, 'f16')} - {k.load(2, i, 'f16')})", "f16")
+    sd = k.let(f"(f32({d}) * {s})")
+    k.store(k.let(f"({sd} + {sd})"))
+    add("gP", k, "thread")
+
+    def colsum(name, out, n, adj, zbuf=None):
+        # Sum over the batch of the adjoint, masked by the ReLU of z when given
+        bufs = [(out, [n], F32), (adj, [B, n], F32)] + ([(zbuf, [B, n], F16)] if zbuf else [])
+        k = Kernel(bufs, [n], f16=zbuf is not None)
+        k.acc()
+        r1 = k.loop(B)
+        a = k.load(1, k.idx2(r1, n, "r0"))
+        if zbuf:
+            z = k.load(2, f"({r1} * {n}) + r0", widen=True)
+            eq = k.let(f"({z} == {k.let(f'max({z}, 0.0)')})", "bool")
+            a = k.let(f"select(0.0, {a}, {eq})")
+        k.update(a)
+        k.end()
+        k.store("acc0")
+        add(name, k, f"tmpl:reduce;op=sum;axis=0;M={B};N={n}" if zbuf is None else "wave")
+
+    def masked_adj(k, adj, zbuf, r, n, col):
+        # Where(z == max(z, 0), adj, 0) at (r, col) of [B, n], z an f16 activation widened
+        z = k.load(zbuf, f"({r} * {n}) + {col}", widen=True)
+        eq = k.let(f"({z} == {k.let(f'max({z}, 0.0)')})", "bool")
+        return k.let(f"select(0.0, {k.load(adj, k.idx2(r, n, col))}, {eq})")
+
+    def dweight(name, out, m, n, adj, zmask, act, relu_act):
+        # dW[m, n] = Sum_b adj'[b, m] * act'[b, n]: adj' the (masked) f32 adjoint, act' the f16 input (ReLU'd)
+        bufs = [(out, [m, n], F32), (adj, [B, m], F32), (act, [B, n], F16)] + ([(zmask, [B, m], F16)] if zmask else [])
+        k = Kernel(bufs, [m, n], f16=True)
+        k.acc()
+        r2 = k.loop(B)
+        a = masked_adj(k, 1, 3, r2, m, "r0") if zmask else k.load(1, k.idx2(r2, m, "r0"))
+        x = k.load(2, f"({r2} * {n}) + r1", widen=True)
+        if relu_act:
+            x = k.let(f"max({x}, 0.0)")
+        k.update(k.let(f"({a} * {x})"))
+        k.end()
+        k.store("acc0")
+        add(name, k, "wave")
+
+    def dinput(name, out, n, m, adj, zmask, w):
+        # dX[b, n] = Sum_j adj'[b, j] * W[j, n]: the f32 adjoint (masked) times the f16 weight
+        bufs = [(out, [B, n], F32), (adj, [B, m], F32), (w, [m, n], F16)] + ([(zmask, [B, m], F16)] if zmask else [])
+        k = Kernel(bufs, [B, n], f16=True)
+        k.acc()
+        r2 = k.loop(m)
+        if zmask:
+            z = k.load(3, f"(r0 * {m}) + {r2}", widen=True)
+            eq = k.let(f"({z} == {k.let(f'max({z}, 0.0)')})", "bool")
+            a = k.let(f"select(0.0, {k.load(1, k.idx2('r0', m, r2))}, {eq})")
+        else:
+            a = k.load(1, k.idx2("r0", m, r2))
+        wv = k.load(2, k.idx2(r2, n, "r1"), widen=True)
+        k.update(k.let(f"({a} * {wv})"))
+        k.end()
+        k.store("acc0")
+        add(name, k, "wave")
+
+    colsum("db3", udb3, D3, ugP)
+    dweight("dW3", udW3, D3, D2, ugP, None, uZ2, True)
+    dinput("dH2", udH2, D2, D3, ugP, None, 7)
+    colsum("db2", udb2, D2, udH2, uZ2)
+    dweight("dW2", udW2, D2, D1, udH2, uZ2, uZ1, True)
+    dinput("dH1", udH1, D1, D2, udH2, uZ2, 5)
+    colsum("db1", udb1, D1, udH1, uZ1)
+    dweight("dW1", udW1, D1, D0, udH1, uZ1, 1, False)
+    outs = dict(loss=uloss, dW1=udW1, db1=udb1, dW2=udW2, db2=udb2, dW3=udW3, db3=udb3)
+    return ks, leaves, outs
