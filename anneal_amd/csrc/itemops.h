@@ -12,6 +12,11 @@ hipError_t zero_fill(void *p, long bytes, hipStream_t s);
 // Contraction operand prologues: dst = z ? Where(z == max(z, 0), src, 0) : max(src, 0), n elements of f32
 // (or f16 when f16 is set).
 hipError_t operand_prologue(const void *src, const void *z, bool f16, long n, void *dst, hipStream_t s);
+// The same prologues into an f32 operand from sources of mixed types (an f16 activation or weight
+// widened into an f32 contraction): kind 1 ReLU, 2 ReLU-backward mask (z >= 0 keeps src), 3 widening
+// only; src_f16 / z_f16 give the stored types. Widening is exact.
+hipError_t operand_prologue_f32(const void *src, bool src_f16, const void *z, bool z_f16, int kind, long n, float *dst,
+                                hipStream_t s);
 // *differs (zeroed first) becomes 1 when any of the `words` 32-bit words of a and b differ.
 hipError_t words_differ(const void *a, const void *b, long words, int *differs, hipStream_t s);
 // out[m] = scale * reduce_n G[m, n] (scale not applied to max); G is f32, or f16 when f16 is set, and the

@@ -44,6 +44,18 @@ __global__ void operand_prologue_kernel(const T *src, const T *z, long n, T *dst
     }
 }
 
+template <typename TS, typename TZ>
+__global__ void operand_prologue_f32_kernel(const TS *src, const TZ *z, int kind, long n, float *dst) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        const float v = (float)src[i];
+        if (kind == 2) dst[i] = (float)z[i] >= 0.0f ? v : 0.0f;
+        else if (kind == 1) dst[i] = v > 0.0f ? v : 0.0f;
+        else dst[i] = v;
+    }
+}
+
 // ── reductions over a row-major [M, N] f32 matrix ──────────────────────────────────────────────────
 __device__ __forceinline__ float red_init(int op) { return op == RED_MAX ? -FLT_MAX : 0.0f; }
 __device__ __forceinline__ float red_step(int op, float acc, float v) {
@@ -239,6 +251,22 @@ hipError_t operand_prologue(const void *src, const void *z, bool f16, long n, vo
     else
         hipLaunchKernelGGL(operand_prologue_kernel<float>, dim3(grid_of(n, 256, 8192)), dim3(256), 0, s, (const float *)src,
                            (const float *)z, n, (float *)dst);
+    return hipGetLastError();
+}
+
+hipError_t operand_prologue_f32(const void *src, bool src_f16, const void *z, bool z_f16, int kind, long n, float *dst,
+                                hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (kind < 1 || kind > 3 || (kind == 2 && !z)) return hipErrorInvalidValue;
+    const dim3 grid(grid_of(n, 256, 8192)), block(256);
+    if (src_f16 && z_f16)
+        hipLaunchKernelGGL((operand_prologue_f32_kernel<half_t, half_t>), grid, block, 0, s, (const half_t *)src, (const half_t *)z, kind, n, dst);
+    else if (src_f16)
+        hipLaunchKernelGGL((operand_prologue_f32_kernel<half_t, float>), grid, block, 0, s, (const half_t *)src, (const float *)z, kind, n, dst);
+    else if (z_f16)
+        hipLaunchKernelGGL((operand_prologue_f32_kernel<float, half_t>), grid, block, 0, s, (const float *)src, (const half_t *)z, kind, n, dst);
+    else
+        hipLaunchKernelGGL((operand_prologue_f32_kernel<float, float>), grid, block, 0, s, (const float *)src, (const float *)z, kind, n, dst);
     return hipGetLastError();
 }
 

@@ -135,13 +135,16 @@ int ensure_ws(TemplateKernel *t, int64_t bytes) {
 
 // ── gemm ─────────────────────────────────────────────────────────────────────────────────────────
 // "tmpl:gemm;dtype=f16|f32;epi=...;ta=0|1;tb=0|1;M=..;N=..;K=..[;scale=s][;lr=l][;variant=v][;tile=t;kg=g]
-//  [;splits=s][;dma=i][;swap_ab=1][;in_a=i;in_b=j;in_bias=k][;pa=relu|mask;za=z][;pb=relu|mask;zb=z]"
+//  [;splits=s][;dma=i][;swap_ab=1][;wa=1][;wb=1][;wza=1][;wzb=1][;in_a=i;in_b=j;in_bias=k][;pa=relu|mask;za=z][;pb=relu|mask;zb=z]"
 // swap_ab: A is the second input PARAM and B the first; in_a / in_b / in_bias name the PARAM of each role
 // outright (a rendered kernel binds its inputs in the scheduler's order). Operand prologues, the
 // elementwise ops the reference's scheduler inlines into a contraction's loop: pa=relu reads max(A, 0)
 // (ReLU = Maximum(x, 0), tensor/nn/nn.go:111-114), pa=mask reads Where(Z == max(Z, 0), A, 0) with Z the
 // PARAM za (the ReLU backward rule, tensor/gradient_ruleset.go:153-161); pb/zb likewise for B. A
 // prologue is applied in one elementwise pass into the template's workspace before the MFMA kernel.
+// wa / wb (dtype f32 only): operand A / B is stored f16 and widened to f32 by that pass (alone, or with
+// its prologue); wza / wzb: the mask prologue's Z is stored f16. These are the reference's mixed
+// contractions, an f32 adjoint times an f16 weight or activation (tensor/ops.go:74-79).
 // variant picks an f16 kernel variant, tile (64/128/256) and kg (k-groups) the f32 tiled kernel's shape.
 // M, N and K may be symbolic. PARAMs by epilogue:
 //   store      C, A, B                     C = scale*acc
@@ -202,9 +205,18 @@ int template_gemm(const Params &P, TemplateKernel *t) {
     static const std::map<std::string, int> pros = {{"", 0}, {"relu", 1}, {"mask", 2}};
     auto pa_it = pros.find(P.str("pa", "")), pb_it = pros.find(P.str("pb", ""));
     if (pa_it == pros.end() || pb_it == pros.end()) return set_error(AH_ERR_UNSUPPORTED, "tmpl gemm: prologue must be relu or mask");
-    const int proA = pa_it->second, proB = pb_it->second;
+    int proA = pa_it->second, proB = pb_it->second;
     const int pZa = proA == 2 ? (int)P.integer("za", -1) : -1, pZb = proB == 2 ? (int)P.integer("zb", -1) : -1;
     if ((proA == 2 && pZa < 1) || (proB == 2 && pZb < 1)) return set_error(AH_ERR_INVALID, "tmpl gemm: a mask prologue names its Z PARAM (za/zb)");
+    // wa / wb: the operand is stored f16 and widened into an f32 contraction (an f32 adjoint times an f16
+    // weight or activation, tensor/ops.go:74-79); wza / wzb: the mask source is stored f16
+    const bool wa = P.integer("wa", 0) != 0, wb = P.integer("wb", 0) != 0;
+    const bool wza = P.integer("wza", 0) != 0, wzb = P.integer("wzb", 0) != 0;
+    if ((wa || wb || wza || wzb) && base.dtype != GEMM_F32) return set_error(AH_ERR_INVALID, "tmpl gemm: wa/wb/wza/wzb widen into an f32 contraction");
+    if ((wza && proA != 2) || (wzb && proB != 2)) return set_error(AH_ERR_INVALID, "tmpl gemm: wza/wzb need a mask prologue");
+    if (wa && proA == 0) proA = 3;   // widening alone
+    if (wb && proB == 0) proB = 3;
+    const bool mixed = wa || wb || wza || wzb;
     if ((proA || proB) && (base.epi == EPI_MSE || base.epi == EPI_MASK || base.epi == EPI_SGD))
         return set_error(AH_ERR_UNSUPPORTED, "tmpl gemm: prologues with the store/bias/bias_relu/grad epilogues");
     if (pA < 1 || pB < 1 || pA == pB) return set_error(AH_ERR_INVALID, "tmpl gemm: in_a/in_b must name two input PARAMs");
@@ -221,14 +233,14 @@ int template_gemm(const Params &P, TemplateKernel *t) {
     };
     if (proA || proB)
         t->workspace = [ws_layout](int64_t sv) -> int64_t { int64_t ob; return ws_layout(sv, &ob); };
-    t->bytes = [base, M, N, K, grad, pA, pB, pBias, pZa, pZb, nbuf, es](int64_t sv) -> std::vector<int64_t> {
+    t->bytes = [base, M, N, K, grad, pA, pB, pBias, pZa, pZb, nbuf, es, wa, wb, wza, wzb](int64_t sv) -> std::vector<int64_t> {
         const int64_t m = M.with(sv), n = N.with(sv), k = K.with(sv);
         std::vector<int64_t> b(nbuf, 0);
         b[0] = m * n * ((base.epi == EPI_SGD || grad) ? 4 : es);
-        b[pA] = m * k * es;
-        b[pB] = n * k * es;
-        if (pZa > 0) b[pZa] = m * k * es;
-        if (pZb > 0) b[pZb] = n * k * es;
+        b[pA] = m * k * (wa ? 2 : es);
+        b[pB] = n * k * (wb ? 2 : es);
+        if (pZa > 0) b[pZa] = m * k * (wza ? 2 : es);
+        if (pZb > 0) b[pZb] = n * k * (wzb ? 2 : es);
         switch (base.epi) {
         case EPI_BIAS: case EPI_BIAS_RELU: b[pBias] = n * es; break;
         case EPI_MASK: b[3] = m * n * es; break;
@@ -239,7 +251,7 @@ int template_gemm(const Params &P, TemplateKernel *t) {
         return b;
     };
     const std::string key = t->key;
-    t->run = [base, M, N, K, nbuf, grad, key, pA, pB, pBias, proA, proB, pZa, pZb, ws_layout](
+    t->run = [base, M, N, K, nbuf, grad, key, pA, pB, pBias, proA, proB, pZa, pZb, ws_layout, mixed, wa, wb, wza, wzb](
                  ah_device *d, TemplateKernel *self, void *const *ptrs, int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
         if (int rc = need(key.c_str(), n_ptrs, nbuf)) return rc;
         GemmDesc g = base;
@@ -261,12 +273,14 @@ int template_gemm(const Params &P, TemplateKernel *t) {
             const bool f16 = base.dtype == GEMM_F16;
             if (proA) {
                 void *dst = self->ws;
-                AH_HIP(operand_prologue(ptrs[pA], proA == 2 ? ptrs[pZa] : nullptr, f16, m * k, dst, d->stream));
+                if (mixed) AH_HIP(operand_prologue_f32(ptrs[pA], wa, proA == 2 ? ptrs[pZa] : nullptr, wza, proA, m * k, (float *)dst, d->stream));
+                else AH_HIP(operand_prologue(ptrs[pA], proA == 2 ? ptrs[pZa] : nullptr, f16, m * k, dst, d->stream));
                 g.A = dst;
             }
             if (proB) {
                 void *dst = (char *)self->ws + offB;
-                AH_HIP(operand_prologue(ptrs[pB], proB == 2 ? ptrs[pZb] : nullptr, f16, n * k, dst, d->stream));
+                if (mixed) AH_HIP(operand_prologue_f32(ptrs[pB], wb, proB == 2 ? ptrs[pZb] : nullptr, wzb, proB, n * k, (float *)dst, d->stream));
+                else AH_HIP(operand_prologue(ptrs[pB], proB == 2 ? ptrs[pZb] : nullptr, f16, n * k, dst, d->stream));
                 g.B = dst;
             }
         }

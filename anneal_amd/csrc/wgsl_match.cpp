@@ -11,7 +11,8 @@
 // after it as `f16(accI)`, and one store `data0[(u32(r0) * S) + u32(r1)] = v;`. The matcher parses that
 // body, substitutes every let into the expression tree it names, and recognises two families:
 //
-//   contraction  REDUCE(ADD, MUL(opA, opB)) over one loop, where an operand is a load, a ReLU prologue
+//   contraction  REDUCE(ADD, MUL(opA, opB)) over one loop (f32, f16, or f32 with f16 operands widened in
+//                the loop, which the key marks wa / wb / wza / wzb), where an operand is a load, a ReLU prologue
 //                max(load, 0.0), or the ReLU-backward mask prologue select(0.0, adj, z == max(z, 0.0))
 //                (tensor/gradient_ruleset.go:153-161 with ReLU = Maximum(x, 0), tensor/nn/nn.go:111-114);
 //                stored as acc, f16(acc), c*acc, acc + bias[n] (f16: f16(acc) + bias) or
@@ -468,7 +469,7 @@ struct Operand {
     int buf = -1, zbuf = -1;
     P idx, zidx;
     int pro = 0;       // 0 none, 1 relu, 2 mask
-    bool widened = false;
+    bool widened = false, zwidened = false;
 };
 
 P unwiden(const P &n, bool *w) {
@@ -500,7 +501,7 @@ bool operand(const P &x0, Operand *o) {
         P adj = unwiden(x->a[1], &w2), c = x->a[2];
         if (adj->k != Node::LOAD || c->k != Node::BIN || c->s != "==") return false;
         P z = c->a[0], m = c->a[1];
-        if (z->k == Node::CALL) std::swap(z, m);
+        if (z->k == Node::CALL && z->s == "max") std::swap(z, m);
         bool w3 = false, w4 = false;
         z = unwiden(z, &w3);
         if (z->k != Node::LOAD || m->k != Node::CALL || m->s != "max" || m->a.size() != 2) return false;
@@ -509,7 +510,7 @@ bool operand(const P &x0, Operand *o) {
         mz = unwiden(mz, &w4);
         if (!is_zero(m0) || !same(mz, z)) return false;
         o->buf = adj->buf; o->idx = adj->a[0]; o->widened = w2;
-        o->zbuf = z->buf; o->zidx = z->a[0]; o->pro = 2;
+        o->zbuf = z->buf; o->zidx = z->a[0]; o->pro = 2; o->zwidened = w3 && w4;
         return true;
     }
     return false;
@@ -625,20 +626,33 @@ std::string classify(const std::string &src, int64_t n0) {
             std::vector<int64_t> cz, cd;
             if (!affine(o->zidx, vn, rg, &cz) || !affine(o->idx, vn, rg, &cd) || cz != cd) return "";
         }
-    // operand dtypes: all f32, or all f16 widened in the loop (an f16 reduce, codegen/lower.go:667-716)
-    std::string dt;
+    // operand dtypes: all f16 widened in the loop (an f16 reduce, codegen/lower.go:667-716), or an f32
+    // contraction whose f16 operands (and mask sources) are widened in the loop (an f32 adjoint times an
+    // f16 weight or activation, the promotion of tensor/ops.go:74-79): those get the wa/wb/wza/wzb flags
+    bool any32 = false;
     for (const Operand *o : {&A, &B}) {
         const int bufs[2] = {o->buf, o->zbuf};
         for (int b : bufs) {
             if (b < 0) continue;
             if (b < 1 || b >= nb) return "";
-            const std::string t = k.btype[b];
-            if (dt.empty()) dt = t;
-            if (t != dt) return "";
+            const std::string &t = k.btype[b];
+            if (t != "f32" && t != "f16") return "";
+            any32 |= t == "f32";
         }
-        if (o->widened != (dt == "f16")) return "";
     }
-    if (dt != "f32" && dt != "f16") return "";
+    const std::string dt = any32 ? "f32" : "f16";
+    bool wflag[2] = {false, false}, wzflag[2] = {false, false};
+    for (int r = 0; r < 2; r++) {
+        const Operand *o = r == 0 ? &A : &B;
+        const bool f16buf = k.btype[o->buf] == "f16";
+        if (o->widened != f16buf) return "";   // an f16 load is widened, an f32 one is not
+        wflag[r] = any32 && f16buf;
+        if (o->zbuf >= 0) {
+            const bool f16z = k.btype[o->zbuf] == "f16";
+            if (o->zwidened != f16z) return "";
+            wzflag[r] = any32 && f16z;
+        }
+    }
     // epilogue
     std::string epi = "store";
     float scale = 1.0f;
@@ -689,6 +703,10 @@ std::string classify(const std::string &src, int64_t n0) {
     static const char *pro[] = {"", "relu", "mask"};
     if (A.pro) key += std::string(";pa=") + pro[A.pro];
     if (B.pro) key += std::string(";pb=") + pro[B.pro];
+    if (wflag[0]) key += ";wa=1";
+    if (wflag[1]) key += ";wb=1";
+    if (wzflag[0]) key += ";wza=1";
+    if (wzflag[1]) key += ";wzb=1";
     // PARAM roles: the default order (A, B, bias) or the two operands swapped is written as before
     // (swap_ab=1); any other order names each role's PARAM
     const bool plain = A.zbuf < 0 && B.zbuf < 0 && (bias < 0 || bias == 3);

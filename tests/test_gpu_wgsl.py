@@ -163,9 +163,9 @@ def test_selected_f16_contraction_matches_rendering(dev, monkeypatch, relu, relu
 def test_rendered_mlp3_step_matches_oracle(dev, shape):
     """Config 3's step as the reference's rendered kernels (13 WGSL kernels: three f16 Linear layers on the
     f16 MFMA template with the bias epilogue and the ReLU prologue, the f16 MSE reduce, the loss adjoint,
-    the f32 column sum on the reduce template, the mixed f32 x f16 backward contractions and masked column
-    sums on the wave rendering), run through ah_run: loss and gradients match ora_mlp3_f16_step at the
-    config-3 bar (2e-2; the f16 forward's roundings differ with the summation order)."""
+    the f32 column sum on the reduce template, the mixed f32 x f16 backward contractions on the f32 template
+    with widening prologues, the masked column sums on the wave rendering), run through ah_run: loss and
+    gradients match ora_mlp3_f16_step at the config-3 bar (2e-2; the f16 forward's roundings differ with the summation order)."""
     B, D0, D1, D2, D3 = shape
     p = data.mlp3_inputs(B, D0, D1, D2, D3)
     q = dict(p)
@@ -182,3 +182,29 @@ def test_rendered_mlp3_step_matches_oracle(dev, shape):
     assert abs(loss - wl) < 2e-2 * abs(wl)
     for k in ("dW1", "db1", "dW2", "db2", "dW3", "db3"):
         assert O.relerr(got[outs[k]], g[k].ravel()) < 2e-2, k
+
+
+@pytest.mark.parametrize("name", ["dW3", "dH2", "dW2", "dH1", "dW1"])
+def test_selected_mixed_type_contraction_matches_rendering(dev, monkeypatch, name):
+    """Each f32 x f16 backward contraction of config 3's rendered step, alone on random inputs, runs the f32
+    template with its f16 operand (and the f16 pre-activation its mask reads) widened by a prologue: the
+    output matches float64 and the wave rendering (selection off) at the f32 reduction bar (1e-5 of the
+    output's scale; widening f16 -> f32 is exact, so only the summation order differs)."""
+    from anneal_amd import _lib as L
+    from anneal_amd.backend import Device
+    ks, _, _ = WL.mlp3_step(192, 96, 160, 128, 64)
+    _, src, bufs, ws, wc, plan = next(k for k in ks if k[0] == name)
+    assert L.wgsl_plan(src) == plan and plan.startswith("tmpl:gemm;dtype=f32")
+    rng = np.random.default_rng(len(name) * 7 + ord(name[-1]))
+    inp = {}
+    for u, n, dt, sh in bufs[1:]:
+        v = rng.standard_normal(n).astype(np.float32)
+        inp[u] = v.astype(np.float16).astype(np.float32) if dt == L.AH_F16 else v
+    item = ExecItem(src, [Buffer(u, n, sh, dtype=dt) for (u, n, dt, sh) in bufs], local_size=ws, workgroup_count=wc)
+    out = bufs[0][0]
+    got = Executor(dev).run([item], inp)[out]
+    monkeypatch.setenv("AH_WGSL_TEMPLATES", "0")
+    with Device(0) as d2:
+        ref = Executor(d2).run([item], inp)[out]
+    scale = np.abs(ref).max()
+    assert scale > 0 and np.abs(got - ref).max() / scale < 1e-5

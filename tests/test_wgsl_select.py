@@ -131,14 +131,26 @@ def test_reduce_with_scale_and_scalar_output():
     assert L.wgsl_template_key(k.source()) == "tmpl:reduce;op=sum;axis=1;M=1;N=300;scale=0x1p-1"
 
 
-def test_rendered_mlp3_step_selects_templates_for_its_same_type_kernels():
+def test_rendered_mlp3_step_selects_templates():
     """Config 3's rendered step: the three f16 layers select the f16 contraction template (ReLU prologue on
-    the second and third), the output bias gradient the column-sum template; the f32 x f16 backward
-    contractions and the masked column sums keep the wave rendering, the loss adjoint the thread one."""
+    the second and third); the five f32 x f16 backward contractions the f32 template with their f16
+    operands and mask sources widened (wa/wb/wza); the output bias gradient the column-sum template; the
+    loss and the masked column sums keep the wave rendering, the loss adjoint the thread one."""
     ks, _, _ = WL.mlp3_step(256, 128, 256, 256, 128)
     plans = {name: L.wgsl_plan(src) for name, src, *_ in ks}
     for name, src, _, _, _, plan in ks:
         assert plans[name] == plan, name
-    assert [n for n, p in plans.items() if p.startswith("tmpl:gemm")] == ["fc1", "fc2", "fc3"]
+    assert [n for n, p in plans.items() if p.startswith("tmpl:gemm;dtype=f16")] == ["fc1", "fc2", "fc3"]
+    assert [n for n, p in plans.items() if p.startswith("tmpl:gemm;dtype=f32")] == ["dW3", "dH2", "dW2", "dH1", "dW1"]
     assert plans["db3"].startswith("tmpl:reduce") and plans["gP"] == "thread"
-    assert sum(p == "wave" for p in plans.values()) == 8
+    assert sorted(n for n, p in plans.items() if p == "wave") == ["db1", "db2", "loss"]
+
+
+def test_mixed_type_contraction_needs_widened_f16_loads():
+    """An f32 x f16 contraction selects the f32 template only when the f16 operand is widened in the loop
+    (f32(load)), as the lowering writes every f16 load inside an f32 reduce."""
+    ks, _, _ = WL.mlp3_step(64, 32, 48, 40, 24)
+    src = dict((n, s) for n, s, *_ in ks)["dH2"]
+    assert L.wgsl_template_key(src).endswith(";wb=1")
+    raw = src.replace("f32(data2[", "(data2[")
+    assert raw != src and L.wgsl_template_key(raw) == ""

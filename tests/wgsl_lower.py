@@ -410,8 +410,8 @@ def mlp3_step(B: int, D0: int, D1: int, D2: int, D3: int):
     for its three readers; the backward contractions in f32 (an f32 adjoint times an f16 weight or
     activation promotes to f32, tensor/ops.go:74-79), the ReLU masks Where(z == max(z, 0), adj, 0)
     inlined into the contractions and column sums that read the adjoint. Returns (kernels, leaves,
-    outputs) like mlp_ce_step. The mixed f32 x f16 contractions have no template (an MFMA takes one
-    operand type) and take the wave-per-output rendering."""
+    outputs) like mlp_ce_step. The mixed f32 x f16 contractions select the f32 template with their f16
+    operands (and mask sources) widened by a prologue (wa / wb / wza keys)."""
     s = f32_lit(1.0 / (B * D3))
     leaves = dict(x=1, t=2, W1=3, b1=4, W2=5, b2=6, W3=7, b3=8)
     uZ1, uZ2, uP, uloss, ugP, udb3, udW3, udH2, udb2, udW2, udH1, udb1, udW1 = range(10, 23)
@@ -495,7 +495,9 @@ def mlp3_step(B: int, D0: int, D1: int, D2: int, D3: int):
         k.update(k.let(f"({a} * {x})"))
         k.end()
         k.store("acc0")
-        add(name, k, "wave")
+        key = f"tmpl:gemm;dtype=f32;epi=store;ta=1;tb=1;M={m};N={n};K={B}"
+        key += (";pa=mask" if zmask else "") + (";pb=relu" if relu_act else "") + ";wb=1"
+        add(name, k, key + (";wza=1;in_a=1;in_b=2;za=3" if zmask else ""))
 
     def dinput(name, out, n, m, adj, zmask, w):
         # dX[b, n] = Sum_j adj'[b, j] * W[j, n]: the f32 adjoint (masked) times the f16 weight
@@ -513,7 +515,8 @@ def mlp3_step(B: int, D0: int, D1: int, D2: int, D3: int):
         k.update(k.let(f"({a} * {wv})"))
         k.end()
         k.store("acc0")
-        add(name, k, "wave")
+        key = f"tmpl:gemm;dtype=f32;epi=store;ta=0;tb=1;M={B};N={n};K={m}" + (";pa=mask" if zmask else "") + ";wb=1"
+        add(name, k, key + (";wza=1;in_a=1;in_b=2;za=3" if zmask else ""))
 
     colsum("db3", udb3, D3, ugP)
     dweight("dW3", udW3, D3, D2, ugP, None, uZ2, True)
