@@ -68,7 +68,7 @@ class ah_beam_result(C.Structure):
                 ("n_opts", C.c_int32), ("opts", ah_opt * 8)]
 
 
-OPT_IDENTITY, OPT_LOCAL, OPT_TILE, OPT_UPCAST, OPT_VECTORIZE, OPT_GROUP, OPT_SCHEDULE = range(7)
+OPT_IDENTITY, OPT_LOCAL, OPT_TILE, OPT_UPCAST, OPT_VECTORIZE, OPT_GROUP, OPT_SCHEDULE, OPT_MFMA = range(8)
 
 # name -> (restype, argtypes)
 _P = C.c_void_p

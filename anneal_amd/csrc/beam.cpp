@@ -74,13 +74,13 @@ long geti(const std::unordered_map<std::string, std::string> &kv, const char *k,
 
 // The lowest-numbered variant with these parameters; fetch 0 means "compiler-scheduled" (modes 0-3, any
 // cross-barrier setting), 4-7 an asm-issued mode with the cross-barrier prefetch; ns 0 means any number
-// of stages in flight (only TILE fixes it).
+// of stages in flight (only TILE fixes it); mi is the MFMA shape (32 unless an MFMA opt sets 16).
 int f16_variant_of(const G16Params &p) {
     for (int v = 1; v <= kGemm16Variants; v++) {
         G16Params q;
         if (!gemm16_variant_params(v, &q)) continue;
         if (q.bm != p.bm || q.bn != p.bn || q.wvm != p.wvm || q.wvn != p.wvn || q.bk != p.bk || q.kg != p.kg ||
-            (p.ns && q.ns != p.ns))
+            (p.ns && q.ns != p.ns) || q.mi != p.mi)
             continue;
         if (p.fetch == 0 ? q.fetch <= 3 : (q.fetch == p.fetch && q.xb == 1)) return v;
     }
@@ -170,6 +170,10 @@ bool apply_opt(Knobs &k, const ah_opt &o) {
             if (o.axis != 0 || o.arg < 5 || o.arg > 7) return false;
             p.fetch = o.arg; p.xb = 1;
             return true;
+        case AH_OPT_MFMA:
+            if (o.axis != 2 || (o.arg != 16 && o.arg != 32)) return false;
+            p.mi = o.arg;
+            return true;
         default: return false;
         }
     }
@@ -231,7 +235,7 @@ std::string emit_key(const KeyInfo &ki, const Knobs &k) {
     return out;
 }
 
-// Every Opt the search may try (the reference's argument lists, beam.go:41-47, plus GROUP and SCHEDULE).
+// Every Opt the search may try (the reference's argument lists, beam.go:41-47, plus GROUP, SCHEDULE and MFMA).
 std::vector<ah_opt> all_opts() {
     std::vector<ah_opt> v;
     for (int axis = 0; axis < 4; axis++) {
@@ -241,6 +245,7 @@ std::vector<ah_opt> all_opts() {
         v.push_back({AH_OPT_VECTORIZE, axis, 4});
         for (int a : {2, 4}) v.push_back({AH_OPT_GROUP, axis, a});
         for (int a : {5, 6, 7}) v.push_back({AH_OPT_SCHEDULE, axis, a});
+        for (int a : {16, 32}) v.push_back({AH_OPT_MFMA, axis, a});
     }
     return v;
 }

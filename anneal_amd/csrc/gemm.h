@@ -14,7 +14,7 @@
 namespace ah {
 
 // Number of f16 kernel variants (table Var<V> in gemm16_kernel.h); variant 0 means the tuned choice.
-constexpr int kGemm16Variants = 31;
+constexpr int kGemm16Variants = 39;
 // Split-K workspace of a device: counters for up to kSplitKMaxTiles tiles, then kSplitKPartFloats floats.
 constexpr int kSplitKMaxTiles = 4096;
 constexpr long kSplitKPartFloats = 4L << 20;
@@ -102,7 +102,7 @@ bool gemm16_try_launch(const GemmDesc &d, hipStream_t s, hipError_t *err);
 // Template parameters of an f16 variant (table Var<V> in gemm16_kernel.h): tile BM x BN, wave layout
 // WVM x WVN, k per LDS stage BK, stages in flight NS, fetch mode, cross-barrier prefetch XB, k-groups KG.
 struct G16Params {
-    int bm, bn, wvm, wvn, bk, ns, fetch, xb, kg;
+    int bm, bn, wvm, wvn, bk, ns, fetch, xb, kg, mi;   // mi: MFMA shape, 32 (32x32x16) or 16 (16x16x32)
 };
 bool gemm16_variant_params(int variant, G16Params *out);
 // The variant an f16 contraction with variant 0 and no tuned choice runs (chosen by shape).

@@ -11,6 +11,8 @@ AH_G16_DECL(14) AH_G16_DECL(15) AH_G16_DECL(16) AH_G16_DECL(17) AH_G16_DECL(18) 
 AH_G16_DECL(20) AH_G16_DECL(21) AH_G16_DECL(22) AH_G16_DECL(23) AH_G16_DECL(24) AH_G16_DECL(25)
 AH_G16_DECL(26) AH_G16_DECL(27) AH_G16_DECL(28)
 AH_G16_DECL(29) AH_G16_DECL(30) AH_G16_DECL(31)
+AH_G16_DECL(32) AH_G16_DECL(33) AH_G16_DECL(34) AH_G16_DECL(35) AH_G16_DECL(36) AH_G16_DECL(37)
+AH_G16_DECL(38) AH_G16_DECL(39)
 #undef AH_G16_DECL
 
 namespace {
@@ -22,7 +24,9 @@ const VariantFn kVariants[g16::kMaxVariant + 1] = {
     gemm16_variant_16, gemm16_variant_17, gemm16_variant_18, gemm16_variant_19, gemm16_variant_20,
     gemm16_variant_21, gemm16_variant_22, gemm16_variant_23, gemm16_variant_24, gemm16_variant_25,
     gemm16_variant_26, gemm16_variant_27, gemm16_variant_28,
-    gemm16_variant_29, gemm16_variant_30, gemm16_variant_31};
+    gemm16_variant_29, gemm16_variant_30, gemm16_variant_31, gemm16_variant_32, gemm16_variant_33,
+    gemm16_variant_34, gemm16_variant_35, gemm16_variant_36, gemm16_variant_37, gemm16_variant_38,
+    gemm16_variant_39};
 
 // k-groups of the variant (the K split must give each group whole 64-wide stages)
 int variant_kgroups(int v) {
@@ -34,6 +38,8 @@ int variant_kgroups(int v) {
         AH_G16_KG(20) AH_G16_KG(21) AH_G16_KG(22) AH_G16_KG(23) AH_G16_KG(24) AH_G16_KG(25)
         AH_G16_KG(26) AH_G16_KG(27) AH_G16_KG(28)
         AH_G16_KG(29) AH_G16_KG(30) AH_G16_KG(31)
+        AH_G16_KG(32) AH_G16_KG(33) AH_G16_KG(34) AH_G16_KG(35) AH_G16_KG(36) AH_G16_KG(37)
+        AH_G16_KG(38) AH_G16_KG(39)
 #undef AH_G16_KG
         default: return 1;
     }
@@ -45,13 +51,14 @@ bool gemm16_variant_params(int v, G16Params *out) {
 #define AH_G16_P(n)                                                                                          \
     case n:                                                                                                  \
         *out = {g16::Var<n>::BM, g16::Var<n>::BM, g16::Var<n>::WVM, g16::Var<n>::WVN, g16::Var<n>::BK,     \
-                g16::Var<n>::NS, g16::Var<n>::FETCH, g16::Var<n>::XB ? 1 : 0, g16::Var<n>::KG};            \
+                g16::Var<n>::NS, g16::Var<n>::FETCH, g16::Var<n>::XB ? 1 : 0, g16::Var<n>::KG, g16::Var<n>::MI};            \
         return true;
         AH_G16_P(1) AH_G16_P(2) AH_G16_P(3) AH_G16_P(4) AH_G16_P(5) AH_G16_P(6) AH_G16_P(7)
         AH_G16_P(8) AH_G16_P(9) AH_G16_P(10) AH_G16_P(11) AH_G16_P(12) AH_G16_P(13)
         AH_G16_P(14) AH_G16_P(15) AH_G16_P(16) AH_G16_P(17) AH_G16_P(18) AH_G16_P(19)
         AH_G16_P(20) AH_G16_P(21) AH_G16_P(22) AH_G16_P(23) AH_G16_P(24) AH_G16_P(25)
         AH_G16_P(26) AH_G16_P(27) AH_G16_P(28) AH_G16_P(29) AH_G16_P(30) AH_G16_P(31)
+        AH_G16_P(32) AH_G16_P(33) AH_G16_P(34) AH_G16_P(35) AH_G16_P(36) AH_G16_P(37) AH_G16_P(38) AH_G16_P(39)
 #undef AH_G16_P
         default: return false;
     }

@@ -17,6 +17,7 @@
 // Each variant (a parameter set of the template, table Var<V> at the end) is instantiated in its own
 // translation unit (gemm16_var.hip) so that the variants compile in parallel.
 #pragma once
+#include <type_traits>
 #include "ah_common.h"
 #include "gemm.h"
 #include "gemm_epi.h"
@@ -37,10 +38,14 @@ __device__ __forceinline__ int koff(int r, int c) {
     return q * 256 + ((((r % SR) * CH + c) ^ (q & 15)) << 4);
 }
 
-// Byte offset of element (k-row k, column m) in an MN-contiguous tile of R columns.
+// Byte offset of element (k-row k, column m) in an MN-contiguous tile of R columns: 32-byte segments
+// XOR-swizzled by 2*(k & 3) + ((k >> 3) & 1). The first term spreads the four k-rows one transposing
+// read covers over the banks; the second separates k-rows 8 apart, which the 16x16 fragments' lane
+// groups read together.
+__device__ __forceinline__ int mn_swz(int k) { return ((k & 3) << 1) ^ ((k >> 3) & 1); }
 template <int R>
 __device__ __forceinline__ int mnoff(int k, int m) {
-    return k * (R * 2) + (((m >> 4) ^ ((k & 3) << 1)) << 5) + ((m & 15) << 1);
+    return k * (R * 2) + (((m >> 4) ^ mn_swz(k)) << 5) + ((m & 15) << 1);
 }
 
 // One 16-byte-per-lane global->LDS DMA issued from inline asm: the compiler's wait-count model does
@@ -92,7 +97,7 @@ struct Fetch {
                 constexpr int ROWS = 512 / R;                 // k-rows per block
                 const int kk = b * ROWS + (16 * lane) / (2 * R);
                 const int pos16 = ((16 * lane) % (2 * R)) / 16;
-                const int seg = (pos16 >> 1) ^ ((kk & 3) << 1);
+                const int seg = (pos16 >> 1) ^ mn_swz(kk);
                 const int m = min(r0 + seg * 16 + (pos16 & 1) * 8, rmax - 8);
                 off[j] = (uint32_t)(((long)kk * ld + m) * 2);
             }
@@ -143,6 +148,24 @@ __device__ __forceinline__ h8 frag(const char *tile, int r, int s, int lane) {
         const int g = lane >> 4, j = lane & 15;
         const int m = r + 16 * (g & 1) + 4 * (j & 3);
         const int k = 16 * s + 8 * (g >> 1) + (j >> 2);
+        s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(tile + mnoff<R>(k, m)));
+        s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(tile + mnoff<R>(k + 4, m)));
+        typedef short s8 __attribute__((ext_vector_type(8)));
+        s8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        return __builtin_bit_cast(h8, v);
+    }
+}
+
+// Fragment of a 16x16x32 MFMA: lane l holds rows r + l%16, k = 32*s + 8*(l/16) .. +7 (the same
+// eight-halves-per-lane form as frag, over 16 rows and 32 k).
+template <int R, int T, int BK>
+__device__ __forceinline__ h8 frag16(const char *tile, int r, int s, int lane) {
+    if constexpr (T == 0) {
+        return *(const h8 *)(tile + koff<BK>(r + (lane & 15), 4 * s + (lane >> 4)));
+    } else {
+        const int g = lane >> 4, j = lane & 15;
+        const int m = r + 4 * (j & 3);
+        const int k = 32 * s + 8 * g + (j >> 2);
         s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(tile + mnoff<R>(k, m)));
         s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(tile + mnoff<R>(k + 4, m)));
         typedef short s8 __attribute__((ext_vector_type(8)));
@@ -213,14 +236,20 @@ __device__ __forceinline__ void g16_tile_origin(int L, int tiles_m, int tiles_n,
 // One output tile at (m0, n0) over k in [kbase, kbase + klen), then fold.run (single k-group) and
 // the epilogue. smem holds G16Smem<...>::SMEM bytes.
 template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG,
-          class Fold, bool HL = false>
+          class Fold, bool HL = false, int MI = 32>
 __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, int n0, long kbase, int klen,
                                          const Fold &fold) {
     using SM = G16Smem<BM, BN, BK, NS, WVM, WVN, FETCH, KG>;
     constexpr int NW = WVM * WVN;
     constexpr int WM = BM / WVM, WN = BN / WVN, FM = WM / 32, FN = WN / 32;
     constexpr int ABYTES = BM * BK * 2, STAGE = SM::STAGE;
-    constexpr int KS = BK / 16;                                           // MFMA k-steps per stage
+    // MI: the MFMA shape, 32 (32x32x16) or 16 (16x16x32). A k-step is one MFMA's k; fragments are
+    // 32 or 16 rows, FA of A and FB of B per k-step, FA*FB MFMAs per k-step.
+    static_assert(MI == 32 || MI == 16, "MFMA shape 32x32x16 or 16x16x32");
+    constexpr int KS = MI == 32 ? BK / 16 : BK / 32;                      // MFMA k-steps per stage
+    constexpr int FA = MI == 32 ? FM : 2 * FM, FB = MI == 32 ? FN : 2 * FN;
+    static_assert(!XB || KS % 2 == 0, "cross-barrier prefetch opens the next stage in fragment slot 0");
+    static_assert(VEPI || MI == 32, "MI 16 tiles use the LDS-staged epilogue");
     constexpr int PERSTAGE = Fetch<BM, TA, BK, NW>::PER + Fetch<BN, TB, BK, NW>::PER;
     constexpr int SMEM0 = SM::SMEM0, SMEMG = SM::SMEMG;
     static_assert(WN % 64 == 0, "the LDS epilogue works in 64-column slabs");
@@ -266,11 +295,29 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
         else return Bb;
     };
 
-    floatx16 acc[FM][FN];
+    // 32x32 accumulator blocks (MI 32) or 16x16 ones (MI 16); the epilogue reads either through
+    // AccView as FM x FN 32x32 blocks
+    floatx16 acc[MI == 32 ? FM : 1][MI == 32 ? FN : 1];
+    floatx4 acc4[MI == 16 ? FA : 1][MI == 16 ? FB : 1];
+    if constexpr (MI == 32) {
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
+            for (int j = 0; j < FN; j++) acc[i][j] = (floatx16){};
+    } else {
+#pragma unroll
+        for (int i = 0; i < FA; i++)
+#pragma unroll
+            for (int j = 0; j < FB; j++) acc4[i][j] = (floatx4){};
+    }
+    auto fragA = [&](const char *t, int i, int ks) -> h8 {
+        if constexpr (MI == 32) return frag<BM, TA, BK>(t, wm0 + i * 32, ks, lane);
+        else return frag16<BM, TA, BK>(t, wm0 + i * 16, ks, lane);
+    };
+    auto fragB = [&](const char *t, int j, int ks) -> h8 {
+        if constexpr (MI == 32) return frag<BN, TB, BK>(t, wn0 + j * 32, ks, lane);
+        else return frag16<BN, TB, BK>(t, wn0 + j * 16, ks, lane);
+    };
 
     static_assert(FETCH != 3 || (BK == 64 && 64 * NW == 2 * BM && BM == BN), "prefetch mapping: one line per thread");
     const char *junk = gsm + SMEM0 + wave * 256;
@@ -322,14 +369,14 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    h8 a[2][FM], b[2][FN];
+    h8 a[2][FA], b[2][FB];
     if constexpr (XB) {
         stage_wait();
         issue_grouped(0, true);
 #pragma unroll
-        for (int i = 0; i < FM; i++) a[0][i] = frag<BM, TA, BK>(gsm, wm0 + i * 32, 0, lane);
+        for (int i = 0; i < FA; i++) a[0][i] = fragA(gsm, i, 0);
 #pragma unroll
-        for (int j = 0; j < FN; j++) b[0][j] = frag<BN, TB, BK>(gsm + ABYTES, wn0 + j * 32, 0, lane);
+        for (int j = 0; j < FB; j++) b[0][j] = fragB(gsm + ABYTES, j, 0);
     }
     for (int kt = 0; kt < nkt; kt++) {
         const char *sa = gsm + (kt % NS) * STAGE, *sb = sa + ABYTES;
@@ -339,16 +386,16 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
             stage_wait();
             if constexpr (FETCH >= 2) issue_grouped(kt);
 #pragma unroll
-            for (int i = 0; i < FM; i++) a[0][i] = frag<BM, TA, BK>(sa, wm0 + i * 32, 0, lane);
+            for (int i = 0; i < FA; i++) a[0][i] = fragA(sa, i, 0);
 #pragma unroll
-            for (int j = 0; j < FN; j++) b[0][j] = frag<BN, TB, BK>(sb, wn0 + j * 32, 0, lane);
+            for (int j = 0; j < FB; j++) b[0][j] = fragB(sb, j, 0);
         }
         // Scheduling fences fix the issue order: the LDS reads of k-step s+1 go out as a group ahead
         // of the MFMAs of k-step s (their latency hides behind the MFMAs); the stage fetches are
         // spread evenly between the MFMAs (issued back to back they fill the vector-memory queue
         // and stall MFMA issue); MFMAs of different k-steps, which share accumulators, never mix.
         __builtin_amdgcn_sched_barrier(0);
-        constexpr int NM = FM * FN;
+        constexpr int NM = FA * FB;
         constexpr int PA = Fetch<BM, TA, BK, NW>::PER;
         constexpr int FPS = (PERSTAGE + KS - 1) / KS;                      // fetches per k-step
         constexpr bool SPREAD = FETCH == 1;
@@ -362,9 +409,9 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
             if (s + 1 < KS) {
                 if constexpr (FETCH >= 6) __builtin_amdgcn_sched_barrier(0);   // one region per k-step
 #pragma unroll
-                for (int i = 0; i < FM; i++) a[n][i] = frag<BM, TA, BK>(sa, wm0 + i * 32, s + 1, lane);
+                for (int i = 0; i < FA; i++) a[n][i] = fragA(sa, i, s + 1);
 #pragma unroll
-                for (int j = 0; j < FN; j++) b[n][j] = frag<BN, TB, BK>(sb, wn0 + j * 32, s + 1, lane);
+                for (int j = 0; j < FB; j++) b[n][j] = fragB(sb, j, s + 1);
                 if constexpr (FETCH < 6) __builtin_amdgcn_sched_barrier(0);
             } else if constexpr (XB) {
                 // Open stage kt+1 now (KS is even, so its first fragments go to slot n = 0). In the
@@ -375,9 +422,9 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
                 issue_grouped(kt + 1);
                 const char *sa1 = gsm + ((kt + 1) % NS) * STAGE, *sb1 = sa1 + ABYTES;
 #pragma unroll
-                for (int i = 0; i < FM; i++) a[n][i] = frag<BM, TA, BK>(sa1, wm0 + i * 32, 0, lane);
+                for (int i = 0; i < FA; i++) a[n][i] = fragA(sa1, i, 0);
 #pragma unroll
-                for (int j = 0; j < FN; j++) b[n][j] = frag<BN, TB, BK>(sb1, wn0 + j * 32, 0, lane);
+                for (int j = 0; j < FB; j++) b[n][j] = fragB(sb1, j, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // mode 5: the refill of stage kt's buffer with stage kt+NS, one DMA after every MPD MFMAs
@@ -388,7 +435,10 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
             const int kr = min(kt + NS, nkt - 1) * BK;
 #pragma unroll
             for (int t = 0; t < NM; t++) {
-                acc[t / FN][t % FN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][t / FN], b[c][t % FN], acc[t / FN][t % FN], 0, 0, 0);
+                if constexpr (MI == 32)
+                    acc[t / FN][t % FN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][t / FN], b[c][t % FN], acc[t / FN][t % FN], 0, 0, 0);
+                else
+                    acc4[t / FB][t % FB] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][t / FB], b[c][t % FB], acc4[t / FB][t % FB], 0, 0, 0);
                 if constexpr (FETCH >= 5) {
                     if (s == KS - 1 && t % MPD == MPD - 1) {
 #pragma unroll
@@ -411,7 +461,7 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
                 if (s + 1 < KS) {
                     // ds reads of k-step s+1 spread evenly: one after every NM/NR MFMAs (or RPM after
                     // each MFMA when there are more reads than MFMAs)
-                    constexpr int NR = (TA ? 2 : 1) * FM + (TB ? 2 : 1) * FN;
+                    constexpr int NR = (TA ? 2 : 1) * FA + (TB ? 2 : 1) * FB;
                     constexpr int RPM = (NR + NM - 1) / NM;
                     constexpr int MPR = NR >= NM ? 1 : NM / NR;
                     constexpr int NG = (NR + RPM - 1) / RPM;
@@ -427,7 +477,7 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
                 if (s + 1 < KS) {
                     // ds reads of k-step s+1 (two per fragment for the transposing read): RPM after
                     // each of the first MFMAs, then the rest of the MFMAs
-                    constexpr int NR = (TA ? 2 : 1) * FM + (TB ? 2 : 1) * FN;
+                    constexpr int NR = (TA ? 2 : 1) * FA + (TB ? 2 : 1) * FB;
                     constexpr int RPM = (NR + NM - 1) / NM;
                     constexpr int NMR = (NR + RPM - 1) / RPM;
 #pragma unroll
@@ -443,8 +493,17 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // drain the tail re-fetches before LDS reuse
 
     const int mb = m0 + wm0, nb = n0 + wn0;
+    // element r of lane l of 32x32 block (i, j) of the accumulators, for either MFMA shape
+    auto accv = [&](int i, int j, int r) -> float {
+        if constexpr (MI == 32) return acc[i][j][r];
+        else return AccView16<FM, FN>{acc4}(i, j, r);
+    };
     if constexpr (KG == 1) {
-        if (!fold.template run<FM, FN, 64 * NW>(acc, tid)) return;
+        if constexpr (MI == 32) {
+            if (!fold.template run<FM, FN, 64 * NW>(acc, tid)) return;
+        } else {
+            static_assert(std::is_same<Fold, G16NoFold>::value, "MI 16 tiles have no split-K fold");
+        }
     }
     if constexpr (KG > 1) {
         // The two k-groups split the finish: group g owns 32-row block g of each wave tile (which has
@@ -459,7 +518,7 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
         for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {   // hand over the block the other group owns
-                const float v = kg == 0 ? acc[1][j][r] : acc[0][j][r];
+                const float v = kg == 0 ? accv(1, j, r) : accv(0, j, r);
                 red[(((1 - kg) * FN + j) * 16 + r) * 64] = v;
             }
         __syncthreads();
@@ -470,12 +529,12 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
         for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float own = kg == 0 ? acc[0][j][r] : acc[1][j][r];
+                const float own = kg == 0 ? accv(0, j, r) : accv(1, j, r);
                 mine[0][j][r] = own + red[((kg * FN + j) * 16 + r) * 64];
             }
         __syncthreads();   // the epilogue below reuses this LDS
         if constexpr (VEPI)
-            epilogue_lds<EPI, half_t, 1, FN>(d, mine, mb + kg * 32, nb, lane, smem + (kg * NW + wave) * (32 * 256));
+            epilogue_lds<EPI, half_t, 1, FN, MI>(d, mine, mb + kg * 32, nb, lane, smem + (kg * NW + wave) * (32 * 256));
         else
             epilogue_tile<EPI, half_t, 1, FN>(d, mine, mb + kg * 32, nb, lane);
         return;
@@ -483,14 +542,15 @@ __device__ __forceinline__ void g16_tile(const GemmDesc &d, char *smem, int m0, 
     if constexpr (VEPI) {
         // Epilogue through the (now idle) operand LDS: each wave owns FM*32 rows x 64 f32 columns.
         __syncthreads();
-        epilogue_lds<EPI, half_t, FM, FN>(d, acc, mb, nb, lane, smem + wave * (WM * 256));
+        if constexpr (MI == 32) epilogue_lds<EPI, half_t, FM, FN>(d, acc, mb, nb, lane, smem + wave * (WM * 256));
+        else epilogue_lds_view<EPI, half_t, FM, FN, 16>(d, AccView16<FM, FN>{acc4}, mb, nb, lane, smem + wave * (WM * 256));
     } else {
         epilogue_tile<EPI, half_t, FM, FN>(d, acc, mb, nb, lane);
     }
 }
 
 template <int BM, int BN, int TA, int TB, int EPI, bool VEPI, int BK, int NS, int WVM, int WVN, int FETCH, bool XB, int KG,
-          bool HL = false>
+          bool HL = false, int MI = 32>
 __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d) {
     __shared__ __attribute__((aligned(1024))) char smem[G16Smem<BM, BN, BK, NS, WVM, WVN, FETCH, KG>::SMEM];
     const int tiles_n = (d.N + BN - 1) / BN;
@@ -500,7 +560,7 @@ __global__ __launch_bounds__(64 * WVM * WVN * KG) void gemm16_kernel(GemmDesc d)
     if ((ntiles & 7) == 0) L = (L & 7) * (ntiles >> 3) + (L >> 3);   // contiguous tile runs per XCD
     int m0, n0;
     g16_tile_origin(L, tiles_m, tiles_n, BM, BN, m0, n0);
-    g16_tile<BM, BN, TA, TB, EPI, VEPI, BK, NS, WVM, WVN, FETCH, XB, KG, G16NoFold, HL>(d, smem, m0, n0, 0, d.K, G16NoFold{});
+    g16_tile<BM, BN, TA, TB, EPI, VEPI, BK, NS, WVM, WVN, FETCH, XB, KG, G16NoFold, HL, MI>(d, smem, m0, n0, 0, d.K, G16NoFold{});
 }
 
 template <int T>
@@ -511,14 +571,16 @@ static bool operand_ok(const void *p, long ld, int rows) {
     return (rows % 8) == 0;
 }
 
-template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, bool XB, int KG, int TA, int TB, int EPI, bool HL = false>
+// MI 16 variants have only the LDS-staged epilogue: a tile that needs the per-element one runs the
+// variant's MI 32 form.
+template <int BM, int WVM, int WVN, int BK, int NS, int FETCH, bool XB, int KG, int TA, int TB, int EPI, bool HL = false, int MI = 32>
 static hipError_t launch(const GemmDesc &d, hipStream_t s) {
     int tiles = ((d.M + BM - 1) / BM) * ((d.N + BM - 1) / BM);
     const uintptr_t a = (uintptr_t)d.C | (uintptr_t)d.aux | (uintptr_t)d.bias | (uintptr_t)d.W32 |
                         (uintptr_t)d.W16 | (uintptr_t)d.gout | (uintptr_t)d.C2;
     const bool vepi = d.M % BM == 0 && d.N % BM == 0 && d.ldc % 4 == 0 && d.ldaux % 4 == 0 && (a & 15) == 0;
     constexpr int NT = 64 * WVM * WVN * KG;
-    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH, XB, KG, HL>), dim3(tiles), dim3(NT), 0, s, d);
+    if (vepi) hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, true, BK, NS, WVM, WVN, FETCH, XB, KG, HL, MI>), dim3(tiles), dim3(NT), 0, s, d);
     else hipLaunchKernelGGL((gemm16_kernel<BM, BM, TA, TB, EPI, false, BK, NS, WVM, WVN, FETCH, XB, KG, HL>), dim3(tiles), dim3(NT), 0, s, d);
     return hipGetLastError();
 }
@@ -526,11 +588,13 @@ static hipError_t launch(const GemmDesc &d, hipStream_t s) {
 // Variants (GemmDesc::variant): tile BM (square), wave layout WVM x WVN, k per stage BK, stages in
 // flight NS, fetch mode, cross-barrier prefetch XB, k-groups KG.
 template <int V> struct Var;
-#define AH_G16_VAR(V, BM_, WVM_, WVN_, BK_, NS_, FETCH_, XB_, KG_)                                      \
+#define AH_G16_VARM(V, BM_, WVM_, WVN_, BK_, NS_, FETCH_, XB_, KG_, MI_)                               \
     template <> struct Var<V> {                                                                      \
         static constexpr int BM = BM_, WVM = WVM_, WVN = WVN_, BK = BK_, NS = NS_, FETCH = FETCH_, KG = KG_; \
+        static constexpr int MI = MI_;                                                               \
         static constexpr bool XB = XB_;                                                              \
     };
+#define AH_G16_VAR(V, BM_, WVM_, WVN_, BK_, NS_, FETCH_, XB_, KG_) AH_G16_VARM(V, BM_, WVM_, WVN_, BK_, NS_, FETCH_, XB_, KG_, 32)
 AH_G16_VAR(1, 128, 2, 2, 64, 2, 0, false, 1)
 AH_G16_VAR(2, 256, 2, 2, 64, 2, 1, false, 1)   // one wave per SIMD
 AH_G16_VAR(3, 256, 4, 2, 64, 2, 1, false, 1)   // two waves per SIMD, 64x128 per wave
@@ -562,8 +626,19 @@ AH_G16_VAR(28, 128, 2, 2, 64, 2, 6, true, 2)
 AH_G16_VAR(29, 256, 2, 2, 64, 2, 7, true, 1)
 AH_G16_VAR(30, 256, 4, 2, 64, 2, 7, true, 1)
 AH_G16_VAR(31, 128, 2, 2, 64, 2, 7, true, 2)
+// 16x16x32 MFMAs (MI 16): under sustained load on varied data the 16x16x32 instruction sustains more
+// of its nominal rate than 32x32x16 before the power limit lowers the clock
+AH_G16_VARM(32, 256, 4, 2, 64, 2, 6, true, 1, 16)
+AH_G16_VARM(33, 256, 4, 2, 64, 2, 7, true, 1, 16)
+AH_G16_VARM(34, 256, 4, 2, 64, 2, 4, true, 1, 16)
+AH_G16_VARM(35, 128, 2, 2, 64, 2, 5, true, 2, 16)
+AH_G16_VARM(36, 128, 2, 2, 64, 2, 4, true, 2, 16)
+AH_G16_VARM(37, 128, 2, 2, 64, 2, 7, true, 2, 16)
+AH_G16_VARM(38, 128, 2, 2, 64, 2, 6, true, 2, 16)
+AH_G16_VARM(39, 256, 4, 2, 64, 2, 5, true, 1, 16)
 #undef AH_G16_VAR
-constexpr int kMaxVariant = 31;
+#undef AH_G16_VARM
+constexpr int kMaxVariant = 39;
 
 template <int V, int TA, int TB>
 static hipError_t run_epi(const GemmDesc &d, hipStream_t s) {
@@ -573,14 +648,14 @@ static hipError_t run_epi(const GemmDesc &d, hipStream_t s) {
         // dX with the ReLU mask (A K-contiguous, B MN-contiguous) and dW with the SGD update (both
         // MN-contiguous)
         if constexpr (TA == 0 && TB == 1) {
-            if (d.epi == EPI_MASK) return launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, 0, 1, EPI_MASK, true>(d, s);
+            if (d.epi == EPI_MASK) return launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, 0, 1, EPI_MASK, true, P::MI>(d, s);
         }
         if constexpr (TA == 1 && TB == 1) {
-            if (d.epi == EPI_SGD) return launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, 1, 1, EPI_SGD, true>(d, s);
+            if (d.epi == EPI_SGD) return launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, 1, 1, EPI_SGD, true, P::MI>(d, s);
         }
         return hipErrorInvalidValue;
     }
-#define AH_G16_L(E) launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, TA, TB, E>(d, s)
+#define AH_G16_L(E) launch<P::BM, P::WVM, P::WVN, P::BK, P::NS, P::FETCH, P::XB, P::KG, TA, TB, E, false, P::MI>(d, s)
     switch (d.epi) {
         case EPI_STORE: return AH_G16_L(EPI_STORE);
         case EPI_BIAS: return AH_G16_L(EPI_BIAS);

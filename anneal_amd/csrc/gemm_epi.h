@@ -127,7 +127,27 @@ __device__ __forceinline__ void epilogue_tile(const GemmDesc &d, const floatx16 
 template <typename T>
 struct Vec4 { typedef T type __attribute__((ext_vector_type(4))); };
 
-__device__ __forceinline__ int epi_lds_off(int row, int col) { return row * 256 + ((col ^ ((row & 4) << 3)) << 2); }
+// MI 32: the 32x32 accumulator layout's two row groups of one write are rows 4 apart, so bit 2 of the
+// row swaps the halves. MI 16: the four row groups of a 16x16 layout's write are rows 4 apart, so bits
+// 2-3 of the row rotate 16-column quarters.
+template <int MI = 32>
+__device__ __forceinline__ int epi_lds_off(int row, int col) {
+    if constexpr (MI == 32) return row * 256 + ((col ^ ((row & 4) << 3)) << 2);
+    else return row * 256 + ((col ^ (((row >> 2) & 3) << 4)) << 2);
+}
+// Row / column in its 32x32 block of element r of lane l of a wave's accumulators: MI 32 is the
+// MFMA's own layout; MI 16 holds the block as four 16x16 MFMA blocks, quarter r/4 (row half, column
+// half), element r%4 of lane l at row 4*(l/16) + r%4, column l%16 of the quarter.
+template <int MI>
+__device__ __forceinline__ int acc_row_mi(int r, int lane) {
+    if constexpr (MI == 32) return acc_row(r, lane);
+    else return 16 * (r >> 3) + 4 * (lane >> 4) + (r & 3);
+}
+template <int MI>
+__device__ __forceinline__ int acc_col_mi(int r, int lane) {
+    if constexpr (MI == 32) return lane & 31;
+    else return 16 * ((r >> 2) & 1) + (lane & 15);
+}
 
 template <int EPI, typename T>
 __device__ __forceinline__ floatx4 epi_in4(const GemmDesc &d, long m, int n) {
@@ -138,9 +158,31 @@ __device__ __forceinline__ floatx4 epi_in4(const GemmDesc &d, long m, int n) {
     } else return (floatx4){};
 }
 
-template <int EPI, typename T, int FM, int FN>
+// A wave's accumulators as FM x FN 32x32 blocks, element r of lane l of block (i, j): AccView32 over
+// 32x32 MFMA blocks, AccView16 over 16x16 ones (block (i, j) is 16x16 blocks 2i..2i+1 x 2j..2j+1,
+// quarter r/8 by row, (r/4)%2 by column, element r%4 of each; acc_row_mi<16> / acc_col_mi<16>).
+template <int FM, int FN>
+struct AccView32 {
+    const floatx16 (&a)[FM][FN];
+    __device__ __forceinline__ float operator()(int i, int j, int r) const { return a[i][j][r]; }
+};
+template <int FM, int FN>
+struct AccView16 {
+    const floatx4 (&a)[2 * FM][2 * FN];
+    __device__ __forceinline__ float operator()(int i, int j, int r) const { return a[2 * i + (r >> 3)][2 * j + ((r >> 2) & 1)][r & 3]; }
+};
+
+template <int EPI, typename T, int FM, int FN, int MI, class View>
+__device__ __forceinline__ void epilogue_lds_view(const GemmDesc &d, const View &acc, int mb, int nb, int lane, char *wlds);
+
+template <int EPI, typename T, int FM, int FN, int MI = 32>
 __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (&acc)[FM][FN], int mb, int nb, int lane,
                                              char *wlds) {
+    epilogue_lds_view<EPI, T, FM, FN, MI>(d, AccView32<FM, FN>{acc}, mb, nb, lane, wlds);
+}
+
+template <int EPI, typename T, int FM, int FN, int MI, class View>
+__device__ __forceinline__ void epilogue_lds_view(const GemmDesc &d, const View &acc, int mb, int nb, int lane, char *wlds) {
     constexpr int ROWS = FM * 32;
     constexpr int G = EPI == EPI_MSE ? 4 : 8;   // row groups whose inputs are loaded together
     typedef typename Vec4<T>::type T4;
@@ -176,7 +218,8 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
             for (int jj = 0; jj < 2; jj++)
 #pragma unroll
                 for (int r = 0; r < 16; r++)
-                    *(float *)(wlds + epi_lds_off(i * 32 + acc_row(r, lane), jj * 32 + (lane & 31))) = acc[i][2 * jp + jj][r];
+                    *(float *)(wlds + epi_lds_off<MI>(i * 32 + acc_row_mi<MI>(r, lane), jj * 32 + acc_col_mi<MI>(r, lane))) =
+                        acc(i, 2 * jp + jj, r);
         __builtin_amdgcn_s_waitcnt(0xc07f);     // lgkmcnt(0): this wave's LDS writes have landed
         __builtin_amdgcn_wave_barrier();
         const int n = nb + jp * 64 + c4;
@@ -192,7 +235,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmDesc &d, const floatx16 (
             for (int u = 0; u < G; u++) {
                 const int row = 4 * (t0 + u) + (lane >> 4);
                 const long m = mb + row;
-                const floatx4 a = *(const floatx4 *)(wlds + epi_lds_off(row, jp * 0 + c4));
+                const floatx4 a = *(const floatx4 *)(wlds + epi_lds_off<MI>(row, c4));
                 floatx4 v;
                 if constexpr (EPI == EPI_STORE) {
                     v = sc * a;

@@ -208,8 +208,8 @@ typedef struct {
     float *lossacc;
     int32_t tile;           /* 0 = auto, 64, 128, 256 (register-staged f32 kernel), 1000 + i (f32 direct-to-LDS
                                configuration i, 0..4; see ah_gemm_tune) */
-    int32_t variant;        /* f16 kernel variant: 0 = auto (the tuned choice if any), 1..31 = fixed tile /
-                               wave / fetch / k-group choices (table Var<V>, gemm16_kernel.h);
+    int32_t variant;        /* f16 kernel variant: 0 = auto (the tuned choice if any), 1..39 = fixed tile /
+                               wave / fetch / k-group / MFMA-shape choices (table Var<V>, gemm16_kernel.h);
                                the knob a BEAM-style search times (codegen/beam.go:41-541) */
 } ah_gemm_desc;
 int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
@@ -222,7 +222,7 @@ int ah_gemm(ah_device *dev, const ah_gemm_desc *d);
  * (ta, tb, M, N, K) with variant 0 use it. d is launched as given, so its outputs must be scratch
  * (the epilogue runs 2 * (iterations + 1) times per variant). Variants without k-groups differ only in
  * tiling and scheduling and accumulate each output over k in the same order (bit-identical results);
- * the k-group variants 10, 11, 15, 25, 28 and 31 add two k-halves, which rounds differently in f32 (relative
+ * the k-group variants 10, 11, 15, 25, 28, 31 and 35-38 add two k-halves, which rounds differently in f32 (relative
  * 1e-6 level). For an f32 contraction (dtype AH_F32) the candidates are the f32 kernel's (tile, k-groups,
  * splits of K across workgroups) configurations and the direct-to-LDS kernel's, 58 in all, and
  * *best_variant is the winner's index: 0 is the shape's automatic choice, then the register-staged
@@ -250,10 +250,11 @@ int ah_gemm_tune_cache(ah_device *dev, const char *path, int32_t save);
  * (arg/8), UPCAST(axis 0|1, 2|4) the MFMA register tile per wave (f32 kernel: tile 64*arg), TILE(axis 2,
  * 8|16|32) the LDS stage (k 32 x 4 stages, 64 x 2, 64 x 3), VECTORIZE(axis 2, 4) 16-byte asm LDS-DMA
  * staging (f32: the direct-to-LDS kernel, whose stage TILE then sets; the key gets dma=i);
- * GROUP(axis 2, 2|4) k-groups and SCHEDULE(axis 0, 5..7) the DMA/fragment-read interleave are
- * MI355X additions. Only "tmpl:gemm" keys have tunable parameters. */
+ * GROUP(axis 2, 2|4) k-groups, SCHEDULE(axis 0, 5..7) the DMA/fragment-read interleave and MFMA(axis 2,
+ * 16|32) the f16 kernel's MFMA shape (16x16x32 or 32x32x16; bit-identical results) are MI355X additions.
+ * Only "tmpl:gemm" keys have tunable parameters. */
 enum { AH_OPT_IDENTITY = 0, AH_OPT_LOCAL = 1, AH_OPT_TILE = 2, AH_OPT_UPCAST = 3, AH_OPT_VECTORIZE = 4,
-       AH_OPT_GROUP = 5, AH_OPT_SCHEDULE = 6 };
+       AH_OPT_GROUP = 5, AH_OPT_SCHEDULE = 6, AH_OPT_MFMA = 7 };
 typedef struct {
     int32_t kind, axis, arg;
 } ah_opt;

@@ -162,8 +162,8 @@ def test_chain_kernel_vs_oracle(dev, R, Cc):
         b.free()
 
 
-F16_VARIANTS = list(range(1, 32))   # every gemm16 variant (gemm16_kernel.h Var<V>)
-KGROUP_VARIANTS = (10, 11, 15, 25, 28, 31)   # variants that add two k-halves
+F16_VARIANTS = list(range(1, 40))   # every gemm16 variant (gemm16_kernel.h Var<V>; 32-39 use 16x16x32 MFMAs)
+KGROUP_VARIANTS = (10, 11, 15, 25, 28, 31, 35, 36, 37, 38)   # variants that add two k-halves
 VARIANT_SHAPES = [
     # ta, tb, M, N, K: full tiles, ragged edges (scalar epilogue), short K, both layouts
     (0, 0, 512, 512, 192), (0, 1, 520, 300, 128), (1, 1, 264, 520, 64), (1, 0, 256, 256, 320),

@@ -37,6 +37,24 @@ def test_schedule_and_group_opts():
     assert params(kg)["variant"] == "10"                 # 128x128, 2 k-groups, compiler-scheduled
 
 
+def test_mfma_shape_opt():
+    """MFMA(axis 2, 16) moves a kernel to its 16x16x32 form where one is instantiated (the asm-issued
+    schedules), and MFMA(axis 2, 32) back; the compiler-scheduled class has no 16x16x32 form."""
+    sched = [(L.OPT_VECTORIZE, 2, 4), (L.OPT_SCHEDULE, 0, 6)]
+    assert params(apply_opts(F16, sched))["variant"] == "27"
+    assert params(apply_opts(F16, sched + [(L.OPT_MFMA, 2, 16)]))["variant"] == "32"
+    assert params(apply_opts(F16, sched + [(L.OPT_MFMA, 2, 16), (L.OPT_MFMA, 2, 32)]))["variant"] == "27"
+    kg = [(L.OPT_LOCAL, 0, 16), (L.OPT_UPCAST, 0, 2), (L.OPT_UPCAST, 1, 2), (L.OPT_GROUP, 2, 2),
+          (L.OPT_VECTORIZE, 2, 4), (L.OPT_SCHEDULE, 0, 7)]
+    assert params(apply_opts(F16, kg))["variant"] == "31"
+    assert params(apply_opts(F16, kg + [(L.OPT_MFMA, 2, 16)]))["variant"] == "37"
+    with pytest.raises(L.AnnealHipError):
+        apply_opts(F16, [(L.OPT_MFMA, 2, 16)])          # variant 3's compiler-scheduled form: no MI 16 twin
+    with pytest.raises(L.AnnealHipError):
+        apply_opts(F16, [(L.OPT_MFMA, 0, 16)])          # the MFMA shape is a reduce-axis opt
+    assert (L.OPT_MFMA, 2, 16) in action_space(apply_opts(F16, sched))
+
+
 def test_invalid_sequences_fail_closed():
     for opts in ([(L.OPT_LOCAL, 3, 16)], [(L.OPT_UPCAST, 2, 2)], [(L.OPT_TILE, 0, 8)],
                  [(L.OPT_LOCAL, 0, 32), (L.OPT_UPCAST, 0, 4)]):        # 4 waves x 4 blocks: no such tile
