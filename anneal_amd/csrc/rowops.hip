@@ -362,9 +362,9 @@ __global__ __launch_bounds__(256) void chain_grad_kernel(const float *X, int R, 
 // Every softmax / RMS row of the chain is one column of X, and dg, the loss terms and dX of a column
 // need only that column. So one workgroup per CU takes a strip of 16 columns x R rows (R = 4096 or
 // 8192: up to 512 KiB), keeps all of it on chip (kResRegs float4 per thread in VGPRs, kResLds in LDS through
-// LDS-DMA), and runs the whole chain on it: the exact column max, then sum e, sum e^2 and the tie
-// count against that max (no rescaling), the per-column scalars of chain_finalize, dg, and dX written
-// once from the on-chip copy. HBM sees X read once and dX written once; the three-kernel chain reads X
+// LDS-DMA), and runs the whole chain on it: the column max, sum e, sum e^2 and the tie count
+// (accumulated while the strip lands, see below), the per-column scalars of chain_finalize, dg, and dX
+// written once from the on-chip copy. HBM sees X read once and dX written once; the three-kernel chain reads X
 // twice and moves its column partials through memory. Thread t owns columns c0 + 4 (t & 3) .. + 3 of
 // rows (t >> 2) + 128 i. Every sum is a fixed tree (slots in order, then lanes by xor, then waves in
 // order), so results are deterministic. Each workgroup stores its 16 columns' loss terms summed in
@@ -421,21 +421,70 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
     for (int j = 0; j < kResLds; j++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void *)&held[j][wave * 64], 16,
                                                      voff, (kResRegs + j) * rstepB, 0, 0);
-    // 2. column max
-    float m[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+    // 2-3. Statistics while the strip lands. Each thread takes a provisional max mt of its own first
+    // kProv slots, then, slot by slot as the loads arrive, adds e = 2^(x/ln2 - mt/ln2) and e^2 to its
+    // column sums and keeps the exact running max with the count of elements equal to it. Once every
+    // slot has landed, the column max m is the max of the running maxima, the tie count the sum of the
+    // counts of the threads whose running max is m, and each thread's sums are rescaled by
+    // 2^((mt - m)/ln2) before the column sums. x stays in place; the dX pass recomputes e against m. An
+    // element more than 2^60 above the thread's reference (where e^2 could overflow) first moves the
+    // reference to itself, rescaling the thread's sums (no such element occurs unless the strip's
+    // values grow by a factor e^41 along the column).
+    constexpr int kProv = 8;
+    static_assert(kResRegs >= kProv, "the provisional max takes register slots");
+    float mt[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
 #pragma unroll
-    for (int i = 0; i < kResRegs; i++)
+    for (int i = 0; i < kProv; i++)
 #pragma unroll
-        for (int u = 0; u < 4; u++) m[u] = fmaxf(m[u], v[i][u]);
+        for (int u = 0; u < 4; u++) mt[u] = fmaxf(mt[u], v[i][u]);
+    float mct[4], mr[4], cnt[4], se[4] = {}, sq[4] = {};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        mct[u] = mt[u] * AH_INV_LN2;
+        mr[u] = -FLT_MAX;
+        cnt[u] = 0.0f;
+    }
+    auto stat = [&](const floatx4 &x) {
+        float d[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) d[u] = __builtin_fmaf(x[u], AH_INV_LN2, -mct[u]);
+        // one wave-uniform test per slot for the (never taken on ordinary data) re-base
+        const float dm = fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3]));
+        if (__builtin_amdgcn_ballot_w64(dm > 60.0f)) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (d[u] > 60.0f) {
+                    const float f = fast_exp2(-d[u]);
+                    se[u] *= f;
+                    sq[u] *= f * f;
+                    mct[u] = x[u] * AH_INV_LN2;
+                    d[u] = __builtin_fmaf(x[u], AH_INV_LN2, -mct[u]);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float e = fast_exp2(d[u]);
+            se[u] += e;
+            sq[u] += e * e;
+            const float mn = fmaxf(mr[u], x[u]);
+            cnt[u] = (mn == mr[u] ? cnt[u] : 0.0f) + (x[u] == mn ? 1.0f : 0.0f);   // count of the running max
+            mr[u] = mn;
+        }
+        // materialise the running values after every slot (left free, the compiler runs one sum over
+        // all slots before the next, keeping every slot's e live in between)
+        asm volatile("" : "+v"(se[0]), "+v"(se[1]), "+v"(se[2]), "+v"(se[3]), "+v"(sq[0]), "+v"(sq[1]), "+v"(sq[2]),
+                     "+v"(sq[3]), "+v"(cnt[0]), "+v"(cnt[1]), "+v"(cnt[2]), "+v"(cnt[3]), "+v"(mr[0]), "+v"(mr[1]),
+                     "+v"(mr[2]), "+v"(mr[3]));
+    };
+#pragma unroll
+    for (int i = 0; i < kResRegs; i++) stat(v[i]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's LDS-DMA has landed (each lane reads its own)
 #pragma unroll 2
     for (int j = 0; j < kResLds; j++) {
         const floatx4 x = *(volatile floatx4 *)&held[j][tid];
-#pragma unroll
-        for (int u = 0; u < 4; u++) m[u] = fmaxf(m[u], x[u]);
+        stat(x);
     }
-#pragma unroll
-    for (int u = 0; u < 4; u++) m[u] = res_tree_max(m[u]);
     // Cross-wave step of a column reduction: lanes 0-3 of each wave post their 4 columns, 16 threads
     // fold the 8 waves in order, and every thread reads its 4 columns back as one vector (the per-thread
     // live set stays at 4 values; the held strip fills most registers).
@@ -456,50 +505,23 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         for (int u = 0; u < 4; u++) x[u] = r4[u];
         __syncthreads();   // colv and red are reused
     };
+    float m[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) m[u] = res_tree_max(mr[u]);
     across_waves(m, true, nullptr);
-    // Passes 3 and 5 walk the register slots, then the LDS slots two at a time. The LDS slots are read
-    // through volatile loads in every pass: otherwise the compiler may keep one pass's reads live in
-    // registers for the next, which the held strip leaves no room for.
-    auto each = [&](auto &&f) {
+    float mc[4], tc[4];
 #pragma unroll
-        for (int i = 0; i < kResRegs; i++) f(i, v[i]);
-#pragma unroll 2
-        for (int j = 0; j < kResLds; j++) {
-            const floatx4 x = *(volatile floatx4 *)&held[j][tid];
-            f(kResRegs + j, x);
-        }
-    };
-    // 3. sum e, sum e^2 and ties against the exact max. Each slot then keeps its e in place of x,
-    // negated where the element ties its column's max (e is exactly 1 there, and every other e is
-    // +0 or positive), so the backward pass needs neither the exp nor the max again.
-    float se[4] = {}, sq[4] = {}, tc[4] = {}, mc[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) mc[u] = m[u] * AH_INV_LN2;
-    auto stat = [&](floatx4 x) -> floatx4 {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float e = fast_exp2(__builtin_fmaf(x[u], AH_INV_LN2, -mc[u]));
-            const bool tie = x[u] == m[u];
-            se[u] += e;
-            sq[u] += e * e;
-            tc[u] += tie ? 1.0f : 0.0f;
-            x[u] = tie ? -e : e;
-        }
-        // materialise all three sums after every slot: left free, the compiler runs the e sums over
-        // all slots first and the e^2 sums after them, keeping every slot's e live in between
-        asm volatile("" : "+v"(se[0]), "+v"(se[1]), "+v"(se[2]), "+v"(se[3]), "+v"(sq[0]), "+v"(sq[1]), "+v"(sq[2]),
-                     "+v"(sq[3]), "+v"(tc[0]), "+v"(tc[1]), "+v"(tc[2]), "+v"(tc[3]), "+v"(x));
-        return x;
-    };
-#pragma unroll
-    for (int i = 0; i < kResRegs; i++) v[i] = stat(v[i]);
-#pragma unroll 2
-    for (int j = 0; j < kResLds; j++) held[j][tid] = stat(*(volatile floatx4 *)&held[j][tid]);
+    for (int u = 0; u < 4; u++) {
+        mc[u] = m[u] * AH_INV_LN2;
+        tc[u] = res_tree_sum(mr[u] == m[u] ? cnt[u] : 0.0f);
+        const float f = fast_exp2(mct[u] - mc[u]);   // 2^((mt - m)/ln2) <= 1
+        se[u] *= f;
+        sq[u] *= f * f;
+    }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         se[u] = res_tree_sum(se[u]);
         sq[u] = res_tree_sum(sq[u]);
-        tc[u] = res_tree_sum(tc[u]);
     }
     across_waves(se, false, colsum3[0]);
     across_waves(sq, false, colsum3[1]);
@@ -541,7 +563,18 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
 #pragma unroll
         for (int u = 0; u < 4; u++) { ca[u] = a[u]; cb[u] = b[u]; sh[u] = e[u]; }
     }
-    // 5. dX from the held strip
+    // 5. dX from the held strip: the register slots, then the LDS slots two at a time. The LDS slots are
+    // read through volatile loads in every pass: otherwise the compiler may keep one pass's reads live in
+    // registers for the next, which the held strip leaves no room for.
+    auto each = [&](auto &&f) {
+#pragma unroll
+        for (int i = 0; i < kResRegs; i++) f(i, v[i]);
+#pragma unroll 2
+        for (int j = 0; j < kResLds; j++) {
+            const floatx4 x = *(volatile floatx4 *)&held[j][tid];
+            f(kResRegs + j, x);
+        }
+    };
     // The stores' row offset is a running value advanced through an empty asm after each slot, so only
     // the current one is live (all 64 kept from the loads overflow the SGPRs into VGPR lanes).
     int soff = 0;
@@ -549,10 +582,9 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         floatx4 o;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const float y = x[u];   // e, negated at the column's max
-            const float e = fabsf(y);
+            const float e = fast_exp2(__builtin_fmaf(x[u], AH_INV_LN2, -mc[u]));
             const float gzs = (ca[u] + cb[u] * e) * e;
-            o[u] = gzs + (y < 0.0f ? sh[u] : 0.0f);
+            o[u] = gzs + (x[u] == m[u] ? sh[u] : 0.0f);
         }
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, o), dr, voff, soff, 0);
         soff += rstepB;

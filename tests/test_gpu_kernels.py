@@ -137,9 +137,14 @@ def test_softmax_ce_kernel(dev, B, C):
 
 # (4096, 256), (8192, 64) and (8192, 528): the column-strip kernel that holds X on chip; the others: the
 # three-kernel chain
-@pytest.mark.parametrize("R,Cc", [(64, 32), (257, 260), (1024, 512), (4096, 256), (8192, 64), (8192, 528)])
-def test_chain_kernel_vs_oracle(dev, R, Cc):
+@pytest.mark.parametrize("R,Cc,grow", [(64, 32, False), (257, 260, False), (1024, 512, False), (4096, 256, False),
+                                       (8192, 64, False), (8192, 528, False), (4096, 256, True), (8192, 64, True)])
+def test_chain_kernel_vs_oracle(dev, R, Cc, grow):
+    """grow: half the columns jump by +50 in their second half of rows, far above the maximum of the
+    rows the strip kernel's threads take their provisional max from (it then re-bases its sums)."""
     X = RNG.standard_normal((R, Cc)).astype(np.float32)
+    if grow:
+        X[R // 2:, : Cc // 2] += 50.0
     X[5, :] = X.max() + 0.5                             # every row of Y gets a tie candidate
     X[9, :] = X[5, :]
     g = (1 + 0.02 * RNG.standard_normal(Cc)).astype(np.float32)
