@@ -22,9 +22,11 @@ hipError_t words_differ(const void *a, const void *b, long words, int *differs, 
 // out[m] = scale * reduce_n G[m, n] (scale not applied to max); G is f32, or f16 when f16 is set, and the
 // reduction runs in f32.
 hipError_t reduce_rows(const void *G, bool f16, int M, int N, int op, float scale, float *out, hipStream_t s);
-// out[n] = scale * reduce_m G[m, n]; work holds reduce_cols_workspace(M, N) floats. Deterministic.
+// out[n] = scale * reduce_m G[m, n]; work holds reduce_cols_workspace(M, N) floats. Deterministic. With Z
+// (same shape as G, f16 or f32) each element is masked first: Where(Z >= 0, G, 0), the ReLU backward mask.
 long reduce_cols_workspace(int M, int N);
-hipError_t reduce_cols(const void *G, bool f16, int M, int N, int op, float scale, float *work, float *out, hipStream_t s);
+hipError_t reduce_cols(const void *G, bool f16, int M, int N, int op, float scale, float *work, float *out, hipStream_t s,
+                       const void *Z = nullptr, bool z_f16 = false);
 // MaxPool2D over [NC, H, W] with window kH x kW and stride sH x sW (no padding), and its backward.
 hipError_t maxpool_fwd(const float *X, long NC, int H, int W, int kH, int kW, int sH, int sW, float *out, hipStream_t s);
 hipError_t maxpool_bwd(const float *X, const float *adj, long NC, int H, int W, int kH, int kW, int sH, int sW,

@@ -77,15 +77,21 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(const T *G, int M, int
 }
 
 // Column reduce, pass 1: block (column group of 64, row chunk) folds kRedRows rows with 4 row lanes per
-// column, then the 4 lanes in a fixed order; the chunk's value goes to part[chunk][n].
-template <typename T>
-__global__ __launch_bounds__(256) void reduce_cols_partial_kernel(const T *G, int M, int N, int op, float *part) {
+// column, then the 4 lanes in a fixed order; the chunk's value goes to part[chunk][n]. With Z, an element
+// enters as Where(Z == max(Z, 0), G, 0) (the ReLU backward mask, gradient_ruleset.go:153-161), else 0.
+template <typename T, typename TZ>
+__global__ __launch_bounds__(256) void reduce_cols_partial_kernel(const T *G, const TZ *Z, int M, int N, int op, float *part) {
     __shared__ float red[4][64];
     const int col = blockIdx.x * 64 + (threadIdx.x & 63), sub = threadIdx.x >> 6;
     const int r0 = blockIdx.y * kRedRows, r1 = min(M, r0 + kRedRows);
     float acc = red_init(op);
     if (col < N)
-        for (int r = r0 + sub; r < r1; r += 4) acc = red_step(op, acc, (float)G[(long)r * N + col]);
+        for (int r = r0 + sub; r < r1; r += 4) {
+            const long i = (long)r * N + col;
+            float v = (float)G[i];
+            if (Z) v = (float)Z[i] >= 0.0f ? v : 0.0f;
+            acc = red_step(op, acc, v);
+        }
     red[sub][threadIdx.x & 63] = acc;
     __syncthreads();
     if (sub == 0 && col < N) {
@@ -287,12 +293,21 @@ hipError_t reduce_rows(const void *G, bool f16, int M, int N, int op, float scal
     return hipGetLastError();
 }
 
-hipError_t reduce_cols(const void *G, bool f16, int M, int N, int op, float scale, float *work, float *out, hipStream_t s) {
+hipError_t reduce_cols(const void *G, bool f16, int M, int N, int op, float scale, float *work, float *out, hipStream_t s,
+                       const void *Z, bool z_f16) {
     if (N <= 0) return hipSuccess;
     const int chunks = M > 0 ? (M + kRedRows - 1) / kRedRows : 0;
-    const dim3 grid((N + 63) / 64, chunks);
-    if (chunks > 0 && f16) hipLaunchKernelGGL(reduce_cols_partial_kernel<half_t>, grid, dim3(256), 0, s, (const half_t *)G, M, N, op, work);
-    if (chunks > 0 && !f16) hipLaunchKernelGGL(reduce_cols_partial_kernel<float>, grid, dim3(256), 0, s, (const float *)G, M, N, op, work);
+    const dim3 grid((N + 63) / 64, chunks), block(256);
+    if (chunks > 0) {
+        if (f16 && z_f16)
+            hipLaunchKernelGGL((reduce_cols_partial_kernel<half_t, half_t>), grid, block, 0, s, (const half_t *)G, (const half_t *)Z, M, N, op, work);
+        else if (f16)
+            hipLaunchKernelGGL((reduce_cols_partial_kernel<half_t, float>), grid, block, 0, s, (const half_t *)G, (const float *)Z, M, N, op, work);
+        else if (z_f16)
+            hipLaunchKernelGGL((reduce_cols_partial_kernel<float, half_t>), grid, block, 0, s, (const float *)G, (const half_t *)Z, M, N, op, work);
+        else
+            hipLaunchKernelGGL((reduce_cols_partial_kernel<float, float>), grid, block, 0, s, (const float *)G, (const float *)Z, M, N, op, work);
+    }
     hipLaunchKernelGGL(reduce_cols_final_kernel, dim3((N + 255) / 256), dim3(256), 0, s, work, chunks, N, op, scale, out);
     return hipGetLastError();
 }

@@ -317,6 +317,10 @@ int template_gemm(const Params &P, TemplateKernel *t) {
 }
 
 // ── reduce ───────────────────────────────────────────────────────────────────────────────────────
+// "tmpl:reduce;op=sum|max|sumsq;axis=0|1;M=..;N=..[;scale=s][;dtype=f16][;pa=mask;za=z[;in_a=i][;wza=1]]"
+// PARAMs: out (f32), A [M,N]. pa=mask (column sums only): each element enters as Where(Z == max(Z, 0), A, 0)
+// with Z [M,N] the PARAM za, stored f16 with wza=1 (the bias gradient of a ReLU layer,
+// gradient_ruleset.go:153-161); in_a names A's PARAM (default 1).
 int template_reduce(const Params &P, TemplateKernel *t) {
     static const std::map<std::string, int> ops = {{"sum", RED_SUM}, {"max", RED_MAX}, {"sumsq", RED_SUMSQ}};
     auto oi = ops.find(P.str("op", "sum"));
@@ -331,26 +335,41 @@ int template_reduce(const Params &P, TemplateKernel *t) {
     const std::string dt = P.str("dtype", "f32");
     if (dt != "f32" && dt != "f16") return set_error(AH_ERR_UNSUPPORTED, "tmpl reduce: dtype %s", dt.c_str());
     const bool f16 = dt == "f16";
+    const std::string pa = P.str("pa", "");
+    const bool mask = pa == "mask";
+    if (!pa.empty() && !mask) return set_error(AH_ERR_UNSUPPORTED, "tmpl reduce: prologue %s", pa.c_str());
+    if (mask && (axis != 0 || op != RED_SUM)) return set_error(AH_ERR_UNSUPPORTED, "tmpl reduce: the mask prologue is for column sums");
+    const int pA = mask ? (int)P.integer("in_a", 1) : 1, pZ = mask ? (int)P.integer("za", -1) : -1;
+    if (mask && (pA < 1 || pA > 2 || pZ < 1 || pZ > 2 || pA == pZ))
+        return set_error(AH_ERR_INVALID, "tmpl reduce: in_a and za name PARAMs 1 and 2");
+    const bool wz = P.integer("wza", 0) != 0;
+    if (wz && !mask) return set_error(AH_ERR_INVALID, "tmpl reduce: wza needs the mask prologue");
+    const int nbuf = mask ? 3 : 2;
     const std::string key = t->key;
-    t->bytes = [axis, M, N, f16](int64_t sv) -> std::vector<int64_t> {
+    t->bytes = [axis, M, N, f16, mask, pA, pZ, wz, nbuf](int64_t sv) -> std::vector<int64_t> {
         const int64_t m = M.with(sv), n = N.with(sv);
-        return {(axis == 0 ? n : m) * 4, m * n * (f16 ? 2 : 4)};
+        std::vector<int64_t> b(nbuf);
+        b[0] = (axis == 0 ? n : m) * 4;
+        b[pA] = m * n * (f16 ? 2 : 4);
+        if (mask) b[pZ] = m * n * (wz ? 2 : 4);
+        return b;
     };
     t->workspace = [axis, M, N](int64_t symv) -> int64_t {
         if (axis != 0) return 0;
         const long m = M.sym ? symv : M.v, n = N.sym ? symv : N.v;
         return m > 0 && n > 0 ? reduce_cols_workspace((int)m, (int)n) * 4 : 0;
     };
-    t->run = [op, axis, M, N, scale, f16, key](ah_device *d, TemplateKernel *self, void *const *ptrs, int32_t n_ptrs,
-                                           const int32_t *sc, int32_t ns) -> int {
-        if (int rc = need(key.c_str(), n_ptrs, 2)) return rc;
+    t->run = [op, axis, M, N, scale, f16, key, mask, pA, pZ, wz, nbuf](ah_device *d, TemplateKernel *self, void *const *ptrs,
+                                                                      int32_t n_ptrs, const int32_t *sc, int32_t ns) -> int {
+        if (int rc = need(key.c_str(), n_ptrs, nbuf)) return rc;
         AT(M, m);
         AT(N, n);
         if (axis == 1) {
             AH_HIP(reduce_rows(ptrs[1], f16, (int)m, (int)n, op, scale, (float *)ptrs[0], d->stream));
         } else {
             if (int rc = ensure_ws(self, reduce_cols_workspace((int)m, (int)n) * 4)) return rc;
-            AH_HIP(reduce_cols(ptrs[1], f16, (int)m, (int)n, op, scale, (float *)self->ws, (float *)ptrs[0], d->stream));
+            AH_HIP(reduce_cols(ptrs[pA], f16, (int)m, (int)n, op, scale, (float *)self->ws, (float *)ptrs[0], d->stream,
+                               mask ? ptrs[pZ] : nullptr, wz));
         }
         return AH_OK;
     };

@@ -19,7 +19,9 @@
 //                max(acc + bias[n], 0.0) (f16: max(f16(acc) + bias, 0.0))  ->  "tmpl:gemm" with ta/tb,
 //                prologues pa/pb and PARAM roles;
 //   reduction    REDUCE(ADD|MAX, load) over the innermost or the outermost axis of a 2-D buffer (or all
-//                of a 1-D one), stored as acc or c*acc into f32  ->  "tmpl:reduce".
+//                of a 1-D one), or REDUCE(ADD) of the ReLU-backward mask prologue down a column (a ReLU
+//                layer's bias gradient, the mask source at the same element, f16 sources widened),
+//                stored as acc or c*acc into f32  ->  "tmpl:reduce" (pa=mask for the masked form).
 //
 // Index expressions are not matched as text: they are evaluated as integer arithmetic (the scheduler's
 // unsimplified chains of / and % included) at every point of each axis and at sampled points of the
@@ -553,11 +555,19 @@ std::string classify(const std::string &src, int64_t n0) {
 
     // ── plain reduction over one axis ──
     if (live.size() <= 1) {
-        bool w = false;
-        P u = unwiden(k.upd, &w);
-        if (u->k != Node::LOAD || u->buf < 1 || u->buf >= nb || nb != 2 || out_t != "f32") return "";
-        const std::string in_t = k.btype[u->buf];
-        if ((in_t != "f32" && in_t != "f16") || w != (in_t == "f16")) return "";
+        // the reduced value: a load (f16 widened), or the ReLU-backward mask of one (column sums)
+        Operand o;
+        if (!operand(k.upd, &o) || o.pro == 1) return "";
+        const bool masked = o.pro == 2;
+        if (o.buf < 1 || o.buf >= nb || nb != (masked ? 3 : 2) || out_t != "f32") return "";
+        const std::string in_t = k.btype[o.buf];
+        if ((in_t != "f32" && in_t != "f16") || o.widened != (in_t == "f16")) return "";
+        std::string z_t;
+        if (masked) {
+            if (o.zbuf < 1 || o.zbuf >= nb || o.zbuf == o.buf || k.accop != '+') return "";
+            z_t = k.btype[o.zbuf];
+            if ((z_t != "f32" && z_t != "f16") || o.zwidened != (z_t == "f16")) return "";
+        }
         float scale = 1.0f;
         P v = k.val;
         if (v->k == Node::BIN && v->s == "*") {
@@ -571,7 +581,11 @@ std::string classify(const std::string &src, int64_t n0) {
         if (k.accop == '+' && k.acc_init != "0.0") return "";
         if (k.accop == 'M' && (k.acc_init != "bitcast<f32>(0xff7fffffu)" || scale != 1.0f)) return "";
         std::vector<int64_t> ci;
-        if (!affine(u->a[0], vn, rg, &ci)) return "";
+        if (!affine(o.idx, vn, rg, &ci)) return "";
+        if (masked) {   // the mask reads Z at A's element
+            std::vector<int64_t> cz;
+            if (!affine(o.zidx, vn, rg, &cz) || cz != ci) return "";
+        }
         std::string M, N;
         int axis;
         if (live.empty()) {   // out[0] = reduce over k of in[k]
@@ -586,10 +600,13 @@ std::string classify(const std::string &src, int64_t n0) {
         } else {
             return "";
         }
+        if (masked && axis != 0) return "";
         std::string key = "tmpl:reduce;op=" + std::string(k.accop == '+' ? "sum" : "max") + ";axis=" + std::to_string(axis) +
                           ";M=" + M + ";N=" + N;
         if (in_t == "f16") key += ";dtype=f16";
         if (scale != 1.0f) key += ";scale=" + fmt_float(scale);
+        if (masked)
+            key += ";pa=mask;in_a=" + std::to_string(o.buf) + ";za=" + std::to_string(o.zbuf) + (z_t == "f16" ? ";wza=1" : "");
         return key;
     }
 

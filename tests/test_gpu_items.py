@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
+import wgsl_lower as WL
 from anneal_amd import _lib as L
 from anneal_amd import data, items
 from anneal_amd.executor import Buffer, ExecItem, Executor, Plan
@@ -287,3 +288,51 @@ def test_unknown_template_and_bad_keys_fail_closed(dev):
                 "tmpl:reduce;op=prod;M=2;N=2", "tmpl:maxpool2d;N=1;C=1;H=2;W=2;kh=3;kw=3;sh=1;sw=1"):
         with pytest.raises(L.AnnealHipError, match="kernel 0"):
             ex.run([ExecItem(src, [Buffer(10, 16, [16]), Buffer(1, 16, [16]), Buffer(2, 16, [16])])], {})
+
+
+@pytest.mark.parametrize("z_f16", [False, True])
+def test_masked_column_sum_template(dev, monkeypatch, z_f16):
+    """A ReLU layer's bias gradient, db[n] = Sum_m Where(Z == max(Z, 0), G, 0)[m, n], as the reference's
+    lowering renders it (configs 1 and 4 with an f32 Z; config 3 with an f16 Z read widened): the selected
+    reduce template with the mask prologue matches float64 at the f32 reduction bar, and the same kernel
+    rendered (selection off) to summation order; Z = -0.0 and 0.0 both pass the mask, as Z == max(Z, 0)
+    holds for them."""
+    from anneal_amd.backend import Device
+    if z_f16:
+        ks, _, _ = WL.mlp3_step(300, 32, 48, 70, 24)
+        name, M, N, ia, iz = "db2", 300, 70, 1, 2
+    else:
+        ks, _, _ = WL.mlp_ce_step(300, 784, 70, 10)
+        name, M, N, ia, iz = "db1", 300, 70, 2, 1
+    _, src, bufs, ws, wc, plan = next(k for k in ks if k[0] == name)
+    assert L.wgsl_plan(src) == plan and ";pa=mask" in plan
+    rng = np.random.default_rng(5)
+    G = rng.standard_normal((M, N)).astype(np.float32)
+    Z = rng.standard_normal((M, N)).astype(np.float32)
+    Z[0, :8] = -0.0
+    Z[1, :8] = 0.0
+    if z_f16:
+        Z = Z.astype(np.float16).astype(np.float32)
+    uid = {i: b[0] for i, b in enumerate(bufs)}
+    inp = {uid[ia]: G.ravel(), uid[iz]: Z.ravel()}
+    item = ExecItem(src, [Buffer(u, n, sh, dtype=dt) for (u, n, dt, sh) in bufs], local_size=ws, workgroup_count=wc)
+    got = Executor(dev).run([item], inp)[uid[0]]
+    want = np.where(Z >= 0, G.astype(np.float64), 0.0).sum(0)
+    assert O.relerr(got, want) < 1e-6
+    monkeypatch.setenv("AH_WGSL_TEMPLATES", "0")
+    with Device(0) as d2:
+        ref = Executor(d2).run([item], inp)[uid[0]]
+    assert O.relerr(got, ref) < 1e-6
+
+
+def test_reduce_template_rejects_bad_mask_keys(dev):
+    """The mask prologue is for column sums with its two PARAMs named; anything else fails at plan time."""
+    ex = Executor(dev)
+    bufs = [Buffer(10, 4, [4]), Buffer(1, 16, [4, 4]), Buffer(2, 16, [4, 4])]
+    for key in ("tmpl:reduce;op=sum;axis=1;M=4;N=4;pa=mask;in_a=1;za=2",   # row sums
+                "tmpl:reduce;op=max;axis=0;M=4;N=4;pa=mask;in_a=1;za=2",   # max
+                "tmpl:reduce;op=sum;axis=0;M=4;N=4;pa=mask;in_a=1;za=1",   # Z is A
+                "tmpl:reduce;op=sum;axis=0;M=4;N=4;pa=relu",               # no such prologue
+                "tmpl:reduce;op=sum;axis=0;M=4;N=4;wza=1"):                # widening without the mask
+        with pytest.raises(L.AnnealHipError):
+            ex.run([ExecItem(key, bufs)], {1: np.ones(16, np.float32), 2: np.ones(16, np.float32)})

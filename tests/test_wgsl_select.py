@@ -88,16 +88,17 @@ import wgsl_lower as WL  # noqa: E402
 @pytest.mark.parametrize("shape", [(64, 784, 128, 10), (256, 512, 2048, 512)])
 def test_rendered_mlp_ce_step_selects_a_template_or_the_wave_rendering(shape, symbolic):
     """Every kernel of the rendered step is run by a hand-written template (the contractions with their
-    ReLU and mask prologues and bias epilogues, the plain row max and column sum) or, for the reductions
-    with elementwise prologues, by the wave-per-output rendering; only the elementwise dZ kernel keeps the
-    one-thread-per-output rendering."""
+    ReLU and mask prologues and bias epilogues, the plain row max and column sum, the masked column sum
+    db1) or, for the softmax-CE reductions with elementwise prologues, by the wave-per-output rendering;
+    only the elementwise dZ kernel keeps the one-thread-per-output rendering."""
     B, D, H, C = shape
     ks, _, _ = WL.mlp_ce_step(B, D, H, C, symbolic=symbolic)
     plans = {name: L.wgsl_plan(src) for name, src, *_ in ks}
     for name, src, bufs, ws, wc, want in ks:
         assert plans[name] == want, (name, plans[name], want)
     assert sum(p.startswith("tmpl:gemm") for p in plans.values()) == 5
-    assert sum(p.startswith("tmpl:reduce") for p in plans.values()) == 2
+    assert sum(p.startswith("tmpl:reduce") for p in plans.values()) == 3
+    assert sorted(n for n, p in plans.items() if p == "wave") == ["gls", "gmax", "loss", "sumexp", "tie"]
     assert [n for n, p in plans.items() if p == "thread"] == ["dZ"]
 
 
@@ -108,6 +109,16 @@ def test_f16_contraction_with_narrowing_is_selected(bias, relu, relu_out):
     with the ReLU as the input's prologue, as the output's epilogue, or both."""
     src, _, _, _, key = WL.f16_linear(256, 128, 192, bias=bias, relu_a=relu, relu_out=relu_out)
     assert L.wgsl_template_key(src) == key
+
+
+def test_masked_column_sum_needs_the_same_index_for_z_and_the_adjoint():
+    """The masked column sum (a ReLU layer's bias gradient) selects the reduce template only when z is read
+    at the adjoint's element; shifted, it keeps the wave rendering."""
+    ks, _, _ = WL.mlp_ce_step(64, 784, 128, 10)
+    src = dict((n, s) for n, s, *_ in ks)["db1"]
+    assert L.wgsl_plan(src) == "tmpl:reduce;op=sum;axis=0;M=64;N=128;pa=mask;in_a=2;za=1"
+    bad = src.replace("data1[(r1 * 128) + r0]", "data1[(r1 * 128) + ((r0 + 1) % 128)]")
+    assert bad != src and L.wgsl_plan(bad) == "wave"
 
 
 def test_mask_prologue_needs_the_same_index_for_z_and_the_adjoint():
@@ -134,8 +145,9 @@ def test_reduce_with_scale_and_scalar_output():
 def test_rendered_mlp3_step_selects_templates():
     """Config 3's rendered step: the three f16 layers select the f16 contraction template (ReLU prologue on
     the second and third); the five f32 x f16 backward contractions the f32 template with their f16
-    operands and mask sources widened (wa/wb/wza); the output bias gradient the column-sum template; the
-    loss and the masked column sums keep the wave rendering, the loss adjoint the thread one."""
+    operands and mask sources widened (wa/wb/wza); the output bias gradient the column-sum template and the
+    masked ones (db2, db1) the column-sum template with the mask prologue on their f16 pre-activations;
+    the loss keeps the wave rendering, the loss adjoint the thread one."""
     ks, _, _ = WL.mlp3_step(256, 128, 256, 256, 128)
     plans = {name: L.wgsl_plan(src) for name, src, *_ in ks}
     for name, src, _, _, _, plan in ks:
@@ -143,7 +155,8 @@ def test_rendered_mlp3_step_selects_templates():
     assert [n for n, p in plans.items() if p.startswith("tmpl:gemm;dtype=f16")] == ["fc1", "fc2", "fc3"]
     assert [n for n, p in plans.items() if p.startswith("tmpl:gemm;dtype=f32")] == ["dW3", "dH2", "dW2", "dH1", "dW1"]
     assert plans["db3"].startswith("tmpl:reduce") and plans["gP"] == "thread"
-    assert sorted(n for n, p in plans.items() if p == "wave") == ["db1", "db2", "loss"]
+    assert plans["db2"].endswith(";pa=mask;in_a=1;za=2;wza=1") and plans["db1"].endswith(";pa=mask;in_a=1;za=2;wza=1")
+    assert [n for n, p in plans.items() if p == "wave"] == ["loss"]
 
 
 def test_mixed_type_contraction_needs_widened_f16_loads():

@@ -357,7 +357,7 @@ def mlp_ce_step(B: int, D: int, H: int, C: int, symbolic: bool = False):
     k.update(masked(k, 1, 2, r1))
     k.end()
     k.store("acc0")
-    add("db1", k, "wave")
+    add("db1", k, f"tmpl:reduce;op=sum;axis=0;M={Bk};N={H};pa=mask;in_a=2;za=1")
 
     # 14. dW1 = Where(Z1 == relu(Z1), dH1, 0)^T x
     k = Kernel([(udW1, [H, D], F32), (udH1, bshape(H), F32), (uZ1, bshape(H), F32), (1, bshape(D), F32)], [H, D], symbolic)
@@ -474,7 +474,7 @@ def mlp3_step(B: int, D0: int, D1: int, D2: int, D3: int):
         k.update(a)
         k.end()
         k.store("acc0")
-        add(name, k, f"tmpl:reduce;op=sum;axis=0;M={B};N={n}" if zbuf is None else "wave")
+        add(name, k, f"tmpl:reduce;op=sum;axis=0;M={B};N={n}" + ("" if zbuf is None else ";pa=mask;in_a=1;za=2;wza=1"))
 
     def masked_adj(k, adj, zbuf, r, n, col):
         # Where(z == max(z, 0), adj, 0) at (r, col) of [B, n], z an f16 activation widened
