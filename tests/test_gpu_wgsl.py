@@ -208,3 +208,31 @@ def test_selected_mixed_type_contraction_matches_rendering(dev, monkeypatch, nam
         ref = Executor(d2).run([item], inp)[out]
     scale = np.abs(ref).max()
     assert scale > 0 and np.abs(got - ref).max() / scale < 1e-5
+
+
+@pytest.mark.parametrize("R,Cc", [(64, 48), (257, 33), (1024, 96)])
+def test_rendered_chain_step_matches_oracle(dev, R, Cc):
+    """Config 5's step as the reference's rendered kernels (10 WGSL kernels, the permute / pad / shrink
+    chain as index arithmetic in every load of Y, tests/wgsl_lower.py chain_step), run through ah_run:
+    loss and dg match ora_chain_step at 1e-5, dX at 1e-4 of max |dX| away from the column maxima, and the
+    tie elements (whose share is a rounding residue of the max path) no further from the float64 closed
+    form than the oracle is, plus 1e-4, as test_chain_kernel_vs_oracle judges the hand-written kernels."""
+    rng = np.random.default_rng(R + Cc)
+    X = rng.standard_normal((R, Cc)).astype(np.float32)
+    X[5, :] = X.max() + 0.5                              # every row of Y gets a tie
+    X[9, :] = X[5, :]
+    g = (1 + 0.02 * rng.standard_normal(Cc)).astype(np.float32)
+    ks, lv, outs = WL.chain_step(R, Cc)
+    items = [ExecItem(src, [Buffer(u, n, sh, dtype=dt) for (u, n, dt, sh) in bufs], local_size=ws, workgroup_count=wc)
+             for _, src, bufs, ws, wc, _ in ks]
+    got = Executor(dev).run(items, {lv["X"]: X.ravel(), lv["g"]: g})
+    wl, wdX, wdg = O.chain_step(X, g)
+    from oracle_np import chain_dX_f64
+    dX = got[outs["dX"]].reshape(R, Cc)
+    exact = chain_dX_f64(X, g)
+    mask = X == X.max(0, keepdims=True)
+    den = np.max(np.abs(wdX))
+    assert np.max(np.abs(dX - wdX)[~mask]) / den < 1e-4
+    assert np.max(np.abs(dX - exact)[mask]) / den <= np.max(np.abs(wdX - exact)[mask]) / den + 1e-4
+    assert O.relerr(got[outs["dg"]], wdg) < 1e-5
+    assert abs(got[outs["loss"]][0] - wl) < 1e-5 * abs(wl)

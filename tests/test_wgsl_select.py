@@ -167,3 +167,17 @@ def test_mixed_type_contraction_needs_widened_f16_loads():
     assert L.wgsl_template_key(src).endswith(";wb=1")
     raw = src.replace("f32(data2[", "(data2[")
     assert raw != src and L.wgsl_template_key(raw) == ""
+
+
+def test_rendered_chain_step_renders_the_movement_chain():
+    """Config 5's rendered step (tests/wgsl_lower.py chain_step): every kernel parses in the lowering's
+    form, the movement chain (shrink offsets, the pad's validity select with the reduce identity as fill,
+    the permute's swapped indices) included; the per-row reductions take the wave rendering (their
+    reduced values are elementwise chains, not plain loads), dX the thread one."""
+    ks, _, _ = WL.chain_step(64, 48)
+    plans = {name: L.wgsl_plan(src) for name, src, *_ in ks}
+    for name, src, _, _, _, plan in ks:
+        assert plans[name] == plan, name
+    assert [n for n, p in plans.items() if p == "thread"] == ["dX"]
+    src = dict((n, s) for n, s, *_ in ks)["max"]
+    assert "select(bitcast<f32>(0xff7fffffu)" in src and "(t5 < 49)" in src

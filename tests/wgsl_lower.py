@@ -528,3 +528,218 @@ def mlp3_step(B: int, D0: int, D1: int, D2: int, D3: int):
     dweight("dW1", udW1, D1, D0, udH1, uZ1, 1, False)
     outs = dict(loss=uloss, dW1=udW1, db1=udb1, dW2=udW2, db2=udb2, dW3=udW3, db3=udb3)
     return ks, leaves, outs
+
+
+def chain_step(R: int, Cc: int):
+    """Config 5's step (Y = Shrink(Pad(Permute(X))) with one element of padding on every side, per-row
+    softmax S = e / s with e = Exp2((y - m) / ln2), r = 1 / Sqrt(Mean(S^2) + 1e-6), out = S * r * g,
+    loss = Sum(out), and its backward) as rendered kernels, following the graph the oracle restates
+    (ora_chain_step, oracle/anneal_oracle.c). Every reduce is materialised (m, the tie count, s, Sum(S^2),
+    the loss, dg, and the backward's gR, gRs, gm); the elementwise chains, the per-row scalars r and the
+    rule-by-rule backward factors are recomputed inline by each kernel that reads them; dX is one
+    elementwise kernel. The movement chain is index arithmetic inside every load of Y
+    (schedule/index.go:30-225): the shrink's +1 offsets, the pad's validity Where (bounds 0 < i + 1 < Cc + 1
+    and 0 < j + 1 < R + 1, fill the enclosing reduce's identity: -FLT_MAX under the max, 0 elsewhere), the
+    pad's -1, and the permute's swapped indices into X[R, Cc]; dX runs the inverse chain (the Pad of the
+    adjoint that Shrink's rule gives, the Shrink that Pad's rule gives, the inverse Permute).
+    Returns (kernels, leaves, outputs) like mlp_ce_step."""
+    leaves = dict(X=1, g=2)
+    um, utie, us, usq, uloss, udg, ugR, ugRs, ugm, udX = range(10, 20)
+    ks = []
+    rR, eps = f32_lit(1.0 / R), f32_lit(1e-6)
+    NEG = "bitcast<f32>(0xff7fffffu)"
+
+    def add(name, k, plan):
+        ks.append((name, k.source(), [(u, int(np.prod(sh)), dt, list(sh)) for u, sh, dt in k.bufs], tuple(k.ws),
+                   tuple(k.wc), plan))
+
+    def y(k, i, j, fill):
+        # element (i, j) of Y: shrink offsets, pad validity and -1, permute into X[R, Cc] (data1)
+        a = k.let(f"({i} + 1)", "i32")
+        b = k.let(f"({j} + 1)", "i32")
+        c = k.let(f"(0 < {a})", "bool")
+        c = k.let(f"({c} && {k.let(f'({a} < {Cc + 1})', 'bool')})", "bool")
+        c = k.let(f"({c} && {k.let(f'(0 < {b})', 'bool')})", "bool")
+        c = k.let(f"({c} && {k.let(f'({b} < {R + 1})', 'bool')})", "bool")
+        sj = k.let(f"({b} - 1)", "i32")
+        si = k.let(f"({a} - 1)", "i32")
+        x = k.load(1, k.idx2(sj, Cc, si))
+        return k.let(f"select({fill}, {x}, {c})")
+
+    def row_kernel(out, extra):
+        """A reduce over the row j of Y for each row i (r0): data1 = X, then the per-row inputs `extra`
+        [(uop, name)] as data2.. . Returns (kernel, loop var, {name: data index})."""
+        bufs = [(out, [Cc], F32), (1, [R, Cc], F32)] + [(u, [Cc], F32) for u, _ in extra]
+        k = Kernel(bufs, [Cc])
+        idx = {nm: 2 + n for n, (_, nm) in enumerate(extra)}
+        return k, idx
+
+    def scalars(k, idx, need):
+        """Per-row values the kernel reads (loaded once, before the loop, as the lowering hoists them)."""
+        v = {nm: k.load(idx[nm], "r0") for nm in need if nm in idx}
+        if "rs" in need:
+            v["rs"] = k.let(f"(1.0 / {v['s']})")
+        if "r" in need:
+            q = k.let(f"({v['sq']} * {rR})")
+            v["T"] = k.let(f"sqrt(({q} + {eps}))")
+            v["r"] = k.let(f"(1.0 / {v['T']})")
+        if "gsq" in need:
+            gT = k.let(f"((-{v['gR']} * {v['r']}) * {v['r']})")
+            gu = k.let(f"({gT} * (1.0 / (2.0 * {v['T']})))")
+            v["gsq"] = k.let(f"({gu} * {rR})")
+        if "gs" in need:
+            v["gs"] = k.let(f"((-{v['gRs']} * {v['rs']}) * {v['rs']})")
+        return v
+
+    def elem(k, v, yv, want):
+        """Per-element values of row r0 at the loop's j from y: e, S, A, gS, gzs."""
+        zs = k.let(f"({yv} - {v['m']})")
+        e = k.let(f"exp2(({zs} * {LOG2E}))")
+        out = {"e": e}
+        if "S" in want or "A" in want or "gS" in want or "gzs" in want:
+            out["S"] = k.let(f"({e} * {v['rs']})")
+        if "A" in want:
+            out["A"] = k.let(f"({out['S']} * {v['r']})")
+        if "gS" in want or "gzs" in want:
+            t2 = k.let(f"({v['gsq']} * {out['S']})")
+            out["gS"] = k.let(f"((({v['g']} * {v['r']}) + {t2}) + {t2})")
+        if "gzs" in want:
+            ge = k.let(f"(({out['gS']} * {v['rs']}) + {v['gs']})")
+            gv = k.let(f"(({ge} * {e}) * {LN2})")
+            out["gzs"] = k.let(f"({gv} * {LOG2E})")
+        return out
+
+    # 1. m = Max over the row (pad fill -FLT_MAX)
+    k, idx = row_kernel(um, [])
+    k.acc("M")
+    r1 = k.loop(R)
+    k.update(y(k, "r0", r1, NEG))
+    k.end()
+    k.store("acc0")
+    add("max", k, "wave")
+
+    # 2. the tie count Sum(Cast(y == m)) (the max rule's mask, tensor/gradient_ruleset.go:307-320)
+    k, idx = row_kernel(utie, [(um, "m")])
+    m = k.load(idx["m"], "r0")
+    k.acc()
+    r1 = k.loop(R)
+    yv = y(k, "r0", r1, "0.0")
+    k.update(k.let(f"select(0.0, 1.0, {k.let(f'({yv} == {m})', 'bool')})"))
+    k.end()
+    k.store("acc0")
+    add("tie", k, "wave")
+
+    # 3. s = Sum(e)
+    k, idx = row_kernel(us, [(um, "m")])
+    v = scalars(k, idx, ["m"])
+    k.acc()
+    r1 = k.loop(R)
+    k.update(elem(k, v, y(k, "r0", r1, "0.0"), [])["e"])
+    k.end()
+    k.store("acc0")
+    add("sumexp", k, "wave")
+
+    # 4. Sum(S^2)
+    k, idx = row_kernel(usq, [(um, "m"), (us, "s")])
+    v = scalars(k, idx, ["m", "s", "rs"])
+    k.acc()
+    r1 = k.loop(R)
+    S = elem(k, v, y(k, "r0", r1, "0.0"), ["S"])["S"]
+    k.update(k.let(f"({S} * {S})"))
+    k.end()
+    k.store("acc0")
+    add("sumsq", k, "wave")
+
+    # 5. loss = Sum over both axes of A * g (row-major)
+    k = Kernel([(uloss, [1], F32), (1, [R, Cc], F32), (um, [Cc], F32), (us, [Cc], F32), (usq, [Cc], F32),
+                (2, [Cc], F32)], [])
+    k.acc()
+    i = k.loop(Cc)
+    v = {"m": k.load(2, i), "s": k.load(3, i), "sq": k.load(4, i), "g": k.load(5, i)}
+    v["rs"] = k.let(f"(1.0 / {v['s']})")
+    q = k.let(f"({v['sq']} * {rR})")
+    v["T"] = k.let(f"sqrt(({q} + {eps}))")
+    v["r"] = k.let(f"(1.0 / {v['T']})")
+    j = k.loop(R)
+    A = elem(k, v, y(k, i, j, "0.0"), ["A"])["A"]
+    k.update(k.let(f"({A} * {v['g']})"))
+    k.end()
+    k.end()
+    k.store("acc0")
+    add("loss", k, "wave")
+
+    # 6. dg = Sum(A) (the Expand rule over the row of out = A * g)
+    k, idx = row_kernel(udg, [(um, "m"), (us, "s"), (usq, "sq")])
+    v = scalars(k, idx, ["m", "s", "sq", "rs", "r"])
+    k.acc()
+    r1 = k.loop(R)
+    k.update(elem(k, v, y(k, "r0", r1, "0.0"), ["A"])["A"])
+    k.end()
+    k.store("acc0")
+    add("dg", k, "wave")
+
+    # 7. gR = Sum(g * S)
+    k, idx = row_kernel(ugR, [(um, "m"), (us, "s"), (2, "g")])
+    v = scalars(k, idx, ["m", "s", "g", "rs"])
+    k.acc()
+    r1 = k.loop(R)
+    S = elem(k, v, y(k, "r0", r1, "0.0"), ["S"])["S"]
+    k.update(k.let(f"({v['g']} * {S})"))
+    k.end()
+    k.store("acc0")
+    add("gR", k, "wave")
+
+    # 8. gRs = Sum(gS * e)
+    k, idx = row_kernel(ugRs, [(um, "m"), (us, "s"), (usq, "sq"), (ugR, "gR"), (2, "g")])
+    v = scalars(k, idx, ["m", "s", "sq", "gR", "g", "rs", "r", "gsq"])
+    k.acc()
+    r1 = k.loop(R)
+    el = elem(k, v, y(k, "r0", r1, "0.0"), ["gS"])
+    k.update(k.let(f"({el['gS']} * {el['e']})"))
+    k.end()
+    k.store("acc0")
+    add("gRs", k, "wave")
+
+    # 9. gm = Sum(-gzs)
+    k, idx = row_kernel(ugm, [(um, "m"), (us, "s"), (usq, "sq"), (ugR, "gR"), (ugRs, "gRs"), (2, "g")])
+    v = scalars(k, idx, ["m", "s", "sq", "gR", "gRs", "g", "rs", "r", "gsq", "gs"])
+    k.acc()
+    r1 = k.loop(R)
+    gz = elem(k, v, y(k, "r0", r1, "0.0"), ["gzs"])["gzs"]
+    k.update(k.let(f"-{gz}"))
+    k.end()
+    k.store("acc0")
+    add("gm", k, "wave")
+
+    # 10. dX[j, i] = gzs + Where(y == m, gm * (1 / tie), 0) through the inverse chain
+    bufs = [(udX, [R, Cc], F32), (1, [R, Cc], F32)] + [(u, [Cc], F32) for u in (um, us, usq, ugR, ugRs, ugm, utie, 2)]
+    k = Kernel(bufs, [R, Cc])
+    # output (j, i) = (r0, r1); the inverse Permute gives adjoint index (i, j), the Shrink of the padded
+    # adjoint adds 1 to each, the Pad's validity guards them (fill 0) and its -1 returns to (i, j)
+    a = k.let("(r1 + 1)", "i32")
+    b = k.let("(r0 + 1)", "i32")
+    c = k.let(f"(0 < {a})", "bool")
+    c = k.let(f"({c} && {k.let(f'({a} < {Cc + 1})', 'bool')})", "bool")
+    c = k.let(f"({c} && {k.let(f'(0 < {b})', 'bool')})", "bool")
+    c = k.let(f"({c} && {k.let(f'({b} < {R + 1})', 'bool')})", "bool")
+    i = k.let(f"({a} - 1)", "i32")
+    j = k.let(f"({b} - 1)", "i32")
+    names = ["m", "s", "sq", "gR", "gRs", "gm", "tie", "g"]
+    v = {nm: k.load(2 + n, i) for n, nm in enumerate(names)}
+    v["rs"] = k.let(f"(1.0 / {v['s']})")
+    q = k.let(f"({v['sq']} * {rR})")
+    v["T"] = k.let(f"sqrt(({q} + {eps}))")
+    v["r"] = k.let(f"(1.0 / {v['T']})")
+    gT = k.let(f"((-{v['gR']} * {v['r']}) * {v['r']})")
+    gu = k.let(f"({gT} * (1.0 / (2.0 * {v['T']})))")
+    v["gsq"] = k.let(f"({gu} * {rR})")
+    v["gs"] = k.let(f"((-{v['gRs']} * {v['rs']}) * {v['rs']})")
+    yv = y(k, i, j, "0.0")
+    gz = elem(k, v, yv, ["gzs"])["gzs"]
+    share = k.let(f"({v['gm']} * (1.0 / {v['tie']}))")
+    tie = k.let(f"({yv} == {v['m']})", "bool")
+    dy = k.let(f"({gz} + select(0.0, {share}, {tie}))")
+    k.store(k.let(f"select(0.0, {dy}, {c})"))
+    add("dX", k, "thread")
+    outs = dict(loss=uloss, dX=udX, dg=udg)
+    return ks, leaves, outs
