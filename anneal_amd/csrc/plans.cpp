@@ -851,12 +851,9 @@ struct Mlp3Trainer : ah_trainer {
                 LAUNCH(q == 0 ? "dW3+dH1" : "dW1+dW2",
                        gemm16_pair_try_launch(ga, kPairSplit, &gb, pair_v[q], pair_count, pair_part, pair_part_floats,
                                               s, &perr) ? perr : hipErrorInvalidValue);
-            } else if (q == 0) {
+            } else {   // unpaired: dW3, dH1, then dW1 (reading dH1's output while the Infinity Cache holds it), dW2
                 LAUNCH(names[a], gemm_run(dev, gemm(a, sg), s));
                 LAUNCH(names[b], gemm_run(dev, gemm(b, sg), s));
-            } else {   // the order of the unpaired step: dW2, then dW1
-                LAUNCH(names[b], gemm_run(dev, gemm(b, sg), s));
-                LAUNCH(names[a], gemm_run(dev, gemm(a, sg), s));
             }
         }
         TailArgs ta{};
