@@ -394,10 +394,8 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
     constexpr int kResRegs = NS < kResMaxRegs ? NS : kResMaxRegs, kResLds = NS - kResRegs;
     static_assert(kResLds <= kResMaxLds, "the strip does not fit on chip");
     __shared__ __attribute__((aligned(1024))) floatx4 held[kResLds > 0 ? kResLds : 1][kResThreads];
-    __shared__ float red[kResThreads / 64][kResCols];
-    __shared__ __attribute__((aligned(16))) float colv[kResCols];
-    __shared__ float colsum3[3][kResCols];                        // sum e, sum e^2, ties per column
-    __shared__ __attribute__((aligned(16))) float coef[6][kResCols];   // rs, g*r, gsq, gs, share, loss term
+    __shared__ float red[4][kResThreads / 64][kResCols];               // per wave: max, sum e, sum e^2, ties
+    __shared__ __attribute__((aligned(16))) float coef[6][kResCols];   // dX factors A, B, column max, -, tie share, loss term
     __shared__ int ticket;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nstrips = Cc / kResCols;
@@ -426,7 +424,7 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
     // column sums and keeps the exact running max with the count of elements equal to it. Once every
     // slot has landed, the column max m is the max of the running maxima, the tie count the sum of the
     // counts of the threads whose running max is m, and each thread's sums are rescaled by
-    // 2^((mt - m)/ln2) before the column sums. x stays in place; the dX pass recomputes e against m. An
+    // 2^((mt - m_w)/ln2) to its wave's max m_w, each wave's by 2^((m_w - m)/ln2) to the column max. x stays in place; the dX pass recomputes e against m. An
     // element more than 2^60 above the thread's reference (where e^2 could overflow) first moves the
     // reference to itself, rescaling the thread's sums (no such element occurs unless the strip's
     // values grow by a factor e^41 along the column).
@@ -485,53 +483,43 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         const floatx4 x = *(volatile floatx4 *)&held[j][tid];
         stat(x);
     }
-    // Cross-wave step of a column reduction: lanes 0-3 of each wave post their 4 columns, 16 threads
-    // fold the 8 waves in order, and every thread reads its 4 columns back as one vector (the per-thread
-    // live set stays at 4 values; the held strip fills most registers).
-    auto across_waves = [&](float (&x)[4], bool is_max, float *keep) {
-        if (lane < 4)
-#pragma unroll
-            for (int u = 0; u < 4; u++) red[wave][4 * lane + u] = x[u];
-        __syncthreads();
-        if (tid < kResCols) {
-            float a = red[0][tid];
-            for (int w = 1; w < kResThreads / 64; w++) a = is_max ? fmaxf(a, red[w][tid]) : a + red[w][tid];
-            colv[tid] = a;
-            if (keep) keep[tid] = a;
-        }
-        __syncthreads();
-        const floatx4 r4 = *(const floatx4 *)&colv[4 * q];
-#pragma unroll
-        for (int u = 0; u < 4; u++) x[u] = r4[u];
-        __syncthreads();   // colv and red are reused
-    };
+    // 4. Column statistics in one cross-wave round: each wave folds its 16 lanes of a column (max,
+    // then the sums rescaled to the wave's max, the tie count at that max) and lanes 0-3 post the
+    // wave's (max, sum e, sum e^2, ties) per column; thread c < 16 folds the 8 waves of column c in
+    // order, rescaling each wave's sums to the column max, and evaluates the column's scalars
+    // (chain_finalize's rules); every thread then reads its 4 columns' scalars back.
     float m[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) m[u] = res_tree_max(mr[u]);
-    across_waves(m, true, nullptr);
-    float mc[4], tc[4];
-#pragma unroll
     for (int u = 0; u < 4; u++) {
-        mc[u] = m[u] * AH_INV_LN2;
-        tc[u] = res_tree_sum(mr[u] == m[u] ? cnt[u] : 0.0f);
-        const float f = fast_exp2(mct[u] - mc[u]);   // 2^((mt - m)/ln2) <= 1
-        se[u] *= f;
-        sq[u] *= f * f;
+        m[u] = res_tree_max(mr[u]);                    // the wave's max of the column
+        const float f = fast_exp2(mct[u] - m[u] * AH_INV_LN2);   // 2^((mt - m_w)/ln2) <= 1
+        se[u] = res_tree_sum(se[u] * f);
+        sq[u] = res_tree_sum(sq[u] * (f * f));
+        cnt[u] = res_tree_sum(mr[u] == m[u] ? cnt[u] : 0.0f);
     }
+    if (lane < 4)
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        se[u] = res_tree_sum(se[u]);
-        sq[u] = res_tree_sum(sq[u]);
-    }
-    across_waves(se, false, colsum3[0]);
-    across_waves(sq, false, colsum3[1]);
-    across_waves(tc, false, colsum3[2]);
-    // 4. the per-column scalars (chain_finalize's rules): thread c < 16 evaluates column c, and every
-    // thread reads its 4 columns' scalars back (one column's temporaries per thread, not four)
+        for (int u = 0; u < 4; u++) {
+            red[0][wave][4 * lane + u] = m[u];
+            red[1][wave][4 * lane + u] = se[u];
+            red[2][wave][4 * lane + u] = sq[u];
+            red[3][wave][4 * lane + u] = cnt[u];
+        }
+    __syncthreads();
     if (tid < kResCols) {
+        float mm = red[0][0][tid];
+        for (int w = 1; w < kResThreads / 64; w++) mm = fmaxf(mm, red[0][w][tid]);
+        const float mmc = mm * AH_INV_LN2;
+        float s_ = 0.0f, q_ = 0.0f, t_ = 0.0f;
+        for (int w = 0; w < kResThreads / 64; w++) {
+            const float mw = red[0][w][tid];
+            const float f = fast_exp2(__builtin_fmaf(mw, AH_INV_LN2, -mmc));
+            s_ += red[1][w][tid] * f;
+            q_ += red[2][w][tid] * (f * f);
+            t_ += mw == mm ? red[3][w][tid] : 0.0f;
+        }
         const int c = strip * kResCols + tid;
         const float eps = 1e-6f, rR = 1.0f / (float)R;
-        const float s_ = colsum3[0][tid], q_ = colsum3[1][tid], t_ = colsum3[2][tid];
         const float r_s = 1.0f / s_;
         const float sumS = s_ * r_s;
         const float sqq = q_ * (r_s * r_s);
@@ -553,15 +541,22 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
         coef[1][tid] = 2.0f * gsq_ * (r_s * r_s);
         coef[4][tid] = gm * (1.0f / t_);
         coef[5][tid] = gi * (r * sumS);
+        coef[2][tid] = mm;
         dg[c] = r * sumS;
     }
     __syncthreads();
-    float ca[4], cb[4], sh[4];
+    float ca[4], cb[4], sh[4], mc[4];
     {
         const floatx4 a = *(const floatx4 *)&coef[0][4 * q], b = *(const floatx4 *)&coef[1][4 * q],
-                      e = *(const floatx4 *)&coef[4][4 * q];
+                      mx = *(const floatx4 *)&coef[2][4 * q], e = *(const floatx4 *)&coef[4][4 * q];
 #pragma unroll
-        for (int u = 0; u < 4; u++) { ca[u] = a[u]; cb[u] = b[u]; sh[u] = e[u]; }
+        for (int u = 0; u < 4; u++) {
+            ca[u] = a[u];
+            cb[u] = b[u];
+            m[u] = mx[u];
+            mc[u] = mx[u] * AH_INV_LN2;
+            sh[u] = e[u];
+        }
     }
     // 5. dX from the held strip: the register slots, then the LDS slots two at a time. The LDS slots are
     // read through volatile loads in every pass: otherwise the compiler may keep one pass's reads live in
