@@ -745,10 +745,12 @@ struct Mlp3Trainer : ah_trainer {
         if (!gemm16_variant_params(v, &p) || p.kg > 1) return 1;
         return std::max(1, p.bm / p.wvm / 32);
     }
-    // Paired launches: for each pair, whole steps are timed with the two contractions launched apart
-    // and paired with each pair variant (interleaved, three rounds, the best mean of 8 steps each), on
-    // hash-filled parameters and data; the fastest is kept. The choice is cached under the pair's key
-    // beside the variant choices.
+    // Paired launches: launched apart unless AH_PAIR_VARIANT fixes a pair variant, a tune cache holds a
+    // choice, or AH_PAIR_TUNE=1 asks for timing. Timing runs whole steps with the two contractions
+    // launched apart and paired with each pair variant (interleaved, three rounds, the best mean of 8
+    // steps each), on hash-filled parameters and data, keeps the fastest and caches the choice under the
+    // pair's key beside the variant choices. (Untimed by default: the paired launches have measured
+    // slower in every alternating comparison, yet a noisy timing round could still pick them.)
     std::string pair_key(int q) const {
         const GemmDesc a = gemm(q == 0 ? 4 : 7, false), b = gemm(q == 0 ? 5 : 6, false);
         return "pair" + std::to_string(kPairSplit) + "/" + tune_key(a) + "/" + tune_key(b);
@@ -775,7 +777,8 @@ struct Mlp3Trainer : ah_trainer {
             todo[q] = pair_admitted(q) && it == dev->gemm_variant.end();
             pair_v[q] = pair_admitted(q) && it != dev->gemm_variant.end() ? it->second : 0;
         }
-        if (!todo[0] && !todo[1]) return AH_OK;
+        const char *tune = getenv("AH_PAIR_TUNE");
+        if ((!todo[0] && !todo[1]) || !tune || strcmp(tune, "1") != 0) return AH_OK;
         hipStream_t s = dev->stream;
         const float x_amp = 1.7320508f;
         AH_HIP(fill_hash(nullptr, X, (long)B * D0, 1u, x_amp, s));

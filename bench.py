@@ -434,21 +434,25 @@ def main():
     kernels = step_kernels(t, batch, kernels)
     _, kinfo = kernel_table(t, batch, kernels)
     dom = int(np.argmax([k["avg_us"] for k in kinfo]))
-    # Timed region: K steps. The dominant kernel's duration is measured as in kernel_table, over the
-    # timed steps themselves: hipEvents before launch dom-1 and after launch dom in the first half, before
-    # launch dom-1 and after launch dom-1 in the second; the difference of the two averages is the launch.
-    # Reading the first half's events synchronizes the stream once, inside the timed region.
+    # Timed region: K steps. The dominant kernel's duration is measured as in kernel_table, on steps of
+    # the timed region itself: hipEvents before launch dom-1 and after launch dom on the first P steps,
+    # before launch dom-1 and after launch dom-1 on the last P; the difference of the two averages is the
+    # launch. P = K/20 (at least 1): each probe event costs the stream a few microseconds, which would be
+    # a sixth of config 5's step if every step carried them. Reading the first probes' events
+    # synchronizes the stream once, inside the timed region. Steps are enqueued by one library call per
+    # run of steps (ah_trainer_steps), so a short step is not held up by a Python call per step.
     j = max(dom - 1, 0)
-    half = max(args.steps // 2, 1)
+    P = max(1, args.steps // 20)
+    rest = max(args.steps - 2 * P, 0)
     t.probe_span(j, dom)
     dev.sync()
     t0 = time.perf_counter()
-    for _ in range(half):
-        t.step(batch)
+    t.steps(batch, P)
     a_ms, a_n = t.probe_read()
+    t.probe(-1)
+    t.steps(batch, rest)
     t.probe_span(j, dom - 1)
-    for _ in range(args.steps - half):
-        t.step(batch)
+    t.steps(batch, args.steps - P - rest)
     dev.sync()
     elapsed = time.perf_counter() - t0
     b_ms, b_n = t.probe_read()
