@@ -565,6 +565,9 @@ struct Mlp3Trainer : ah_trainer {
     }
     // The step's eight contractions, in launch order (fc1 fc2 fc3_mse dH2 dW3 dH1 dW2 dW1).
     static constexpr int kGemms = 8;
+    // Launch position of contraction i in the unpaired step: dW1 (7) goes before dW2 (6), reading dH1's
+    // output while the Infinity Cache still holds it.
+    static constexpr int kLaunchPos[kGemms] = {0, 1, 2, 3, 4, 5, 7, 6};
     GemmDesc gemm(int i, bool sg) const {
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
@@ -692,6 +695,8 @@ struct Mlp3Trainer : ah_trainer {
         constexpr int kSteps = 4;
         int rc = AH_OK;
         const int saved = probe_index, saved_last = probe_last;
+        const int saved_pairs[2] = {pair_v[0], pair_v[1]};
+        pair_v[0] = pair_v[1] = 0;   // launch positions are those of the unpaired step
         auto steps = [&](int n) {
             for (int k = 0; k < n; k++) {
                 launch_idx = 0;
@@ -711,7 +716,7 @@ struct Mlp3Trainer : ah_trainer {
                 for (int v = 1; v <= kGemm16Variants && rc == AH_OK; v++) {
                     dev->gemm_variant[keys[i]] = v;
                     if ((rc = steps(1))) break;   // the variant's first launch is not timed
-                    probe_index = probe_last = i;
+                    probe_index = probe_last = kLaunchPos[i];
                     n_probe = 0;
                     rc = steps(kSteps);
                     probe_index = saved;
@@ -728,6 +733,8 @@ struct Mlp3Trainer : ah_trainer {
         }
         probe_index = saved;
         probe_last = saved_last;
+        pair_v[0] = saved_pairs[0];
+        pair_v[1] = saved_pairs[1];
         n_probe = 0;
         launch_idx = 0;
         return rc;
