@@ -852,7 +852,9 @@ struct Mlp3Trainer : ah_trainer {
         for (int i = 0; i < 4; i++) LAUNCH(names[i], gemm_run(dev, gemm(i, sg), s));
         // dW3 beside dH1, then dW1 beside dW2 (each pair reads only finished inputs and writes
         // disjoint outputs)
-        static const int pairs[2][2] = {{4, 5}, {7, 6}};
+        static constexpr int pairs[2][2] = {{4, 5}, {7, 6}};
+        static_assert(kLaunchPos[4] == 4 && kLaunchPos[5] == 5 && kLaunchPos[7] == 6 && kLaunchPos[6] == 7,
+                      "the unpaired launch order is the one the variant refinement probes");
         for (int q = 0; q < 2; q++) {
             const int a = pairs[q][0], b = pairs[q][1];
             if (pair_v[q]) {
