@@ -424,10 +424,11 @@ __global__ __launch_bounds__(kResThreads) void chain_resident_kernel(const float
     // column sums and keeps the exact running max with the count of elements equal to it. Once every
     // slot has landed, the column max m is the max of the running maxima, the tie count the sum of the
     // counts of the threads whose running max is m, and each thread's sums are rescaled by
-    // 2^((mt - m_w)/ln2) to its wave's max m_w, each wave's by 2^((m_w - m)/ln2) to the column max. x stays in place; the dX pass recomputes e against m. An
-    // element more than 2^60 above the thread's reference (where e^2 could overflow) first moves the
-    // reference to itself, rescaling the thread's sums (no such element occurs unless the strip's
-    // values grow by a factor e^41 along the column).
+    // 2^((mt - m_w)/ln2) to its wave's max m_w, each wave's by 2^((m_w - m)/ln2) to the column max.
+    // x stays in place; the dX pass recomputes e against m. An element more than 2^60 above the
+    // thread's reference (where e^2 could overflow) first moves the reference to itself, rescaling the
+    // thread's sums (no such element occurs unless the strip's values grow by a factor e^41 along the
+    // column).
     constexpr int kProv = 8;
     static_assert(kResRegs >= kProv, "the provisional max takes register slots");
     float mt[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
