@@ -291,6 +291,18 @@ def test_config3_steps_bit_repeatable(dev):
         np.testing.assert_array_equal(runs[0][k], runs[1][k], err_msg=k)
 
 
+def test_config3_launch_order(dev, monkeypatch):
+    """The config-3 step launches its contractions apart unless pair timing is asked for, with dW1
+    before dW2 (dW1 reads dH1's output while the Infinity Cache still holds it); the variant refinement
+    at creation probes each contraction at this position."""
+    monkeypatch.delenv("AH_PAIR_VARIANT", raising=False)
+    monkeypatch.delenv("AH_PAIR_TUNE", raising=False)
+    B, D0, D1, D2, D3 = 512, 256, 512, 384, 256
+    t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], 1e-3)
+    assert t.kernel_names(B) == ["fc1", "fc2", "fc3_mse", "dH2", "dW3", "dH1", "dW1", "dW2", "tail"]
+    t.close()
+
+
 def _params_bits(t, p, names):
     return {k: t.get(k, p[k].size).view(np.uint32).copy() for k in names}
 
