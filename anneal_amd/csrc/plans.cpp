@@ -463,6 +463,18 @@ struct MlpCeTrainer : ah_trainer {
 // 2/(B*D3) is applied in the f32 weight-update epilogues; this keeps f16 MFMA operands in range
 // (the raw adjoint, ~1e-7 at B*D3 = 2^22, is below f16's normal range).
 
+// The unpaired config-3 step's launch order (contraction indices 0-7: fc1, fc2, fc3, dH2, dW3, dH1, dW2,
+// dW1): the backward runs dH2, dH1, dW1, dW3, dW2, so dH1 reads dH2's output and dW1 dH1's while the
+// Infinity Cache still holds them. kMlp3LaunchPos[i] is contraction i's position.
+constexpr int kMlp3Order[8] = {0, 1, 2, 3, 5, 7, 4, 6};
+constexpr int mlp3_launch_pos(int i) {
+    int p = 0;
+    while (kMlp3Order[p] != i) p++;
+    return p;
+}
+constexpr int kMlp3LaunchPos[8] = {mlp3_launch_pos(0), mlp3_launch_pos(1), mlp3_launch_pos(2), mlp3_launch_pos(3),
+                                   mlp3_launch_pos(4), mlp3_launch_pos(5), mlp3_launch_pos(6), mlp3_launch_pos(7)};
+
 struct Mlp3Trainer : ah_trainer {
     int B, D0, D1, D2, D3;
     half_t *X, *T, *W1h, *W2h, *W3h, *b1h, *b2h, *b3h, *H1, *H2, *Dd, *dZ2, *dZ1;
@@ -565,9 +577,6 @@ struct Mlp3Trainer : ah_trainer {
     }
     // The step's eight contractions, in launch order (fc1 fc2 fc3_mse dH2 dW3 dH1 dW2 dW1).
     static constexpr int kGemms = 8;
-    // Launch position of contraction i in the unpaired step: dW1 (7) goes before dW2 (6), reading dH1's
-    // output while the Infinity Cache still holds it.
-    static constexpr int kLaunchPos[kGemms] = {0, 1, 2, 3, 4, 5, 7, 6};
     GemmDesc gemm(int i, bool sg) const {
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
@@ -716,7 +725,7 @@ struct Mlp3Trainer : ah_trainer {
                 for (int v = 1; v <= kGemm16Variants && rc == AH_OK; v++) {
                     dev->gemm_variant[keys[i]] = v;
                     if ((rc = steps(1))) break;   // the variant's first launch is not timed
-                    probe_index = probe_last = kLaunchPos[i];
+                    probe_index = probe_last = kMlp3LaunchPos[i];
                     n_probe = 0;
                     rc = steps(kSteps);
                     probe_index = saved;
@@ -849,12 +858,13 @@ struct Mlp3Trainer : ah_trainer {
         const float sc = (float)(1.0 / ((double)B * (double)D3));
         const float bs = 2.0f * sc;
         static const char *names[kGemms] = {"fc1", "fc2", "fc3_mse", "dH2", "dW3", "dH1", "dW2", "dW1"};
+        if (!pair_v[0] && !pair_v[1]) {
+            for (int i = 0; i < kGemms; i++) LAUNCH(names[kMlp3Order[i]], gemm_run(dev, gemm(kMlp3Order[i], sg), s));
+        } else {
         for (int i = 0; i < 4; i++) LAUNCH(names[i], gemm_run(dev, gemm(i, sg), s));
         // dW3 beside dH1, then dW1 beside dW2 (each pair reads only finished inputs and writes
         // disjoint outputs)
         static constexpr int pairs[2][2] = {{4, 5}, {7, 6}};
-        static_assert(kLaunchPos[4] == 4 && kLaunchPos[5] == 5 && kLaunchPos[7] == 6 && kLaunchPos[6] == 7,
-                      "the unpaired launch order is the one the variant refinement probes");
         for (int q = 0; q < 2; q++) {
             const int a = pairs[q][0], b = pairs[q][1];
             if (pair_v[q]) {
@@ -863,10 +873,11 @@ struct Mlp3Trainer : ah_trainer {
                 LAUNCH(q == 0 ? "dW3+dH1" : "dW1+dW2",
                        gemm16_pair_try_launch(ga, kPairSplit, &gb, pair_v[q], pair_count, pair_part, pair_part_floats,
                                               s, &perr) ? perr : hipErrorInvalidValue);
-            } else {   // unpaired: dW3, dH1, then dW1 (reading dH1's output while the Infinity Cache holds it), dW2
+            } else {
                 LAUNCH(names[a], gemm_run(dev, gemm(a, sg), s));
                 LAUNCH(names[b], gemm_run(dev, gemm(b, sg), s));
             }
+        }
         }
         TailArgs ta{};
         const int R = rblocks();

@@ -292,14 +292,14 @@ def test_config3_steps_bit_repeatable(dev):
 
 
 def test_config3_launch_order(dev, monkeypatch):
-    """The config-3 step launches its contractions apart unless pair timing is asked for, with dW1
-    before dW2 (dW1 reads dH1's output while the Infinity Cache still holds it); the variant refinement
-    at creation probes each contraction at this position."""
+    """The config-3 step launches its contractions apart unless pair timing is asked for, its backward
+    as dH2, dH1, dW1, dW3, dW2 (dH1 reads dH2's output and dW1 dH1's while the Infinity Cache still
+    holds them); the variant refinement at creation probes each contraction at this position."""
     monkeypatch.delenv("AH_PAIR_VARIANT", raising=False)
     monkeypatch.delenv("AH_PAIR_TUNE", raising=False)
     B, D0, D1, D2, D3 = 512, 256, 512, 384, 256
     t = Trainer(dev, L.TRAIN_MLP3_F16, [B, D0, D1, D2, D3], 1e-3)
-    assert t.kernel_names(B) == ["fc1", "fc2", "fc3_mse", "dH2", "dW3", "dH1", "dW1", "dW2", "tail"]
+    assert t.kernel_names(B) == ["fc1", "fc2", "fc3_mse", "dH2", "dH1", "dW1", "dW3", "dW2", "tail"]
     t.close()
 
 
