@@ -34,7 +34,7 @@ PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
 # the reference's own WebGPU path needs Go and a software Vulkan adapter, neither of which is on the box.
 CPU_LABEL = "CPU restatement \u2014 not the reference binary"
 
-TRAFFIC_BYTES = {(3, "dW2"): 270.7e6 + 102.8e6, (5, "chain_resident"): 135.1e6 + 136.0e6,
+TRAFFIC_BYTES = {(3, "dW2"): 270.7e6 + 102.8e6, (5, "chain_resident"): 135.2e6 + 136.0e6,
                  (5, "chain_grad"): 134.4e6 + 134.4e6,
                  (5, "chain_stats"): 134.3e6 + 4.2e6}
 
