@@ -439,10 +439,10 @@ struct MlpCeTrainer : ah_trainer {
         LAUNCH("dH1", gemm_run(dev, g3, s));
         GemmDesc g4 = gdesc(GEMM_F32, EPI_SGD, 1, 1, C, H, B, dZ2, C, H1, H, nullptr, H);
         g4.W32 = W2; g4.lr = lr; g4.gout = sg ? gW2 : nullptr;
-        LAUNCH("dW2", gemm_run(dev, g4, s));
         GemmDesc g5 = gdesc(GEMM_F32, EPI_SGD, 1, 1, H, D, B, dZ1, H, x, D, nullptr, D);
         g5.W32 = W1; g5.lr = lr; g5.gout = sg ? gW1 : nullptr;
         LAUNCH("dW1", gemm_run(dev, g5, s));
+        LAUNCH("dW2", gemm_run(dev, g4, s));
         TailArgs ta{};
         ta.seg[0] = {b2, nullptr, db2, sg ? gb2 : nullptr, C, 1.0f};
         if (dbpart) {   // the bias gradient as softmax_ce_cols' partial rows, rewritten every step

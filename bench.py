@@ -155,7 +155,7 @@ def mlp_ce_kernels(B, D, H, C):
     # partial rows, which the tail sums; a wider C takes a separate column-sum launch (db2)
     parts = min(256, max(1, (B + 15) // 16)) if C <= 1024 else 0
     return [("fc1", *f(B, H, D)), ("fc2", *f(B, C, H)), ("softmax_ce", "bytes", 8.0 * B * C + 8.0 * B + 4.0 * parts * C),
-            ("db2", "bytes", 4.0 * B * C), ("dH1", *f(B, H, C)), ("dW2", *f(C, H, B)), ("dW1", *f(H, D, B)),
+            ("db2", "bytes", 4.0 * B * C), ("dH1", *f(B, H, C)), ("dW1", *f(H, D, B)), ("dW2", *f(C, H, B)),
             ("tail", "bytes", 4.0 * B + 16.0 * (H + C) + 4.0 * parts * C)]
 
 
